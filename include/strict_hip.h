@@ -1,0 +1,187 @@
+/*
+ * libstrict_hip -- C ABI of the MI355X (gfx950) kernel path behind Strict's
+ * `Strict.Compiler.Cuda` surface.
+ *
+ * The reference reaches the GPU through ManagedCuda objects (Kernel.cs,
+ * CSharpToCudaTranspilerTests.cs, Cuda.Tests/BlurPerformanceTests.cs). This
+ * header is the flat replacement a C# host binds with P/Invoke: opaque
+ * handles, plain pointers and sizes, an int status per call (0 = SH_OK) and a
+ * thread-local message from sh_last_error() in place of the exceptions
+ * ManagedCuda throws.
+ *
+ * Conventions
+ *  - Device pointers are the addresses sh_alloc returns (the counterpart of
+ *    CudaDeviceVariable<T>.DevicePointer). Typed ops check that every pointer
+ *    plus its extent lies inside one allocation of the context (or a range
+ *    registered with sh_register_external) before anything is launched.
+ *  - Ops are ordered on the context's stream and return before the GPU is
+ *    done; sh_sync() waits. sh_upload/sh_download/sh_launch are synchronous,
+ *    as the ManagedCuda calls they replace.
+ *  - Zero-sized work is a successful no-op.
+ */
+#ifndef STRICT_HIP_H
+#define STRICT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SH_API __attribute__((visibility("default")))
+
+typedef enum sh_status {
+  SH_OK = 0,
+  SH_ERR_INVALID_ARGUMENT = 1, /* null pointer, bad size, pointer outside its allocation */
+  SH_ERR_NO_DEVICE = 2,        /* no HIP device / device index out of range */
+  SH_ERR_HIP = 3,              /* a HIP runtime call failed (message has the HIP error) */
+  SH_ERR_OUT_OF_MEMORY = 4,
+  SH_ERR_COMPILE = 5,          /* hipRTC compile failed; the program holds the log */
+  SH_ERR_NOT_FOUND = 6,        /* unknown kernel name in a module */
+  SH_ERR_UNSUPPORTED = 7,      /* valid request this build does not implement */
+} sh_status;
+
+typedef struct sh_ctx sh_ctx;
+typedef struct sh_program sh_program;
+typedef struct sh_module sh_module;
+typedef struct sh_function sh_function;
+
+typedef struct sh_device_info_t {
+  int device;
+  int compute_units;
+  int wavefront_size;
+  int clock_khz;
+  int memory_clock_khz;
+  int memory_bus_width_bits;
+  size_t total_memory_bytes;
+  size_t lds_bytes_per_block;
+  char name[256];
+  char arch[64]; /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+} sh_device_info_t;
+
+/* ---- errors and library ------------------------------------------------- */
+
+/* Message of the last failing call on this thread ("" if none). Replaces the
+ * exception text of CudaException / NVRTCException. */
+SH_API const char *sh_last_error(void);
+SH_API int sh_version(void); /* major * 10000 + minor * 100 + patch */
+SH_API int sh_device_count(int *count);
+
+/* ---- context: replaces `new CudaContext(0)` (Kernel.cs:9) and
+ *      Kernel.Dispose (Kernel.cs:13-17) -------------------------------------- */
+
+SH_API int sh_create(int device, sh_ctx **ctx);
+SH_API int sh_destroy(sh_ctx *ctx); /* frees every allocation and module of ctx */
+SH_API int sh_device_info(sh_ctx *ctx, sh_device_info_t *info);
+SH_API int sh_sync(sh_ctx *ctx);
+/* Raw hipStream_t the context orders its work on (for interop). */
+SH_API int sh_stream(sh_ctx *ctx, void **stream);
+
+/* ---- buffers: replace CudaDeviceVariable<T> and its implicit T[] <-> device
+ *      conversions (CSharpToCudaTranspilerTests.cs:64, :75-76;
+ *      Cuda.Tests/BlurPerformanceTests.cs:151-153, :178) ------------------- */
+
+SH_API int sh_alloc(sh_ctx *ctx, size_t bytes, void **device_ptr);
+SH_API int sh_free(sh_ctx *ctx, void *device_ptr);
+SH_API int sh_upload(sh_ctx *ctx, void *device_dst, const void *host_src, size_t bytes);
+SH_API int sh_download(sh_ctx *ctx, void *host_dst, const void *device_src, size_t bytes);
+SH_API int sh_copy(sh_ctx *ctx, void *device_dst, const void *device_src, size_t bytes);
+SH_API int sh_memset(sh_ctx *ctx, void *device_ptr, int byte_value, size_t bytes);
+/* Lets typed ops accept device memory the context did not allocate. */
+SH_API int sh_register_external(sh_ctx *ctx, void *device_ptr, size_t bytes);
+SH_API int sh_unregister_external(sh_ctx *ctx, void *device_ptr);
+
+/* ---- timing on the context stream (HIP events) ---------------------------- */
+
+SH_API int sh_timer_start(sh_ctx *ctx);
+SH_API int sh_timer_stop(sh_ctx *ctx, float *elapsed_ms); /* waits for the stop event */
+
+/* Free-standing events for per-launch timing (CudaEvent counterpart). */
+typedef struct sh_event sh_event;
+SH_API int sh_event_create(sh_ctx *ctx, sh_event **event);
+SH_API int sh_event_record(sh_event *event); /* on the context stream */
+/* ms between two recorded events of one context; waits for `stop`. */
+SH_API int sh_event_elapsed(sh_event *start, sh_event *stop, float *elapsed_ms);
+SH_API int sh_event_destroy(sh_event *event);
+
+/* ---- runtime compilation and modules: replace CudaRuntimeCompiler (NVRTC,
+ *      Kernel.cs:29-30, :43), GetPTX / GetLogAsString
+ *      (Cuda.Tests/BlurPerformanceTests.cs:133, :148) and
+ *      CudaContext.LoadKernelPTX (CSharpToCudaTranspilerTests.cs:65) --------- */
+
+/* Compiles HIP C++ `source` with hipRTC for the device's architecture (gfx950
+ * unless an --offload-arch option is given). On SH_ERR_COMPILE *program is
+ * still set so the log can be read; always release it with
+ * sh_program_destroy. */
+SH_API int sh_compile(const char *source, const char *name, const char *const *options,
+                      int num_options, sh_program **program);
+SH_API int sh_program_code(sh_program *program, const void **code, size_t *bytes);
+SH_API const char *sh_program_log(sh_program *program);
+SH_API int sh_program_destroy(sh_program *program);
+
+SH_API int sh_module_load(sh_ctx *ctx, const void *code_object, size_t bytes, sh_module **module);
+SH_API int sh_module_function(sh_module *module, const char *name, sh_function **function);
+SH_API int sh_module_unload(sh_module *module);
+
+/* Replaces CudaKernel.Run (CSharpToCudaTranspilerTests.cs:77, :86): launches
+ * with kernelParams-style `args` (one pointer per argument value), waits for
+ * completion and returns the kernel time in ms (may be NULL). */
+SH_API int sh_launch(sh_function *function, const unsigned grid[3], const unsigned block[3],
+                     unsigned shared_bytes, void **args, float *elapsed_ms);
+
+/* ---- typed ops: elementwise ------------------------------------------------ */
+
+typedef enum sh_binary_op {
+  SH_ADD = 0,      /* InstructionsToCuda.cs:104 "+" */
+  SH_SUBTRACT = 1, /* :105 "-" */
+  SH_MULTIPLY = 2, /* :106 "*" */
+  SH_DIVIDE = 3,   /* :107 "/" */
+} sh_binary_op;
+
+/* output[i] = first[i] OP second[i] for i < count: the kernel
+ * InstructionsToCuda.BuildCudaKernel emits (InstructionsToCuda.cs:58-73),
+ * with a linear index (the generator's `y * blockDim.x + x` aliases rows once
+ * gridDim.x > 1). */
+SH_API int sh_binary_f32(sh_ctx *ctx, int op, const float *first, const float *second,
+                         float *output, size_t count);
+/* output[i] = value: the generated `Process` kernel of InitializeDepths
+ * (InstructionsToCuda.cs:79-96, Output/InitializeDepths.cu:5-11). */
+SH_API int sh_fill_f32(sh_ctx *ctx, float value, float *output, size_t count);
+/* out[i] = a * x[i] + y[i], product and sum rounded separately: the saxpy
+ * Kernel.CompileKernelAndSaveAsPtxFile builds (Kernel.cs:22-28). */
+SH_API int sh_saxpy_f32(sh_ctx *ctx, float a, const float *x, const float *y, float *out,
+                        size_t n);
+/* y[i] = 1 / (1 + exp(-x[i])): SigmoidPerformanceTests.cs:27 over an array
+ * (the reference's GPU leg, RunGpu at :32, is an empty stub). <= 2 ulp. */
+SH_API int sh_sigmoid_f32(sh_ctx *ctx, const float *x, float *y, size_t n);
+
+/* ---- typed ops: image (interleaved 8-bit channels, row-major, no padding) -- */
+
+#define SH_BRIGHTNESS_ALL_CHANNELS 1 /* also adjust the 4th (alpha) byte */
+
+typedef enum sh_blur_mode {
+  /* clamp-to-edge taps, (sum + 12) / 25 on every channel */
+  SH_BLUR_CONFIG = 0,
+  /* Assembly.Tests/BlurPerformanceTests.cs:85-141: in-bounds taps only,
+   * sum / count truncating (interior count = 25) */
+  SH_BLUR_REFERENCE = 1,
+} sh_blur_mode;
+
+/* p' = clamp(p + delta, 0, 255) on channels 0..2 of each pixel
+ * (Assembly.Tests/BlurPerformanceTests.cs:287-294); channel 3 passes through
+ * unless flags has SH_BRIGHTNESS_ALL_CHANNELS. in == out is allowed.
+ * channels: 1..4 bytes per pixel; delta in [-255, 255]. */
+SH_API int sh_adjust_brightness_u8(sh_ctx *ctx, const uint8_t *in, uint8_t *out, int width,
+                                   int height, int channels, int delta, int flags);
+/* 5x5 box blur of every channel; in and out must not overlap. */
+SH_API int sh_box_blur5_u8(sh_ctx *ctx, const uint8_t *in, uint8_t *out, int width, int height,
+                           int channels, int mode);
+/* Brightness then blur in one pass (same bytes as the two calls in a row). */
+SH_API int sh_brightness_blur5_u8(sh_ctx *ctx, const uint8_t *in, uint8_t *out, int width,
+                                  int height, int channels, int delta, int flags, int mode);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* STRICT_HIP_H */

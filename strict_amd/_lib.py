@@ -1,0 +1,116 @@
+"""ctypes declarations of the libstrict_hip C ABI (include/strict_hip.h).
+
+Loading fails loudly when ``libstrict_hip.so`` has not been built: there is no
+CPU fallback anywhere in the package.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libstrict_hip.so"
+
+SH_OK = 0
+SH_ERR_INVALID_ARGUMENT = 1
+SH_ERR_NO_DEVICE = 2
+SH_ERR_HIP = 3
+SH_ERR_OUT_OF_MEMORY = 4
+SH_ERR_COMPILE = 5
+SH_ERR_NOT_FOUND = 6
+SH_ERR_UNSUPPORTED = 7
+
+STATUS_NAMES = {
+    SH_OK: "SH_OK",
+    SH_ERR_INVALID_ARGUMENT: "SH_ERR_INVALID_ARGUMENT",
+    SH_ERR_NO_DEVICE: "SH_ERR_NO_DEVICE",
+    SH_ERR_HIP: "SH_ERR_HIP",
+    SH_ERR_OUT_OF_MEMORY: "SH_ERR_OUT_OF_MEMORY",
+    SH_ERR_COMPILE: "SH_ERR_COMPILE",
+    SH_ERR_NOT_FOUND: "SH_ERR_NOT_FOUND",
+    SH_ERR_UNSUPPORTED: "SH_ERR_UNSUPPORTED",
+}
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [
+        ("device", ctypes.c_int),
+        ("compute_units", ctypes.c_int),
+        ("wavefront_size", ctypes.c_int),
+        ("clock_khz", ctypes.c_int),
+        ("memory_clock_khz", ctypes.c_int),
+        ("memory_bus_width_bits", ctypes.c_int),
+        ("total_memory_bytes", ctypes.c_size_t),
+        ("lds_bytes_per_block", ctypes.c_size_t),
+        ("name", ctypes.c_char * 256),
+        ("arch", ctypes.c_char * 64),
+    ]
+
+
+_P = ctypes.c_void_p
+_PP = ctypes.POINTER(ctypes.c_void_p)
+_I = ctypes.c_int
+_SZ = ctypes.c_size_t
+_F = ctypes.c_float
+_U = ctypes.c_uint
+
+# name -> (restype, argtypes). Every entry point include/strict_hip.h declares.
+SIGNATURES = {
+    "sh_last_error": (ctypes.c_char_p, []),
+    "sh_version": (_I, []),
+    "sh_device_count": (_I, [ctypes.POINTER(_I)]),
+    "sh_create": (_I, [_I, _PP]),
+    "sh_destroy": (_I, [_P]),
+    "sh_device_info": (_I, [_P, ctypes.POINTER(DeviceInfo)]),
+    "sh_sync": (_I, [_P]),
+    "sh_stream": (_I, [_P, _PP]),
+    "sh_alloc": (_I, [_P, _SZ, _PP]),
+    "sh_free": (_I, [_P, _P]),
+    "sh_upload": (_I, [_P, _P, _P, _SZ]),
+    "sh_download": (_I, [_P, _P, _P, _SZ]),
+    "sh_copy": (_I, [_P, _P, _P, _SZ]),
+    "sh_memset": (_I, [_P, _P, _I, _SZ]),
+    "sh_register_external": (_I, [_P, _P, _SZ]),
+    "sh_unregister_external": (_I, [_P, _P]),
+    "sh_timer_start": (_I, [_P]),
+    "sh_timer_stop": (_I, [_P, ctypes.POINTER(_F)]),
+    "sh_event_create": (_I, [_P, _PP]),
+    "sh_event_record": (_I, [_P]),
+    "sh_event_elapsed": (_I, [_P, _P, ctypes.POINTER(_F)]),
+    "sh_event_destroy": (_I, [_P]),
+    "sh_compile": (_I, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p), _I,
+                        _PP]),
+    "sh_program_code": (_I, [_P, _PP, ctypes.POINTER(_SZ)]),
+    "sh_program_log": (ctypes.c_char_p, [_P]),
+    "sh_program_destroy": (_I, [_P]),
+    "sh_module_load": (_I, [_P, _P, _SZ, _PP]),
+    "sh_module_function": (_I, [_P, ctypes.c_char_p, _PP]),
+    "sh_module_unload": (_I, [_P]),
+    "sh_launch": (_I, [_P, ctypes.POINTER(_U), ctypes.POINTER(_U), _U, _PP,
+                       ctypes.POINTER(_F)]),
+    "sh_binary_f32": (_I, [_P, _I, _P, _P, _P, _SZ]),
+    "sh_fill_f32": (_I, [_P, _F, _P, _SZ]),
+    "sh_saxpy_f32": (_I, [_P, _F, _P, _P, _P, _SZ]),
+    "sh_sigmoid_f32": (_I, [_P, _P, _P, _SZ]),
+    "sh_adjust_brightness_u8": (_I, [_P, _P, _P, _I, _I, _I, _I, _I]),
+    "sh_box_blur5_u8": (_I, [_P, _P, _P, _I, _I, _I, _I]),
+    "sh_brightness_blur5_u8": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I]),
+}
+
+_lib = None
+
+
+def load():
+    """Load libstrict_hip.so and declare every C-ABI entry point."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise ImportError(
+                f"{LIB_PATH} is not built; run `make -C strict_amd/csrc` or "
+                "__graft_entry__.build() (there is no CPU fallback)")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
