@@ -86,6 +86,8 @@ SH_API int sh_alloc(sh_ctx *ctx, size_t bytes, void **device_ptr);
 SH_API int sh_free(sh_ctx *ctx, void *device_ptr);
 SH_API int sh_upload(sh_ctx *ctx, void *device_dst, const void *host_src, size_t bytes);
 SH_API int sh_download(sh_ctx *ctx, void *host_dst, const void *device_src, size_t bytes);
+/* Stream-ordered device-to-device copy by a plain 16-byte-vector kernel;
+ * the ranges must not overlap (dst == src is a no-op). */
 SH_API int sh_copy(sh_ctx *ctx, void *device_dst, const void *device_src, size_t bytes);
 SH_API int sh_memset(sh_ctx *ctx, void *device_ptr, int byte_value, size_t bytes);
 /* Lets typed ops accept device memory the context did not allocate. */

@@ -38,6 +38,7 @@ hipError_t launch_fill_f32(hipStream_t s, float value, float *out, size_t n);
 hipError_t launch_saxpy_f32(hipStream_t s, float a, const float *x, const float *y, float *out,
                             size_t n);
 hipError_t launch_sigmoid_f32(hipStream_t s, const float *x, float *y, size_t n);
+hipError_t launch_copy_bytes(hipStream_t s, void *dst, const void *src, size_t bytes);
 
 hipError_t launch_brightness_u8(hipStream_t s, const uint8_t *in, uint8_t *out, size_t bytes,
                                 int channels, int delta, int all_channels);

@@ -1,6 +1,7 @@
 // Elementwise fp32 kernels: the generated binary ops and `Process` fill
 // (InstructionsToCuda.cs:58-96), saxpy (Kernel.cs:22-28) and sigmoid
-// (SigmoidPerformanceTests.cs:27).
+// (SigmoidPerformanceTests.cs:27), plus the device-to-device byte copy behind
+// sh_copy (also the HBM calibration kernel of the benchmark).
 //
 // All are HBM-bound streams. Layout for gfx950: 256-thread blocks (4 waves),
 // each thread moves kUnroll 16-byte vectors (f32x4) whose addresses are strided by the
@@ -139,6 +140,35 @@ __global__ __launch_bounds__(kBlock) void fill_scalar_kernel(float value, float 
   if (i < n) out[i] = value;
 }
 
+__global__ __launch_bounds__(kBlock) void copy_vec_kernel(const u32x4 *__restrict__ src,
+                                                           u32x4 *__restrict__ dst, size_t n16,
+                                                           const uint8_t *src_b, uint8_t *dst_b,
+                                                           size_t bytes) {
+  const size_t base = (size_t)blockIdx.x * kPerBlock + threadIdx.x;
+  u32x4 v[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; u++) {
+    size_t i = base + (size_t)u * kBlock;
+    if (i < n16) v[u] = __builtin_nontemporal_load(src + i);
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; u++) {
+    size_t i = base + (size_t)u * kBlock;
+    if (i < n16) __builtin_nontemporal_store(v[u], dst + i);
+  }
+  if (blockIdx.x == 0 && threadIdx.x < (bytes & 15)) {
+    size_t i = n16 * 16 + threadIdx.x;
+    dst_b[i] = src_b[i];
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void copy_byte_kernel(const uint8_t *src, uint8_t *dst,
+                                                            size_t bytes) {
+  for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < bytes;
+       i += (size_t)gridDim.x * kBlock)
+    dst[i] = src[i];
+}
+
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 unsigned vector_grid(size_t n) {
@@ -185,6 +215,21 @@ hipError_t launch_fill_f32(hipStream_t s, float value, float *out, size_t n) {
 hipError_t launch_saxpy_f32(hipStream_t s, float a, const float *x, const float *y, float *out,
                             size_t n) {
   return run_binary(s, x, y, out, n, SaxpyOp{a});
+}
+
+hipError_t launch_copy_bytes(hipStream_t s, void *dst, const void *src, size_t bytes) {
+  const uint8_t *sb = static_cast<const uint8_t *>(src);
+  uint8_t *db = static_cast<uint8_t *>(dst);
+  if (aligned16(src) && aligned16(dst)) {
+    const size_t n16 = bytes / 16;
+    size_t g = (n16 + kPerBlock - 1) / kPerBlock;
+    copy_vec_kernel<<<(unsigned)(g == 0 ? 1 : g), kBlock, 0, s>>>(
+        reinterpret_cast<const u32x4 *>(src), reinterpret_cast<u32x4 *>(dst), n16, sb, db, bytes);
+  } else {
+    size_t g = (bytes + kBlock - 1) / kBlock;
+    copy_byte_kernel<<<(unsigned)(g > 65536 ? 65536 : g), kBlock, 0, s>>>(sb, db, bytes);
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_sigmoid_f32(hipStream_t s, const float *x, float *y, size_t n) {

@@ -2,27 +2,19 @@
 // (Assembly.Tests/BlurPerformanceTests.cs:287-294) and the 5x5 box blur in
 // both semantics (config: clamp-to-edge, (sum + 12) / 25; reference:
 // BlurInteriorPixel / BlurEdgePixel at :85-141, in-bounds taps, sum / count),
-// plus brightness fused into the blur's tile load.
+// plus brightness fused into the blur's row loads.
 //
-// RGBA fast path (channels == 4, width % 4 == 0, 16-byte aligned buffers):
-//  - a workgroup of 256 threads owns a 256 x 32 pixel output tile and stages
-//    the (256 + 8) x (32 + 4) input pixels (halo included, coordinates clamped
-//    or zero-padded by mode) in LDS with 16-byte global loads, all issued
-//    before the barrier;
-//  - each thread then produces a 4 x 8 block of output pixels: the four
-//    channels are split into two words of 16-bit lanes (R|B and G|A), the
-//    horizontal 5-sums slide along the row and the vertical 5-sums slide
-//    down the 12 staged rows; a 25-tap sum (<= 6375) fits a 16-bit lane;
-//  - each output row of a thread is one 16-byte store.
-//  - Workgroup ids are remapped so that each XCD (ids round-robin over 8 XCDs)
-//    gets a contiguous band of tiles: the halo rows a tile shares with its
-//    neighbours then hit the same L2.
-// Any other shape takes a direct kernel (one pixel per thread, taps read
-// through the cache), which is exact for every channel count and mode.
+// RGBA fast path (channels == 4, width % 4 == 0, 16-byte aligned buffers): a
+// register-streaming kernel in which each wave walks down a column strip
+// (described above the kernel). Any other shape takes a direct kernel (one
+// pixel per thread, taps read through the cache), which is exact for every
+// channel count and mode.
 #include <hip/hip_runtime.h>
 
 #include "common.h"
 #include "swar.h"
+
+#include <cstdlib>
 
 namespace sh {
 namespace {
@@ -82,16 +74,23 @@ __global__ __launch_bounds__(kBlock) void brightness_byte_kernel(const uint8_t *
 }
 
 // ---------------------------------------------------------------------------
-// Blur, RGBA tile kernel.
+// Blur, RGBA streaming kernel.
+//
+// One wave owns a column strip of kStripPx output pixels and kRows output rows.
+// Lane l holds the 16-byte chunk of pixels [x0 - 4 + 4l, x0 + 4l) of each
+// input row; lanes 1..62 produce output, lanes 0 and 63 only supply the two
+// halo pixels their neighbours need (exchanged with lane shuffles, no LDS).
+// The wave walks down its strip: every input row is loaded once (16-byte
+// loads, the next group of 5 rows in flight while the current one is summed),
+// split into 16-bit lanes (R|B and G|A words), summed horizontally over 5
+// pixels, and pushed into a 5-row register ring whose running column sum is
+// the 25-tap box sum. Ring slots are static because rows are processed in
+// unrolled groups of 5.
 // ---------------------------------------------------------------------------
 
-constexpr int kTileW = 256;             // output pixels per tile row
-constexpr int kTileH = 32;              // output rows per tile
-constexpr int kLdsW = kTileW + 8;       // staged columns: x0 - 4 .. x0 + 259
-constexpr int kLdsH = kTileH + 4;       // staged rows: y0 - 2 .. y0 + 33
-constexpr int kChunksPerRow = kLdsW / 4;
-constexpr int kRowsPerThread = 8;       // 256 threads = 64 column groups x 4 row groups
+constexpr int kStripPx = 248;  // 62 output lanes x 4 pixels
 
+// SWAR brightness on packed RGBA words (direct kernel and byte paths).
 struct Brightness {
   uint32_t mag, mask;
   bool negative, enabled;
@@ -100,122 +99,225 @@ struct Brightness {
   }
 };
 
-template <int kMode>
-__global__ __launch_bounds__(kBlock) void blur_rgba_tile_kernel(const uint32_t *__restrict__ in,
-                                                                uint32_t *__restrict__ out,
-                                                                int width, int height,
-                                                                int tiles_x, int tiles_total,
-                                                                Brightness br) {
-  __shared__ __attribute__((aligned(16))) uint32_t tile[kLdsH][kLdsW];
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+typedef int16_t i16x2 __attribute__((ext_vector_type(2)));
 
-  // XCD-aware tile order: blocks b, b+8, b+16 ... run on one XCD; give that
-  // XCD a contiguous run of row-major tiles.
-  int b = blockIdx.x;
-  int t = b;
-  if ((tiles_total & 7) == 0) t = (b & 7) * (tiles_total >> 3) + (b >> 3);
-  const int tx = t % tiles_x, ty = t / tiles_x;
-  const int x0 = tx * kTileW, y0 = ty * kTileH;
+// Brightness of the streaming kernel, applied to 16-bit lanes (values 0..255):
+// kFuse 1 adds, min 255; kFuse 2 adds the two's complement, max 0 as signed.
+// d_lo / d_hi hold delta per lane of the R|B and G|A words (0 for a channel
+// left unchanged).
+template <int kFuse>
+__device__ __forceinline__ uint32_t brighten_lanes(uint32_t w, uint32_t d) {
+  if (kFuse == 0) return w;
+  const u16x2 sum = __builtin_bit_cast(u16x2, w) + __builtin_bit_cast(u16x2, d);
+  if (kFuse == 1) return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(sum, u16x2{255, 255}));
+  return __builtin_bit_cast(
+      uint32_t, __builtin_elementwise_max(__builtin_bit_cast(i16x2, sum), i16x2{0, 0}));
+}
 
-  // ---- stage input + halo ----
-  for (int idx = threadIdx.x; idx < kLdsH * kChunksPerRow; idx += kBlock) {
-    const int r = idx / kChunksPerRow, j = idx - r * kChunksPerRow;
-    const int gy = y0 - 2 + r;
-    const int gx = x0 - 4 + 4 * j;
-    u32x4 v;
-    const bool row_in = gy >= 0 && gy < height;
-    if (kMode == SH_BLUR_CONFIG) {
-      const int cy = min(max(gy, 0), height - 1);
-      const uint32_t *row = in + (size_t)cy * width;
-      if (gx >= 0 && gx + 3 < width) {
-        v = *reinterpret_cast<const u32x4 *>(row + gx);
-      } else {  // chunk fully left or right of the image (width % 4 == 0)
-        const uint32_t p = row[gx < 0 ? 0 : width - 1];
-        v = u32x4{p, p, p, p};
-      }
-      v.x = br(v.x); v.y = br(v.y); v.z = br(v.z); v.w = br(v.w);
-    } else {
-      if (row_in && gx >= 0 && gx + 3 < width) {
-        v = *reinterpret_cast<const u32x4 *>(in + (size_t)gy * width + gx);
-        v.x = br(v.x); v.y = br(v.y); v.z = br(v.z); v.w = br(v.w);
-      } else {
-        v = u32x4{0, 0, 0, 0};  // out-of-bounds taps add nothing
-      }
-    }
-    *reinterpret_cast<u32x4 *>(&tile[r][4 * j]) = v;
+// Whole-wave lane shifts by DPP (GFX9 wave_shr:1 / wave_shl:1): lane i gets
+// lane i-1 (from_left) or lane i+1 (from_right); lanes 0 / 63 keep their own
+// value, which the streaming kernel never uses.
+__device__ __forceinline__ uint32_t from_left(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x138, 0xf, 0xf, false);
+}
+__device__ __forceinline__ uint32_t from_right(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x130, 0xf, 0xf, false);
+}
+
+struct StreamArgs {
+  const uint32_t *in;
+  uint32_t *out;
+  int width, height, strips_x, total_waves, xcd_blocks;
+  uint32_t d_lo, d_hi;  // brightness deltas per 16-bit lane (R|B, G|A)
+};
+
+// Horizontal 5-pixel sums of the 4 pixels of this lane, as 16-bit lanes:
+// h[2k] = R|B, h[2k+1] = G|A of pixel k. `v` is this lane's 4 pixels; the two
+// pixels on either side come from the neighbouring lanes. At the image's left
+// and right edges the missing neighbours are replaced by the edge pixel
+// (config: clamp) or by zero (reference: out-of-bounds taps add nothing).
+template <int kMode, int kFuse>
+__device__ __forceinline__ void hsum(const u32x4 v, int y, int height, uint32_t h[8],
+                                     bool left_edge, bool right_edge, uint32_t d_lo,
+                                     uint32_t d_hi) {
+  if (kMode == SH_BLUR_REFERENCE && (y < 0 || y >= height)) {  // row outside: no taps
+#pragma unroll
+    for (int k = 0; k < 8; k++) h[k] = 0;
+    return;
   }
-  __syncthreads();
-
-  // ---- 4 x 8 output block per thread ----
-  const int cg = threadIdx.x & 63;       // column group: pixels 4*cg .. 4*cg+3
-  const int rg = threadIdx.x >> 6;       // row group: rows 8*rg .. 8*rg+7
-  const int ox = x0 + 4 * cg;
-  const int oy0 = y0 + kRowsPerThread * rg;
-  if (ox >= width || oy0 >= height) return;
-
-  // horizontal sums, two 16-bit-lane words (R|B, G|A) per output pixel
-  uint32_t hs[kRowsPerThread + 4][4][2];
-#pragma unroll
-  for (int rr = 0; rr < kRowsPerThread + 4; rr++) {
-    const uint32_t *row = &tile[kRowsPerThread * rg + rr][4 * cg];
-    // staged cols 4cg+2 .. 4cg+9 feed output pixels 4cg+4 .. 4cg+7
-    const u32x2 a = *reinterpret_cast<const u32x2 *>(row + 2);
-    const u32x4 m = *reinterpret_cast<const u32x4 *>(row + 4);
-    const u32x2 c = *reinterpret_cast<const u32x2 *>(row + 8);
-    const uint32_t p[8] = {a.x, a.y, m.x, m.y, m.z, m.w, c.x, c.y};
-    uint32_t lo[8], hi[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      lo[k] = p[k] & 0x00ff00ffu;
-      hi[k] = (p[k] >> 8) & 0x00ff00ffu;
-    }
-    uint32_t sl = lo[0] + lo[1] + lo[2] + lo[3] + lo[4];
-    uint32_t sh = hi[0] + hi[1] + hi[2] + hi[3] + hi[4];
-    hs[rr][0][0] = sl;
-    hs[rr][0][1] = sh;
-#pragma unroll
-    for (int k = 1; k < 4; k++) {
-      sl += lo[k + 4] - lo[k - 1];
-      sh += hi[k + 4] - hi[k - 1];
-      hs[rr][k][0] = sl;
-      hs[rr][k][1] = sh;
-    }
-  }
-
-  // per-pixel tap counts for the reference mode's border pixels
-  int cx[4];
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  uint32_t lo[8], hi[8];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    const int x = ox + k;
-    cx[k] = min(x + 2, width - 1) - max(x - 2, 0) + 1;
+    lo[k + 2] = brighten_lanes<kFuse>(__builtin_amdgcn_perm(0u, w[k], 0x0c020c00u), d_lo);
+    hi[k + 2] = brighten_lanes<kFuse>(__builtin_amdgcn_perm(0u, w[k], 0x0c030c01u), d_hi);
+  }
+  lo[0] = from_left(lo[4]);
+  lo[1] = from_left(lo[5]);
+  hi[0] = from_left(hi[4]);
+  hi[1] = from_left(hi[5]);
+  lo[6] = from_right(lo[2]);
+  lo[7] = from_right(lo[3]);
+  hi[6] = from_right(hi[2]);
+  hi[7] = from_right(hi[3]);
+  if (kMode == SH_BLUR_CONFIG) {
+    lo[0] = left_edge ? lo[2] : lo[0];
+    lo[1] = left_edge ? lo[2] : lo[1];
+    hi[0] = left_edge ? hi[2] : hi[0];
+    hi[1] = left_edge ? hi[2] : hi[1];
+    lo[6] = right_edge ? lo[5] : lo[6];
+    lo[7] = right_edge ? lo[5] : lo[7];
+    hi[6] = right_edge ? hi[5] : hi[6];
+    hi[7] = right_edge ? hi[5] : hi[7];
+  } else {
+    lo[0] = left_edge ? 0u : lo[0];
+    lo[1] = left_edge ? 0u : lo[1];
+    hi[0] = left_edge ? 0u : hi[0];
+    hi[1] = left_edge ? 0u : hi[1];
+    lo[6] = right_edge ? 0u : lo[6];
+    lo[7] = right_edge ? 0u : lo[7];
+    hi[6] = right_edge ? 0u : hi[6];
+    hi[7] = right_edge ? 0u : hi[7];
+  }
+#pragma unroll
+  for (int part = 0; part < 2; part++) {
+    const uint32_t *a = part ? hi : lo;
+    const uint32_t u34 = a[3] + a[4];
+    const uint32_t s = a[2] + u34, t = u34 + a[5];
+    h[0 + part] = s + a[0] + a[1];
+    h[2 + part] = s + a[1] + a[5];
+    h[4 + part] = t + a[2] + a[6];
+    h[6 + part] = t + a[6] + a[7];
+  }
+}
+
+// Bytes of one output pixel from its 25-tap sums (lo word R|B, hi word G|A,
+// each lane < 6400; in config mode the lanes already carry the +12 rounding
+// bias). floor(s / 25) = (s * 671089) >> 24 exactly for s < 6400: 671089 /
+// 2^24 exceeds 1/25 by < 2.2e-8, the product fits 32 bits and the quotient is
+// its top byte, which v_perm gathers.
+template <int kMode>
+__device__ __forceinline__ uint32_t finish_pixel(uint32_t vl, uint32_t vh, uint32_t count) {
+  if (kMode == SH_BLUR_CONFIG || count == 25) {
+    const uint32_t r = __umul24(vl & 0xffffu, 671089u);
+    const uint32_t b = __umul24(vl >> 16, 671089u);
+    const uint32_t g = __umul24(vh & 0xffffu, 671089u);
+    const uint32_t a = __umul24(vh >> 16, 671089u);
+    const uint32_t rg = __builtin_amdgcn_perm(g, r, 0x0c0c0703u);
+    const uint32_t ba = __builtin_amdgcn_perm(a, b, 0x07030c0cu);
+    return rg | ba;
+  }
+  const uint32_t c0 = (vl & 0xffffu) / count, c2 = (vl >> 16) / count;
+  const uint32_t c1 = (vh & 0xffffu) / count, c3 = (vh >> 16) / count;
+  return c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
+}
+
+// One input row for this lane (a cached load: the band above and below read
+// the same halo rows). The row index is wave-uniform (scalar), so the
+// row address is scalar and each lane adds its column offset. Lanes whose
+// chunk lies outside the image load a valid chunk nobody uses (the edge fix-up
+// in hsum supplies the clamped or zero taps instead).
+template <int kMode>
+__device__ __forceinline__ u32x4 load_row(const StreamArgs &a, int y, int lx) {
+  if (kMode == SH_BLUR_CONFIG) {
+    const int cy = min(max(y, 0), a.height - 1);
+    return *reinterpret_cast<const u32x4 *>(a.in + (size_t)cy * (size_t)a.width + lx);
+  } else {
+    if (y < 0 || y >= a.height) return u32x4{0, 0, 0, 0};
+    return *reinterpret_cast<const u32x4 *>(a.in + (size_t)y * (size_t)a.width + lx);
+  }
+}
+
+template <int kMode, int kFuse, int kGroups>
+__global__ __launch_bounds__(kBlock) void blur_rgba_stream_kernel(const StreamArgs a) {
+  constexpr int kRows = 5 * kGroups;
+  // Blocks are dealt round-robin to the 8 XCDs; renumber them so each XCD
+  // walks a contiguous range of waves (neighbouring bands share halo rows in
+  // that XCD's L2).
+  int b = blockIdx.x;
+  if (a.xcd_blocks) b = (b & 7) * a.xcd_blocks + (b >> 3);
+  const int lane = threadIdx.x & 63;
+  const int wi = b * (kBlock / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (wi >= a.total_waves) return;
+  const int sx = wi % a.strips_x, band = wi / a.strips_x;
+  const int x0 = sx * kStripPx;
+  const int cx = x0 - 4 + 4 * lane;  // first pixel of this lane's chunk
+  const int lx = min(max(cx, 0), a.width - 4);
+  const bool left_edge = cx == 0;              // pixels -2, -1 are outside
+  const bool right_edge = cx + 4 == a.width;   // pixels W, W+1 are outside
+  const int y0 = band * kRows;
+  const bool writer = lane >= 1 && lane <= 62 && cx < a.width;
+  const int out_rows = min(kRows, a.height - y0);
+
+  int cxk[4];  // reference mode: in-bounds taps per row for each pixel
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int x = cx + k;
+    cxk[k] = min(x + 2, a.width - 1) - max(x - 2, 0) + 1;
   }
 
+  // vs starts at the config mode's +12 rounding bias in every lane.
+  const uint32_t bias = kMode == SH_BLUR_CONFIG ? 0x000c000cu : 0u;
+  uint32_t ring[5][8];
+  uint32_t vs[8];
 #pragma unroll
-  for (int r = 0; r < kRowsPerThread; r++) {
-    const int y = oy0 + r;
-    if (y >= height) break;
-    const int ry = min(y + 2, height - 1) - max(y - 2, 0) + 1;
-    uint32_t res[4];
+  for (int i = 0; i < 8; i++) {
+    vs[i] = bias;
+    ring[4][i] = 0;
+  }
+  {  // prologue: input rows y0-2 .. y0+1 into slots 0..3
+    u32x4 p[4];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const uint32_t vl = hs[r][k][0] + hs[r + 1][k][0] + hs[r + 2][k][0] + hs[r + 3][k][0] +
-                          hs[r + 4][k][0];
-      const uint32_t vh = hs[r][k][1] + hs[r + 1][k][1] + hs[r + 2][k][1] + hs[r + 3][k][1] +
-                          hs[r + 4][k][1];
-      uint32_t c0 = vl & 0xffffu, c2 = vl >> 16, c1 = vh & 0xffffu, c3 = vh >> 16;
-      if (kMode == SH_BLUR_CONFIG) {
-        c0 = div25(c0 + 12); c1 = div25(c1 + 12); c2 = div25(c2 + 12); c3 = div25(c3 + 12);
-      } else {
-        const uint32_t cnt = (uint32_t)(ry * cx[k]);
-        if (cnt == 25) {
-          c0 = div25(c0); c1 = div25(c1); c2 = div25(c2); c3 = div25(c3);
-        } else {
-          c0 /= cnt; c1 /= cnt; c2 /= cnt; c3 /= cnt;
-        }
-      }
-      res[k] = c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
+    for (int r = 0; r < 4; r++) p[r] = load_row<kMode>(a, y0 - 2 + r, lx);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      hsum<kMode, kFuse>(p[r], y0 - 2 + r, a.height, ring[r], left_edge, right_edge, a.d_lo,
+                         a.d_hi);
+#pragma unroll
+      for (int i = 0; i < 8; i++) vs[i] += ring[r][i];
     }
-    *reinterpret_cast<u32x4 *>(out + (size_t)y * width + ox) =
-        u32x4{res[0], res[1], res[2], res[3]};
+  }
+
+  u32x4 cur[5], nxt[5];
+#pragma unroll
+  for (int r = 0; r < 5; r++) cur[r] = load_row<kMode>(a, y0 + 2 + r, lx);
+
+#pragma unroll 1
+  for (int g = 0; g < kGroups; g++) {
+    if (5 * g >= out_rows) break;
+    if (g + 1 < kGroups) {
+#pragma unroll
+      for (int r = 0; r < 5; r++) nxt[r] = load_row<kMode>(a, y0 + 7 + 5 * g + r, lx);
+    }
+#pragma unroll
+    for (int i = 0; i < 5; i++) {
+      const int slot = (4 + i) % 5;  // input row 4 + 5g + i of the strip
+      uint32_t h[8];
+      hsum<kMode, kFuse>(cur[i], y0 + 2 + 5 * g + i, a.height, h, left_edge, right_edge, a.d_lo,
+                         a.d_hi);
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        vs[k] = (vs[k] - ring[slot][k]) + h[k];  // lanes never borrow: ring is part of vs
+        ring[slot][k] = h[k];
+      }
+      const int row = 5 * g + i;
+      const int y = y0 + row;
+      if (writer && row < out_rows) {
+        const uint32_t ry = kMode == SH_BLUR_CONFIG
+                                ? 5u
+                                : (uint32_t)(min(y + 2, a.height - 1) - max(y - 2, 0) + 1);
+        u32x4 o;
+        o.x = finish_pixel<kMode>(vs[0], vs[1], ry * cxk[0]);
+        o.y = finish_pixel<kMode>(vs[2], vs[3], ry * cxk[1]);
+        o.z = finish_pixel<kMode>(vs[4], vs[5], ry * cxk[2]);
+        o.w = finish_pixel<kMode>(vs[6], vs[7], ry * cxk[3]);
+        __builtin_nontemporal_store(
+            o, reinterpret_cast<u32x4 *>(a.out + (size_t)y * (size_t)a.width + cx));
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 5; r++) cur[r] = nxt[r];
   }
 }
 
@@ -272,6 +374,56 @@ Brightness make_brightness(bool enabled, int channels, int delta, int all_channe
   return br;
 }
 
+// Output rows per wave = 5 * groups: 2 (10 rows) by default; the
+// STRICT_HIP_BLUR_GROUPS environment variable (1, 2 or 4) overrides it for
+// tuning sweeps.
+int blur_groups() {
+  static const int groups = [] {
+    const char *e = getenv("STRICT_HIP_BLUR_GROUPS");
+    const int g = e ? atoi(e) : 2;
+    return (g == 1 || g == 4) ? g : 2;
+  }();
+  return groups;
+}
+
+template <int kMode, int kGroups>
+void launch_stream_fuse(hipStream_t s, const StreamArgs &a, int fuse) {
+  const int blocks = (a.total_waves + kBlock / 64 - 1) / (kBlock / 64);
+  if (fuse == 1)
+    blur_rgba_stream_kernel<kMode, 1, kGroups><<<blocks, kBlock, 0, s>>>(a);
+  else if (fuse == 2)
+    blur_rgba_stream_kernel<kMode, 2, kGroups><<<blocks, kBlock, 0, s>>>(a);
+  else
+    blur_rgba_stream_kernel<kMode, 0, kGroups><<<blocks, kBlock, 0, s>>>(a);
+}
+
+template <int kGroups>
+void launch_blur_stream(hipStream_t s, const uint32_t *in, uint32_t *out, int width, int height,
+                        int mode, bool fuse, int delta, int all_channels) {
+  StreamArgs a;
+  a.in = in;
+  a.out = out;
+  a.width = width;
+  a.height = height;
+  a.strips_x = (width + kStripPx - 1) / kStripPx;
+  const int bands = (height + 5 * kGroups - 1) / (5 * kGroups);
+  a.total_waves = a.strips_x * bands;
+  const int blocks = (a.total_waves + kBlock / 64 - 1) / (kBlock / 64);
+  a.xcd_blocks = (blocks % 8 == 0) ? blocks / 8 : 0;
+  int f = 0;
+  a.d_lo = a.d_hi = 0;
+  if (fuse && delta != 0) {
+    f = delta > 0 ? 1 : 2;
+    const uint32_t d = (uint32_t)(uint16_t)(int16_t)delta;  // lane value, two's complement
+    a.d_lo = d | (d << 16);                                 // R and B
+    a.d_hi = d | (all_channels ? d << 16 : 0u);             // G, and A only if asked
+  }
+  if (mode == SH_BLUR_CONFIG)
+    launch_stream_fuse<SH_BLUR_CONFIG, kGroups>(s, a, f);
+  else
+    launch_stream_fuse<SH_BLUR_REFERENCE, kGroups>(s, a, f);
+}
+
 }  // namespace
 
 hipError_t launch_brightness_u8(hipStream_t s, const uint8_t *in, uint8_t *out, size_t bytes,
@@ -293,18 +445,19 @@ hipError_t launch_brightness_u8(hipStream_t s, const uint8_t *in, uint8_t *out, 
 hipError_t launch_blur5_u8(hipStream_t s, const uint8_t *in, uint8_t *out, int width, int height,
                            int channels, int mode, bool fuse, int delta, int all_channels) {
   if (channels == 4 && width % 4 == 0 && aligned16(in) && aligned16(out)) {
-    const int tiles_x = (width + kTileW - 1) / kTileW;
-    const int tiles_y = (height + kTileH - 1) / kTileH;
-    const int total = tiles_x * tiles_y;
-    const Brightness br = make_brightness(fuse, channels, delta, all_channels);
     const uint32_t *in32 = reinterpret_cast<const uint32_t *>(in);
     uint32_t *out32 = reinterpret_cast<uint32_t *>(out);
-    if (mode == SH_BLUR_CONFIG)
-      blur_rgba_tile_kernel<SH_BLUR_CONFIG>
-          <<<total, kBlock, 0, s>>>(in32, out32, width, height, tiles_x, total, br);
-    else
-      blur_rgba_tile_kernel<SH_BLUR_REFERENCE>
-          <<<total, kBlock, 0, s>>>(in32, out32, width, height, tiles_x, total, br);
+    switch (blur_groups()) {
+      case 1:
+        launch_blur_stream<1>(s, in32, out32, width, height, mode, fuse, delta, all_channels);
+        break;
+      case 4:
+        launch_blur_stream<4>(s, in32, out32, width, height, mode, fuse, delta, all_channels);
+        break;
+      default:
+        launch_blur_stream<2>(s, in32, out32, width, height, mode, fuse, delta, all_channels);
+        break;
+    }
   } else {
     const long long pixels = (long long)width * height;
     blur_direct_kernel<<<(unsigned)((pixels + kBlock - 1) / kBlock), kBlock, 0, s>>>(

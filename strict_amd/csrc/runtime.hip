@@ -257,7 +257,11 @@ SH_API int sh_copy(sh_ctx *ctx, void *dst, const void *src, size_t bytes) {
   if (bytes == 0) return SH_OK;
   SH_CHECK(check_range(ctx, dst, bytes, "device destination"));
   SH_CHECK(check_range(ctx, src, bytes, "device source"));
-  SH_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+  uintptr_t d = reinterpret_cast<uintptr_t>(dst), r = reinterpret_cast<uintptr_t>(src);
+  if (d != r && d < r + bytes && r < d + bytes)
+    return fail(SH_ERR_INVALID_ARGUMENT, "source and destination overlap");
+  if (d == r) return SH_OK;
+  SH_HIP_TRY(launch_copy_bytes(ctx->stream, dst, src, bytes));
   return SH_OK;
 }
 
