@@ -31,6 +31,8 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
+GEMM_N = 4096
 IMG_W = IMG_H = 4096
 IMG_BYTES = IMG_W * IMG_H * 4
 SIGMOID_N = 1 << 24
@@ -226,6 +228,26 @@ def main() -> int:
     def sigmoid(k):
         s, d = srot[k]
         ctx.sigmoid(s, d, SIGMOID_N)
+
+    # -- bf16 GEMM: compute-bound, operands reused across launches --
+    ga = rng.normal(0, 0.02, (GEMM_N, GEMM_N)).astype(np.float32)
+    gbits = (ga.view(np.uint32) + 0x7FFF + ((ga.view(np.uint32) >> 16) & 1)) >> 16
+    dA = ctx.upload(gbits.astype(np.uint16))
+    dB = ctx.upload(np.ascontiguousarray(gbits.T).astype(np.uint16))
+    dC = ctx.empty((GEMM_N, GEMM_N), np.uint16)
+
+    def gemm(k):
+        ctx.gemm_bf16(dA, dB, dC, GEMM_N, GEMM_N, GEMM_N)
+
+    _, gavg, _ = time_launches(ctx, gemm, 20, 3)
+    gflop = 2.0 * GEMM_N ** 3
+    tflops = gflop / (gavg * 1e-3) / 1e12
+    kernels.append({"kernel": "gemm_bf16 4096^3", "alg_flop": gflop, "avg_ms": round(gavg, 5),
+                    "TFLOP/s": round(tflops, 1),
+                    "frac_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4)})
+    log(f"gemm: {kernels[-1]}")
+    for v in (dA, dB, dC):
+        v.free()
 
     # -- the workload of the headline line --
     if args.workload == "image":

@@ -183,6 +183,18 @@ SH_API int sh_box_blur5_u8(sh_ctx *ctx, const uint8_t *in, uint8_t *out, int wid
 SH_API int sh_brightness_blur5_u8(sh_ctx *ctx, const uint8_t *in, uint8_t *out, int width,
                                   int height, int channels, int delta, int flags, int mode);
 
+/* ---- typed ops: dense GEMM --------------------------------------------------
+ * The reference's only GEMM hook is the cuBLAS handle of Kernel.Handle
+ * (Kernel.cs:10-11, :16), never used; BASELINE configs[2] fixes the op. */
+
+/* C[M,N] = A[M,K] * B[K,N]: bf16 operands (raw 16-bit patterns), fp32
+ * accumulation, bf16 result (round to nearest even), row-major with leading
+ * dimensions lda >= K, ldb >= N, ldc >= N (elements). K == 0 writes zeros.
+ * The MFMA path needs M, N multiples of 256, K of 64, lda/ldb multiples of 8
+ * and 16-byte aligned A/B; other shapes run a slower exact-fp32 kernel. */
+SH_API int sh_gemm_bf16(sh_ctx *ctx, const uint16_t *A, const uint16_t *B, uint16_t *C, int M,
+                        int N, int K, int lda, int ldb, int ldc);
+
 #ifdef __cplusplus
 }
 #endif

@@ -385,6 +385,15 @@ class Context:
                                               channels, delta, flags, mode))
 
 
+    def gemm_bf16(self, a, b, c, m: int, n: int, k: int, lda: int | None = None,
+                  ldb: int | None = None, ldc: int | None = None) -> None:
+        """C[m,n] = A[m,k] @ B[k,n]; bf16 operands (uint16 bit patterns), fp32
+        accumulation, bf16 result, row-major with leading dimensions."""
+        _check(self._l.sh_gemm_bf16(self.handle, _ptr(a), _ptr(b), _ptr(c), m, n, k,
+                                    k if lda is None else lda, n if ldb is None else ldb,
+                                    n if ldc is None else ldc))
+
+
 class Event:
     """A HIP event on a context's stream (per-launch timing)."""
 

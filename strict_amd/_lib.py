@@ -94,6 +94,7 @@ SIGNATURES = {
     "sh_adjust_brightness_u8": (_I, [_P, _P, _P, _I, _I, _I, _I, _I]),
     "sh_box_blur5_u8": (_I, [_P, _P, _P, _I, _I, _I, _I]),
     "sh_brightness_blur5_u8": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I]),
+    "sh_gemm_bf16": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I]),
 }
 
 _lib = None

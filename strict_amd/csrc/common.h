@@ -40,6 +40,11 @@ hipError_t launch_saxpy_f32(hipStream_t s, float a, const float *x, const float 
 hipError_t launch_sigmoid_f32(hipStream_t s, const float *x, float *y, size_t n);
 hipError_t launch_copy_bytes(hipStream_t s, void *dst, const void *src, size_t bytes);
 
+hipError_t launch_gemm_bf16(hipStream_t s, const uint16_t *A, const uint16_t *B, uint16_t *C,
+                            int M, int N, int K, int lda, int ldb, int ldc);
+bool gemm_bf16_uses_mfma(int M, int N, int K, int lda, int ldb, int ldc, const void *A,
+                         const void *B, const void *C);
+
 hipError_t launch_brightness_u8(hipStream_t s, const uint8_t *in, uint8_t *out, size_t bytes,
                                 int channels, int delta, int all_channels);
 hipError_t launch_blur5_u8(hipStream_t s, const uint8_t *in, uint8_t *out, int width, int height,

@@ -612,4 +612,36 @@ SH_API int sh_brightness_blur5_u8(sh_ctx *ctx, const uint8_t *in, uint8_t *out, 
   return blur_common(ctx, in, out, width, height, channels, mode, true, delta, flags);
 }
 
+// ---- typed ops: dense GEMM ----------------------------------------------------
+
+// Elements a row-major [rows x cols] operand with leading dimension ld spans.
+static size_t span_elems(int rows, int cols, int ld) {
+  return rows == 0 || cols == 0 ? 0 : (size_t)(rows - 1) * (size_t)ld + (size_t)cols;
+}
+
+static int check_gemm_dims(int M, int N, int K, int lda, int ldb, int ldc) {
+  if (M < 0 || N < 0 || K < 0)
+    return fail(SH_ERR_INVALID_ARGUMENT, "negative GEMM size M=%d N=%d K=%d", M, N, K);
+  if (lda < K || ldb < N || ldc < N)
+    return fail(SH_ERR_INVALID_ARGUMENT,
+                "leading dimensions too small: lda=%d (K=%d) ldb=%d (N=%d) ldc=%d (N=%d)", lda, K,
+                ldb, N, ldc, N);
+  return SH_OK;
+}
+
+SH_API int sh_gemm_bf16(sh_ctx *ctx, const uint16_t *A, const uint16_t *B, uint16_t *C, int M,
+                        int N, int K, int lda, int ldb, int ldc) {
+  SH_CHECK(enter(ctx));
+  SH_CHECK(check_gemm_dims(M, N, K, lda, ldb, ldc));
+  if (M == 0 || N == 0) return SH_OK;
+  SH_CHECK(check_range(ctx, C, span_elems(M, N, ldc) * 2, "C"));
+  if (K == 0) {  // empty sum: C = 0
+    for (int m = 0; m < M; m++) SH_HIP_TRY(hipMemsetAsync(C + (size_t)m * ldc, 0, (size_t)N * 2, ctx->stream));
+    return SH_OK;
+  }
+  SH_CHECK(check_range(ctx, A, span_elems(M, K, lda) * 2, "A"));
+  SH_CHECK(check_range(ctx, B, span_elems(K, N, ldb) * 2, "B"));
+  return launched(launch_gemm_bf16(ctx->stream, A, B, C, M, N, K, lda, ldb, ldc), "gemm_bf16");
+}
+
 }  // extern "C"

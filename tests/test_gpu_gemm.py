@@ -1,0 +1,111 @@
+"""GPU parity of the bf16 GEMM (sh_gemm_bf16) against fp32/fp64 references.
+
+The reference has no GEMM of its own (Kernel.cs:10-11 holds an unused cuBLAS
+handle); BASELINE configs[2] fixes the workload: C = A*B, bf16 inputs, fp32
+accumulation, bf16 output, M = N = K = 4096, row-major, N(0, 0.02) entries.
+Tolerance (north star): within 1e-2 relative. Stated here as
+  max |C_gpu - C_ref| <= 1e-2 * max |C_ref|   and   ||C_gpu - C_ref|| / ||C_ref|| <= 1e-2,
+with C_ref the exact product of the bf16-rounded operands (oracle.gemm_f32,
+double accumulation), checked on sampled rows at 4096^3 and in full below.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import strict_amd
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16_operands(m, n, k, seed):
+    rng = np.random.default_rng(seed)
+    a = oracle.f32_to_bf16(rng.normal(0, 0.02, (m, k)).astype(np.float32))
+    b = oracle.f32_to_bf16(rng.normal(0, 0.02, (k, n)).astype(np.float32))
+    return a, b
+
+
+def _run(ctx, a, b, m, n, k, lda=None, ldb=None, ldc=None):
+    da, db = ctx.upload(a), ctx.upload(b)
+    ldc_ = n if ldc is None else ldc
+    dc = ctx.empty((m, ldc_) if m else (1,), np.uint16)
+    ctx.gemm_bf16(da, db, dc, m, n, k, lda, ldb, ldc_)
+    ctx.sync()
+    c = dc.to_host()
+    for v in (da, db, dc):
+        v.free()
+    return c
+
+
+def _check(c_gpu_bits, ref):
+    c = oracle.bf16_to_f32(c_gpu_bits)
+    err = np.abs(c - ref)
+    scale = np.abs(ref).max()
+    assert err.max() <= 1e-2 * scale, (err.max(), scale)
+    assert np.linalg.norm(c - ref) <= 1e-2 * np.linalg.norm(ref)
+    return float(err.max() / scale)
+
+
+def test_gemm_4096_config(ctx):
+    m = n = k = 4096
+    a, b = _bf16_operands(m, n, k, seed=42)
+    c = _run(ctx, a, b, m, n, k)
+    af, bf = oracle.bf16_to_f32(a), oracle.bf16_to_f32(b)
+    rows = np.random.default_rng(1).choice(m, 48, replace=False)
+    ref_rows = oracle.gemm_f32(af[rows], bf)  # double accumulation
+    rel = _check(c[rows], ref_rows)
+    # full matrix against an fp32 BLAS product of the same operands
+    ref = af @ bf
+    _check(c, ref)
+    print(f"gemm 4096^3 max err / max |C| = {rel:.3e}")
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 256, 64), (512, 768, 320), (768, 512, 4096),
+                                   (1024, 2048, 128)])
+def test_gemm_mfma_shapes(ctx, m, n, k):
+    a, b = _bf16_operands(m, n, k, seed=m + n + k)
+    c = _run(ctx, a, b, m, n, k)
+    _check(c, oracle.gemm_f32(oracle.bf16_to_f32(a), oracle.bf16_to_f32(b)))
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (100, 37, 50), (3, 300, 7), (257, 255, 65),
+                                   (64, 64, 1000)])
+def test_gemm_generic_shapes(ctx, m, n, k):
+    a, b = _bf16_operands(m, n, k, seed=m * 7 + n)
+    c = _run(ctx, a, b, m, n, k)
+    _check(c, oracle.gemm_f32(oracle.bf16_to_f32(a), oracle.bf16_to_f32(b)))
+
+
+def test_gemm_leading_dimensions(ctx):
+    m, n, k, lda, ldb, ldc = 256, 256, 128, 136, 264, 272
+    rng = np.random.default_rng(3)
+    a = oracle.f32_to_bf16(rng.normal(0, 1, (m, lda)).astype(np.float32))
+    b = oracle.f32_to_bf16(rng.normal(0, 1, (k, ldb)).astype(np.float32))
+    c = _run(ctx, a, b, m, n, k, lda, ldb, ldc)[:, :n]
+    _check(c, oracle.gemm_f32(oracle.bf16_to_f32(a[:, :k]), oracle.bf16_to_f32(b[:, :n])))
+
+
+def test_gemm_identity_is_exact(ctx):
+    # A * I == A bit for bit (each output is one bf16 product plus zeros)
+    m = n = k = 512
+    a, _ = _bf16_operands(m, n, k, seed=9)
+    eye = oracle.f32_to_bf16(np.eye(k, dtype=np.float32))
+    assert np.array_equal(_run(ctx, a, eye, m, n, k), a)
+
+
+def test_gemm_k_zero_gives_zeros(ctx):
+    c = _run(ctx, np.zeros(8, np.uint16), np.zeros(8, np.uint16), 4, 4, 0)
+    assert not c.any()
+
+
+def test_gemm_deterministic(ctx):
+    a, b = _bf16_operands(512, 512, 512, seed=4)
+    assert np.array_equal(_run(ctx, a, b, 512, 512, 512), _run(ctx, a, b, 512, 512, 512))
+
+
+def test_gemm_rejects_bad_arguments(ctx):
+    buf = ctx.empty(64 * 64, np.uint16)
+    with pytest.raises(strict_amd.StrictHipError):
+        ctx.gemm_bf16(buf, buf, buf, 64, 64, 64, lda=32)  # lda < K
+    with pytest.raises(strict_amd.StrictHipError):
+        ctx.gemm_bf16(buf, buf, buf, 128, 64, 64)  # A does not fit its buffer
+    buf.free()
