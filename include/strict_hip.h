@@ -195,6 +195,81 @@ SH_API int sh_brightness_blur5_u8(sh_ctx *ctx, const uint8_t *in, uint8_t *out, 
 SH_API int sh_gemm_bf16(sh_ctx *ctx, const uint16_t *A, const uint16_t *B, uint16_t *C, int M,
                         int N, int K, int lda, int ldb, int ldc);
 
+/* ---- weight quantization ------------------------------------------------------
+ * No reference counterpart: BASELINE configs[4] fixes the format. */
+
+/* Per-row OCP E4M3 quantization of a device fp32 matrix W[N][K]:
+ * scale[n] = max_k |W[n][k]| / 448 (1 for an all-zero row), q = e4m3(W / scale)
+ * rounded to nearest even and saturated to +-448, written row-major
+ * (q[n * K + k]); K must be a multiple of 64. */
+SH_API int sh_quantize_e4m3(sh_ctx *ctx, const float *W, int N, int K, uint8_t *q, float *scales);
+
+/* Row-major E4M3 q[N][K] -> the tiled layout sh_gemv_w8a16 reads (16-row x
+ * 64-column 1 KiB tiles in MFMA operand order; N % 16 == 0, K % 64 == 0). */
+SH_API int sh_pack_e4m3_tiles(sh_ctx *ctx, const uint8_t *q, int N, int K, uint8_t *tiled);
+
+/* W8A16 GEMV / skinny GEMM: y[b][n] = scale[n] * sum_k x[b][k] * e4m3(q[n][k])
+ * for b < batch (1..16); x fp16 [batch][K], y fp32 [batch][N], fp32
+ * accumulation of exact products. K % 256 == 0, N % 16 == 0, x and w_tiled
+ * 16-byte aligned. */
+SH_API int sh_gemv_w8a16(sh_ctx *ctx, const uint16_t *x, const uint8_t *w_tiled,
+                         const float *scales, float *y, int batch, int K, int N);
+
+/* ---- LLM decode (model runners) ------------------------------------------------
+ * No reference counterpart: BASELINE configs[3] (GPT-2 small, fp16 weights)
+ * and configs[4] (Qwen3-0.6B shape, FP8-E4M3 weights with per-output-channel
+ * fp32 scales) define the models. One sh_llm owns its weights, KV cache and
+ * work buffers on the context's device; steps are ordered on the context's
+ * stream and replayed from a HIP graph after the first step of a batch. */
+
+typedef enum sh_llm_arch {
+  SH_LLM_QWEN3 = 0, /* RMSNorm, q/k head RMSNorm, RoPE (rotate-half), GQA, SwiGLU,
+                       FP8 linears, FP8 LM head tied to the embedding */
+  SH_LLM_GPT2 = 1,  /* LayerNorm, learned positions, MHA, GELU (tanh), biases,
+                       fp16 linears, LM head tied to the token embedding */
+} sh_llm_arch;
+
+typedef struct sh_llm_config {
+  int arch;
+  int layers, hidden, heads, kv_heads, head_dim, intermediate, vocab;
+  int max_positions; /* KV cache length per sequence (GPT-2: also the position table) */
+  int max_batch;     /* 1..16 */
+  float rope_theta;  /* Qwen3 */
+  float norm_eps;
+} sh_llm_config;
+
+typedef struct sh_llm sh_llm;
+
+SH_API int sh_llm_create(sh_ctx *ctx, const sh_llm_config *config, sh_llm **model);
+SH_API int sh_llm_destroy(sh_llm *model);
+/* Every linear (and the head / GPT-2 position table) ~ N(0, stddev) from a
+ * counter-based generator seeded by `seed`, then quantized (Qwen3) or rounded
+ * to fp16 (GPT-2); norm gains 1, biases 0. */
+SH_API int sh_llm_init_random(sh_llm *model, uint64_t seed, float stddev);
+/* Replaces one linear from a device fp32 matrix W[N][K] in logical row order.
+ * name: "qkv" (rows q | k | v), "o", "gate_up" (Qwen3, rows gate | up), "fc"
+ * (GPT-2), "down" (Qwen3) / "proj" (GPT-2), "head" (layer ignored; vocab
+ * rounded up to a multiple of 16 rows, the padding rows zero). */
+SH_API int sh_llm_load_linear(sh_llm *model, const char *name, int layer, const float *W);
+/* Device address and size of a named tensor, for uploads and read-back:
+ * "<linear>.w" (tiled layout), "<linear>.scale", "<linear>.bias", "norm1.g",
+ * "norm1.b", "norm2.g", "norm2.b", "q_norm", "k_norm", "final.g", "final.b",
+ * "wpe", "inv_freq", "kcache", "vcache" (per layer), "logits", "hist", "lens". */
+SH_API int sh_llm_tensor(sh_llm *model, const char *name, int layer, void **device_ptr,
+                         size_t *bytes);
+/* Starts `batch` empty sequences (clears the KV lengths). */
+SH_API int sh_llm_reset(sh_llm *model, int batch);
+/* One decode step for every sequence: embeds tokens[b] (host array) or, when
+ * tokens is NULL, the greedy token the previous step produced; runs the layers;
+ * with want_logits, the LM head writes logits and the greedy (argmax) token. */
+SH_API int sh_llm_step(sh_llm *model, const int32_t *tokens, int want_logits);
+/* Waits for the stream and copies the greedy tokens of the last step (host). */
+SH_API int sh_llm_next_tokens(sh_llm *model, int32_t *tokens);
+/* prompt[b * prompt_len + i] (host): prompt_len steps, then greedy decoding
+ * until `steps` tokens per sequence are produced into out[b * steps + j]. */
+SH_API int sh_llm_generate(sh_llm *model, const int32_t *prompt, int prompt_len, int steps,
+                           int32_t *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -394,6 +394,19 @@ class Context:
                                     n if ldc is None else ldc))
 
 
+    def quantize_e4m3(self, w, q, scales, n: int, k: int) -> None:
+        """Per-row OCP E4M3 quantization of a device fp32 [n, k] matrix."""
+        _check(self._l.sh_quantize_e4m3(self.handle, _ptr(w), n, k, _ptr(q), _ptr(scales)))
+
+    def pack_e4m3_tiles(self, q, tiled, n: int, k: int) -> None:
+        _check(self._l.sh_pack_e4m3_tiles(self.handle, _ptr(q), n, k, _ptr(tiled)))
+
+    def gemv_w8a16(self, x, w_tiled, scales, y, batch: int, k: int, n: int) -> None:
+        """y[b] = scales * (x[b] @ e4m3(q).T); x fp16 [batch, k], y fp32 [batch, n]."""
+        _check(self._l.sh_gemv_w8a16(self.handle, _ptr(x), _ptr(w_tiled), _ptr(scales), _ptr(y),
+                                     batch, k, n))
+
+
 class Event:
     """A HIP event on a context's stream (per-launch timing)."""
 

@@ -46,6 +46,23 @@ class DeviceInfo(ctypes.Structure):
     ]
 
 
+class LlmConfig(ctypes.Structure):
+    _fields_ = [
+        ("arch", ctypes.c_int),
+        ("layers", ctypes.c_int),
+        ("hidden", ctypes.c_int),
+        ("heads", ctypes.c_int),
+        ("kv_heads", ctypes.c_int),
+        ("head_dim", ctypes.c_int),
+        ("intermediate", ctypes.c_int),
+        ("vocab", ctypes.c_int),
+        ("max_positions", ctypes.c_int),
+        ("max_batch", ctypes.c_int),
+        ("rope_theta", ctypes.c_float),
+        ("norm_eps", ctypes.c_float),
+    ]
+
+
 _P = ctypes.c_void_p
 _PP = ctypes.POINTER(ctypes.c_void_p)
 _I = ctypes.c_int
@@ -95,6 +112,18 @@ SIGNATURES = {
     "sh_box_blur5_u8": (_I, [_P, _P, _P, _I, _I, _I, _I]),
     "sh_brightness_blur5_u8": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I]),
     "sh_gemm_bf16": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I]),
+    "sh_quantize_e4m3": (_I, [_P, _P, _I, _I, _P, _P]),
+    "sh_pack_e4m3_tiles": (_I, [_P, _P, _I, _I, _P]),
+    "sh_gemv_w8a16": (_I, [_P, _P, _P, _P, _P, _I, _I, _I]),
+    "sh_llm_create": (_I, [_P, ctypes.POINTER(LlmConfig), _PP]),
+    "sh_llm_destroy": (_I, [_P]),
+    "sh_llm_init_random": (_I, [_P, ctypes.c_uint64, _F]),
+    "sh_llm_load_linear": (_I, [_P, ctypes.c_char_p, _I, _P]),
+    "sh_llm_tensor": (_I, [_P, ctypes.c_char_p, _I, _PP, ctypes.POINTER(_SZ)]),
+    "sh_llm_reset": (_I, [_P, _I]),
+    "sh_llm_step": (_I, [_P, _P, _I]),
+    "sh_llm_next_tokens": (_I, [_P, _P]),
+    "sh_llm_generate": (_I, [_P, _P, _I, _I, _P]),
 }
 
 _lib = None

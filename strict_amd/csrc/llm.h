@@ -1,0 +1,92 @@
+// Internal interface between the LLM decode kernels (llm_kernels.hip) and the
+// model runner (llm.hip). Not part of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace sh {
+
+constexpr int kMaxBatch = 16;        // rows of the GEMV's MFMA A operand
+constexpr int kMaxSplitChunk = 1024; // positions one attention workgroup may score
+
+enum { kWeightFp8 = 0, kWeightFp16 = 1 };
+enum { kProNone = 0, kProRms = 1, kProLayer = 2 };
+enum { kEpiStore = 0, kEpiResidual = 1, kEpiSwiGLU = 2, kEpiGelu = 3, kEpiLogits = 4 };
+
+// y[b][n] = (sum_k A[b][k] * W[n][k]) * scale[n] + bias[n], then the epilogue.
+// A is fp16 activations (`act`, kProNone) or the fp32 residual stream `x`
+// normalised per row (RMSNorm: x / sqrt(mean(x^2) + eps) * gamma; LayerNorm:
+// (x - mean) / sqrt(var + eps) * gamma + beta), rounded to fp16.
+struct GemvArgs {
+  const uint8_t *w = nullptr;   // tiled weights, N rows (multiple of 16)
+  const float *scale = nullptr; // per-row FP8 scales, or nullptr
+  const float *bias = nullptr;  // per-row bias, or nullptr
+  const float *x = nullptr;     // fp32 input rows (kProRms / kProLayer)
+  int x_ld = 0;
+  const uint16_t *act = nullptr;  // fp16 input rows (kProNone)
+  int act_ld = 0;
+  const float *gamma = nullptr, *beta = nullptr;
+  float eps = 0.0f;
+  int B = 0, K = 0, N = 0;
+  int n_valid = 0;  // logits: columns >= n_valid are padding
+  float *out = nullptr;      // fp32 output / residual rows
+  uint16_t *out16 = nullptr; // fp16 output rows (SwiGLU, GELU)
+  int out_ld = 0;
+  unsigned long long *argmax = nullptr;  // logits: per-row argmax keys (atomicMax)
+};
+
+struct AttnArgs {
+  const float *qkv = nullptr;  // [B][qkv_ld] fp32: q (heads*d) | k (kv_heads*d) | v
+  int qkv_ld = 0;
+  uint16_t *kcache = nullptr, *vcache = nullptr;  // this layer: [B][kv_heads][max_pos][d] fp16
+  int max_pos = 0;
+  const int *pos = nullptr;  // [B] position of the new token (= tokens already cached)
+  const float *q_norm = nullptr, *k_norm = nullptr;  // Qwen3 per-head RMSNorm gains [d]
+  float eps = 0.0f;
+  const float *inv_freq = nullptr;  // Qwen3 RoPE inverse frequencies [d/2]
+  float scale = 1.0f;               // 1 / sqrt(d)
+  int heads = 0, kv_heads = 0;
+  int splits = 1;                   // grid.x
+  float *part = nullptr;            // [B][heads][splits][d + 2]
+  int *counters = nullptr;          // [B][kv_heads], zero between launches
+  uint16_t *out = nullptr;          // [B][out_ld] fp16 head outputs
+  int out_ld = 0;
+};
+
+struct EmbedArgs {
+  unsigned long long *keys = nullptr;  // [B] argmax keys (token = ~low word)
+  int *lens = nullptr;                 // [B] tokens cached so far (advanced here)
+  int *pos = nullptr;                  // [B] position of this step's token (written here)
+  int *hist = nullptr;                 // [B][hist_len] token history
+  int hist_len = 0;
+  float *x = nullptr;                  // [B][x_ld] fp32 residual stream
+  int x_ld = 0, K = 0, vocab = 0, max_pos = 0;
+  int fp8_head = 0;
+  const uint8_t *head8 = nullptr;      // FP8 tiled head (Qwen3, tied embedding)
+  const float *head_scale = nullptr;
+  const uint16_t *head16 = nullptr;    // fp16 tiled head (GPT-2, tied wte)
+  const uint16_t *wpe = nullptr;       // GPT-2 positions [max_pos][K] fp16
+};
+
+// Lets every GEMV instantiation use up to 160 KiB of dynamic LDS (current device).
+hipError_t prepare_gemv_kernels();
+hipError_t launch_gemv(hipStream_t s, const GemvArgs &a, int weight_type, int pro, int epi,
+                       int max_grid);
+hipError_t launch_attention(hipStream_t s, const AttnArgs &a, int head_dim, int group, bool qwen,
+                            int batch);
+hipError_t launch_embed(hipStream_t s, const EmbedArgs &a, int batch);
+hipError_t launch_quantize_e4m3_tiled(hipStream_t s, const float *w, int N, int K,
+                                      int interleave_rows, uint8_t *q, float *scales,
+                                      bool tiled);
+hipError_t launch_pack_e4m3_tiles(hipStream_t s, const uint8_t *q, int N, int K, uint8_t *out);
+hipError_t launch_tile_f16(hipStream_t s, const float *w, int N, int K, int interleave_rows,
+                           uint16_t *out);
+hipError_t launch_fill_normal(hipStream_t s, float *out, size_t n, uint64_t seed, float mean,
+                              float stddev);
+hipError_t launch_fill_value(hipStream_t s, float *out, size_t n, float v);
+hipError_t launch_f32_to_f16(hipStream_t s, const float *in, uint16_t *out, size_t n);
+
+}  // namespace sh

@@ -1,0 +1,664 @@
+// LLM model runner behind sh_llm_*: owns the weights, KV cache and work
+// buffers of one decoder on a context's device and enqueues a decode step as
+//   embed -> per layer [norm+QKV GEMV, attention, O GEMV + residual,
+//                       norm+up GEMV (SwiGLU / GELU), down GEMV + residual]
+//         -> final norm + LM head GEMV with argmax
+// on the context's stream. Every per-step quantity (tokens, positions, argmax
+// keys) lives in device memory, so a step is captured once per batch size as
+// a HIP graph and replayed.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "llm.h"
+
+using namespace sh;
+
+namespace {
+
+struct Linear {
+  uint8_t *w = nullptr;  // tiled (FP8 bytes or fp16)
+  float *scale = nullptr;
+  float *bias = nullptr;
+  int N = 0, K = 0;          // N = rows as stored (gate/up: 2 * intermediate)
+  int interleave = 0;        // gate/up: intermediate (tiles interleaved), else 0
+  size_t w_bytes = 0;
+};
+
+struct Layer {
+  float *norm1_g = nullptr, *norm1_b = nullptr, *norm2_g = nullptr, *norm2_b = nullptr;
+  float *q_norm = nullptr, *k_norm = nullptr;
+  Linear qkv, o, up, down;
+  uint16_t *kcache = nullptr, *vcache = nullptr;
+};
+
+int attention_splits(int batch, int kv_heads, int max_pos) {
+  int s = 1024 / (batch * kv_heads);
+  if (s > 64) s = 64;
+  const int min_s = (max_pos + kMaxSplitChunk - 1) / kMaxSplitChunk;
+  if (s < min_s) s = min_s;
+  return s < 1 ? 1 : s;
+}
+
+}  // namespace
+
+struct sh_llm {
+  sh_ctx *ctx = nullptr;
+  sh_llm_config cfg{};
+  bool qwen = true;
+  int wtype = kWeightFp8;
+  int qkv_n = 0, vocab_pad = 0;
+  std::vector<void *> allocs;
+  std::vector<Layer> layers;
+  Linear head;
+  float *final_g = nullptr, *final_b = nullptr;
+  uint16_t *wpe = nullptr;
+  float *inv_freq = nullptr;
+  // per-step state
+  float *x = nullptr, *qkv = nullptr, *logits = nullptr, *part = nullptr;
+  uint16_t *attn = nullptr, *act = nullptr;
+  int *counters = nullptr, *lens = nullptr, *pos = nullptr, *hist = nullptr;
+  unsigned long long *keys = nullptr;
+  int batch = 0, splits = 1, steps_done = 0;
+  size_t kv_layer_elems = 0;
+  hipGraphExec_t graph[2] = {nullptr, nullptr};
+  int graph_batch[2] = {-1, -1};
+};
+
+namespace {
+
+int llm_alloc(sh_llm *m, size_t bytes, void **p) {
+  *p = nullptr;
+  if (bytes == 0) return SH_OK;
+  SH_HIP_TRY(hipMalloc(p, bytes));
+  m->allocs.push_back(*p);
+  // registered with the context so that sh_upload / sh_download / typed ops
+  // accept the model's tensors
+  int rc = sh_register_external(m->ctx, *p, bytes);
+  if (rc != SH_OK) return rc;
+  SH_HIP_TRY(hipMemsetAsync(*p, 0, bytes, stream_of(m->ctx)));
+  return SH_OK;
+}
+
+template <class T>
+int alloc_n(sh_llm *m, size_t n, T **p) {
+  void *v = nullptr;
+  int rc = llm_alloc(m, n * sizeof(T), &v);
+  *p = static_cast<T *>(v);
+  return rc;
+}
+
+int alloc_linear(sh_llm *m, Linear &l, int N, int K, int interleave, bool bias) {
+  l.N = N;
+  l.K = K;
+  l.interleave = interleave;
+  l.w_bytes = (size_t)N * K * (m->wtype == kWeightFp8 ? 1 : 2);
+  int rc = llm_alloc(m, l.w_bytes, reinterpret_cast<void **>(&l.w));
+  if (rc == SH_OK && m->wtype == kWeightFp8) rc = alloc_n(m, (size_t)N, &l.scale);
+  if (rc == SH_OK && bias) rc = alloc_n(m, (size_t)N, &l.bias);
+  return rc;
+}
+
+int fill(sh_llm *m, float *p, size_t n, float v) {
+  if (!p) return SH_OK;
+  const hipError_t e = launch_fill_value(stream_of(m->ctx), p, n, v);
+  return e == hipSuccess ? SH_OK : hip_fail(e, "fill");
+}
+
+// Quantizes / tiles a device fp32 [N][K] matrix (logical order) into `l`.
+int store_linear(sh_llm *m, Linear &l, const float *w) {
+  hipStream_t s = stream_of(m->ctx);
+  hipError_t e = m->wtype == kWeightFp8
+                     ? launch_quantize_e4m3_tiled(s, w, l.N, l.K, l.interleave, l.w, l.scale, true)
+                     : launch_tile_f16(s, w, l.N, l.K, l.interleave, reinterpret_cast<uint16_t *>(l.w));
+  return e == hipSuccess ? SH_OK : hip_fail(e, "storing a linear layer");
+}
+
+Linear *find_linear(sh_llm *m, const std::string &name, int layer) {
+  if (name == "head") return &m->head;
+  if (layer < 0 || layer >= (int)m->layers.size()) return nullptr;
+  Layer &L = m->layers[layer];
+  if (name == "qkv") return &L.qkv;
+  if (name == "o") return &L.o;
+  if (name == (m->qwen ? "gate_up" : "fc")) return &L.up;
+  if (name == (m->qwen ? "down" : "proj")) return &L.down;
+  return nullptr;
+}
+
+int enqueue_step(sh_llm *m, bool logits) {
+  const sh_llm_config &c = m->cfg;
+  hipStream_t s = stream_of(m->ctx);
+  const int B = m->batch, H = c.hidden, d = c.head_dim;
+  const int pro = m->qwen ? kProRms : kProLayer;
+
+  EmbedArgs e;
+  e.keys = m->keys;
+  e.lens = m->lens;
+  e.pos = m->pos;
+  e.hist = m->hist;
+  e.hist_len = c.max_positions;
+  e.x = m->x;
+  e.x_ld = H;
+  e.K = H;
+  e.vocab = c.vocab;
+  e.max_pos = c.max_positions;
+  e.fp8_head = m->qwen ? 1 : 0;
+  e.head8 = m->head.w;
+  e.head_scale = m->head.scale;
+  e.head16 = reinterpret_cast<const uint16_t *>(m->head.w);
+  e.wpe = m->wpe;
+  SH_HIP_TRY(launch_embed(s, e, B));
+
+  for (Layer &L : m->layers) {
+    GemvArgs g;
+    g.w = L.qkv.w;
+    g.scale = L.qkv.scale;
+    g.bias = L.qkv.bias;
+    g.x = m->x;
+    g.x_ld = H;
+    g.gamma = L.norm1_g;
+    g.beta = L.norm1_b;
+    g.eps = c.norm_eps;
+    g.B = B;
+    g.K = H;
+    g.N = L.qkv.N;
+    g.out = m->qkv;
+    g.out_ld = m->qkv_n;
+    SH_HIP_TRY(launch_gemv(s, g, m->wtype, pro, kEpiStore, 0));
+
+    AttnArgs a;
+    a.qkv = m->qkv;
+    a.qkv_ld = m->qkv_n;
+    a.kcache = L.kcache;
+    a.vcache = L.vcache;
+    a.max_pos = c.max_positions;
+    a.pos = m->pos;
+    a.q_norm = L.q_norm;
+    a.k_norm = L.k_norm;
+    a.eps = c.norm_eps;
+    a.inv_freq = m->inv_freq;
+    a.scale = 1.0f / std::sqrt((float)d);
+    a.heads = c.heads;
+    a.kv_heads = c.kv_heads;
+    a.splits = m->splits;
+    a.part = m->part;
+    a.counters = m->counters;
+    a.out = m->attn;
+    a.out_ld = c.heads * d;
+    SH_HIP_TRY(launch_attention(s, a, d, c.heads / c.kv_heads, m->qwen, B));
+
+    GemvArgs o;
+    o.w = L.o.w;
+    o.scale = L.o.scale;
+    o.bias = L.o.bias;
+    o.act = m->attn;
+    o.act_ld = c.heads * d;
+    o.B = B;
+    o.K = c.heads * d;
+    o.N = L.o.N;
+    o.out = m->x;
+    o.out_ld = H;
+    SH_HIP_TRY(launch_gemv(s, o, m->wtype, kProNone, kEpiResidual, 0));
+
+    GemvArgs u;
+    u.w = L.up.w;
+    u.scale = L.up.scale;
+    u.bias = L.up.bias;
+    u.x = m->x;
+    u.x_ld = H;
+    u.gamma = L.norm2_g;
+    u.beta = L.norm2_b;
+    u.eps = c.norm_eps;
+    u.B = B;
+    u.K = H;
+    u.N = L.up.N;
+    u.out16 = m->act;
+    u.out_ld = c.intermediate;
+    SH_HIP_TRY(launch_gemv(s, u, m->wtype, pro, m->qwen ? kEpiSwiGLU : kEpiGelu, 0));
+
+    GemvArgs dn;
+    dn.w = L.down.w;
+    dn.scale = L.down.scale;
+    dn.bias = L.down.bias;
+    dn.act = m->act;
+    dn.act_ld = c.intermediate;
+    dn.B = B;
+    dn.K = c.intermediate;
+    dn.N = L.down.N;
+    dn.out = m->x;
+    dn.out_ld = H;
+    SH_HIP_TRY(launch_gemv(s, dn, m->wtype, kProNone, kEpiResidual, 0));
+  }
+
+  if (logits) {
+    GemvArgs h;
+    h.w = m->head.w;
+    h.scale = m->head.scale;
+    h.x = m->x;
+    h.x_ld = H;
+    h.gamma = m->final_g;
+    h.beta = m->final_b;
+    h.eps = c.norm_eps;
+    h.B = B;
+    h.K = H;
+    h.N = m->head.N;
+    h.n_valid = c.vocab;
+    h.out = m->logits;
+    h.out_ld = m->vocab_pad;
+    h.argmax = m->keys;
+    SH_HIP_TRY(launch_gemv(s, h, m->wtype, pro, kEpiLogits, 1024));
+  }
+  return SH_OK;
+}
+
+void drop_graphs(sh_llm *m) {
+  for (int i = 0; i < 2; i++) {
+    if (m->graph[i]) (void)hipGraphExecDestroy(m->graph[i]);
+    m->graph[i] = nullptr;
+    m->graph_batch[i] = -1;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+SH_API int sh_quantize_e4m3(sh_ctx *ctx, const float *W, int N, int K, uint8_t *q,
+                            float *scales) {
+  int rc = enter(ctx);
+  if (rc != SH_OK) return rc;
+  if (N < 0 || K <= 0 || K % 64 != 0)
+    return fail(SH_ERR_INVALID_ARGUMENT, "quantize: need N >= 0 and K a positive multiple of 64 (N=%d K=%d)", N, K);
+  if (N == 0) return SH_OK;
+  if ((rc = check_range(ctx, W, (size_t)N * K * 4, "W")) != SH_OK) return rc;
+  if ((rc = check_range(ctx, q, (size_t)N * K, "q")) != SH_OK) return rc;
+  if ((rc = check_range(ctx, scales, (size_t)N * 4, "scales")) != SH_OK) return rc;
+  hipError_t e = launch_quantize_e4m3_tiled(stream_of(ctx), W, N, K, 0, q, scales, false);
+  return e == hipSuccess ? SH_OK : hip_fail(e, "quantize_e4m3");
+}
+
+SH_API int sh_pack_e4m3_tiles(sh_ctx *ctx, const uint8_t *q, int N, int K, uint8_t *tiled) {
+  int rc = enter(ctx);
+  if (rc != SH_OK) return rc;
+  if (N < 0 || N % 16 != 0 || K <= 0 || K % 64 != 0)
+    return fail(SH_ERR_INVALID_ARGUMENT, "pack: N must be a multiple of 16 and K of 64 (N=%d K=%d)", N, K);
+  if (N == 0) return SH_OK;
+  if ((rc = check_range(ctx, q, (size_t)N * K, "q")) != SH_OK) return rc;
+  if ((rc = check_range(ctx, tiled, (size_t)N * K, "tiled")) != SH_OK) return rc;
+  const hipError_t e = launch_pack_e4m3_tiles(stream_of(ctx), q, N, K, tiled);
+  return e == hipSuccess ? SH_OK : hip_fail(e, "pack_e4m3_tiles");
+}
+
+SH_API int sh_gemv_w8a16(sh_ctx *ctx, const uint16_t *x, const uint8_t *w_tiled,
+                         const float *scales, float *y, int batch, int K, int N) {
+  int rc = enter(ctx);
+  if (rc != SH_OK) return rc;
+  if (batch < 1 || batch > kMaxBatch)
+    return fail(SH_ERR_INVALID_ARGUMENT, "gemv batch %d outside 1..%d", batch, kMaxBatch);
+  if (K <= 0 || K % 256 != 0 || N < 0 || N % 16 != 0)
+    return fail(SH_ERR_INVALID_ARGUMENT, "gemv: K must be a multiple of 256 and N of 16 (K=%d N=%d)", K, N);
+  if (N == 0) return SH_OK;
+  if ((rc = check_range(ctx, x, (size_t)batch * K * 2, "x")) != SH_OK) return rc;
+  if ((rc = check_range(ctx, w_tiled, (size_t)N * K, "w_tiled")) != SH_OK) return rc;
+  if ((rc = check_range(ctx, scales, (size_t)N * 4, "scales")) != SH_OK) return rc;
+  if ((rc = check_range(ctx, y, (size_t)batch * N * 4, "y")) != SH_OK) return rc;
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_tiled)) & 15)
+    return fail(SH_ERR_INVALID_ARGUMENT, "x and w_tiled must be 16-byte aligned");
+  static bool prepared = false;  // dynamic-LDS attributes (process-wide, first device)
+  if (!prepared) {
+    SH_HIP_TRY(prepare_gemv_kernels());
+    prepared = true;
+  }
+  GemvArgs g;
+  g.w = w_tiled;
+  g.scale = scales;
+  g.act = x;
+  g.act_ld = K;
+  g.B = batch;
+  g.K = K;
+  g.N = N;
+  g.out = y;
+  g.out_ld = N;
+  const hipError_t e = launch_gemv(stream_of(ctx), g, kWeightFp8, kProNone, kEpiStore, 2048);
+  return e == hipSuccess ? SH_OK : hip_fail(e, "gemv_w8a16");
+}
+
+SH_API int sh_llm_create(sh_ctx *ctx, const sh_llm_config *config, sh_llm **out) {
+  int rc = enter(ctx);
+  if (rc != SH_OK) return rc;
+  if (!config || !out) return fail(SH_ERR_INVALID_ARGUMENT, "NULL argument");
+  *out = nullptr;
+  const sh_llm_config c = *config;
+  const bool qwen = c.arch == SH_LLM_QWEN3;
+  if (c.arch != SH_LLM_QWEN3 && c.arch != SH_LLM_GPT2)
+    return fail(SH_ERR_INVALID_ARGUMENT, "unknown architecture %d", c.arch);
+  if (c.layers <= 0 || c.hidden <= 0 || c.heads <= 0 || c.kv_heads <= 0 || c.vocab <= 0 ||
+      c.intermediate <= 0 || c.max_positions <= 0)
+    return fail(SH_ERR_INVALID_ARGUMENT, "model sizes must be positive");
+  if (c.max_batch < 1 || c.max_batch > kMaxBatch)
+    return fail(SH_ERR_INVALID_ARGUMENT, "max_batch must be 1..%d", kMaxBatch);
+  if (c.heads % c.kv_heads != 0)
+    return fail(SH_ERR_INVALID_ARGUMENT, "heads %d not a multiple of kv_heads %d", c.heads, c.kv_heads);
+  const int group = c.heads / c.kv_heads;
+  const bool attn_ok = qwen ? (c.head_dim == 128 && (group == 1 || group == 2))
+                            : ((c.head_dim == 64 || c.head_dim == 128) && group == 1);
+  if (!attn_ok)
+    return fail(SH_ERR_UNSUPPORTED, "attention kernel not built for head_dim %d, group %d (%s)",
+                c.head_dim, group, qwen ? "qwen3" : "gpt2");
+  // K of every GEMV must split into 4 waves of whole 16-byte tile loads
+  const int kalign = qwen ? 256 : 128;
+  const int ks[3] = {c.hidden, c.heads * c.head_dim, c.intermediate};
+  for (int k : ks)
+    if (k % kalign != 0)
+      return fail(SH_ERR_UNSUPPORTED, "GEMV input width %d is not a multiple of %d", k, kalign);
+  if (c.intermediate % 16 != 0 || c.hidden % 16 != 0)
+    return fail(SH_ERR_UNSUPPORTED, "hidden and intermediate must be multiples of 16");
+  if (c.max_positions > 65536) return fail(SH_ERR_INVALID_ARGUMENT, "max_positions > 65536");
+  if (!qwen && c.hidden % 8 != 0) return fail(SH_ERR_UNSUPPORTED, "hidden must be a multiple of 8");
+
+  auto *m = new sh_llm();
+  m->ctx = ctx;
+  m->cfg = c;
+  m->qwen = qwen;
+  m->wtype = qwen ? kWeightFp8 : kWeightFp16;
+  m->qkv_n = (c.heads + 2 * c.kv_heads) * c.head_dim;
+  m->vocab_pad = (c.vocab + 15) / 16 * 16;
+  const int B = c.max_batch, H = c.hidden, d = c.head_dim;
+  m->kv_layer_elems = (size_t)B * c.kv_heads * c.max_positions * d;
+  const int max_splits = attention_splits(1, c.kv_heads, c.max_positions);
+
+  auto cleanup = [&](int status) {
+    for (void *p : m->allocs) {
+      (void)sh_unregister_external(ctx, p);
+      (void)hipFree(p);
+    }
+    delete m;
+    return status;
+  };
+  m->layers.resize(c.layers);
+  for (Layer &L : m->layers) {
+    if ((rc = alloc_n(m, H, &L.norm1_g)) || (rc = alloc_n(m, H, &L.norm2_g))) return cleanup(rc);
+    if (!qwen && ((rc = alloc_n(m, H, &L.norm1_b)) || (rc = alloc_n(m, H, &L.norm2_b))))
+      return cleanup(rc);
+    if (qwen && ((rc = alloc_n(m, d, &L.q_norm)) || (rc = alloc_n(m, d, &L.k_norm))))
+      return cleanup(rc);
+    const bool bias = !qwen;
+    if ((rc = alloc_linear(m, L.qkv, m->qkv_n, H, 0, bias)) ||
+        (rc = alloc_linear(m, L.o, H, c.heads * d, 0, bias)) ||
+        (rc = alloc_linear(m, L.up, qwen ? 2 * c.intermediate : c.intermediate, H,
+                           qwen ? c.intermediate : 0, bias)) ||
+        (rc = alloc_linear(m, L.down, H, c.intermediate, 0, bias)))
+      return cleanup(rc);
+    if ((rc = alloc_n(m, m->kv_layer_elems, &L.kcache)) ||
+        (rc = alloc_n(m, m->kv_layer_elems, &L.vcache)))
+      return cleanup(rc);
+  }
+  if ((rc = alloc_linear(m, m->head, m->vocab_pad, H, 0, false))) return cleanup(rc);
+  if ((rc = alloc_n(m, H, &m->final_g))) return cleanup(rc);
+  if (!qwen && ((rc = alloc_n(m, H, &m->final_b)) ||
+                (rc = alloc_n(m, (size_t)c.max_positions * H, &m->wpe))))
+    return cleanup(rc);
+  if (qwen) {
+    if ((rc = alloc_n(m, d / 2, &m->inv_freq))) return cleanup(rc);
+    std::vector<float> f(d / 2);
+    for (int i = 0; i < d / 2; i++)
+      f[i] = (float)std::pow((double)c.rope_theta, -2.0 * i / (double)d);
+    hipError_t e = hipMemcpyAsync(m->inv_freq, f.data(), f.size() * 4, hipMemcpyHostToDevice,
+                                  stream_of(ctx));
+    if (e == hipSuccess) e = hipStreamSynchronize(stream_of(ctx));
+    if (e != hipSuccess) return cleanup(hip_fail(e, "uploading RoPE frequencies"));
+  }
+  if ((rc = alloc_n(m, (size_t)B * H, &m->x)) || (rc = alloc_n(m, (size_t)B * m->qkv_n, &m->qkv)) ||
+      (rc = alloc_n(m, (size_t)B * c.heads * d, &m->attn)) ||
+      (rc = alloc_n(m, (size_t)B * c.intermediate, &m->act)) ||
+      (rc = alloc_n(m, (size_t)B * m->vocab_pad, &m->logits)) ||
+      (rc = alloc_n(m, (size_t)B * c.heads * max_splits * (d + 2), &m->part)) ||
+      (rc = alloc_n(m, (size_t)B * c.kv_heads, &m->counters)) ||
+      (rc = alloc_n(m, (size_t)B, &m->lens)) || (rc = alloc_n(m, (size_t)B, &m->pos)) ||
+      (rc = alloc_n(m, (size_t)B * c.max_positions, &m->hist)) ||
+      (rc = alloc_n(m, (size_t)B, &m->keys)))
+    return cleanup(rc);
+  // norm gains start at 1 (biases and weights at 0)
+  for (Layer &L : m->layers) {
+    if ((rc = fill(m, L.norm1_g, H, 1.0f)) || (rc = fill(m, L.norm2_g, H, 1.0f)) ||
+        (rc = fill(m, L.q_norm, d, 1.0f)) || (rc = fill(m, L.k_norm, d, 1.0f)))
+      return cleanup(rc);
+  }
+  if ((rc = fill(m, m->final_g, H, 1.0f))) return cleanup(rc);
+  hipError_t e = prepare_gemv_kernels();
+  if (e == hipSuccess) e = hipStreamSynchronize(stream_of(ctx));
+  if (e != hipSuccess) return cleanup(hip_fail(e, "preparing the model"));
+  *out = m;
+  return SH_OK;
+}
+
+SH_API int sh_llm_destroy(sh_llm *m) {
+  if (!m) return SH_OK;
+  (void)hipSetDevice(device_of(m->ctx));
+  (void)hipStreamSynchronize(stream_of(m->ctx));
+  drop_graphs(m);
+  for (void *p : m->allocs) {
+    (void)sh_unregister_external(m->ctx, p);
+    (void)hipFree(p);
+  }
+  delete m;
+  return SH_OK;
+}
+
+SH_API int sh_llm_init_random(sh_llm *m, uint64_t seed, float stddev) {
+  if (!m) return fail(SH_ERR_INVALID_ARGUMENT, "model is NULL");
+  int rc = enter(m->ctx);
+  if (rc != SH_OK) return rc;
+  hipStream_t s = stream_of(m->ctx);
+  size_t max_elems = (size_t)m->head.N * m->head.K;
+  for (Layer &L : m->layers)
+    for (Linear *l : {&L.qkv, &L.o, &L.up, &L.down})
+      if ((size_t)l->N * l->K > max_elems) max_elems = (size_t)l->N * l->K;
+  float *tmp = nullptr;
+  SH_HIP_TRY(hipMalloc(&tmp, max_elems * sizeof(float)));
+  uint64_t stream_id = seed * 1000003ull;
+  auto gen = [&](Linear &l) -> int {
+    hipError_t e = launch_fill_normal(s, tmp, (size_t)l.N * l.K, stream_id++, 0.0f, stddev);
+    if (e != hipSuccess) return hip_fail(e, "fill_normal");
+    return store_linear(m, l, tmp);
+  };
+  for (Layer &L : m->layers)
+    for (Linear *l : {&L.qkv, &L.o, &L.up, &L.down})
+      if ((rc = gen(*l)) != SH_OK) break;
+  if (rc == SH_OK) {
+    // head: only the real vocabulary rows are random, padding rows stay zero
+    Linear real = m->head;
+    real.N = m->cfg.vocab / 16 * 16;
+    if ((rc = gen(real)) == SH_OK && real.N < m->head.N) {
+      // the last partial tile: generate full rows, zero the padding rows
+      const int n0 = real.N, rows = m->head.N - n0;
+      hipError_t e = launch_fill_normal(s, tmp, (size_t)rows * m->head.K, stream_id++, 0.0f, stddev);
+      if (e == hipSuccess)
+        e = hipMemsetAsync(tmp + (size_t)(m->cfg.vocab - n0) * m->head.K, 0,
+                           (size_t)(m->head.N - m->cfg.vocab) * m->head.K * 4, s);
+      Linear last = m->head;
+      last.N = 16;
+      last.w = m->head.w + (size_t)n0 * m->head.K * (m->wtype == kWeightFp8 ? 1 : 2);
+      last.scale = m->head.scale ? m->head.scale + n0 : nullptr;
+      if (e != hipSuccess) rc = hip_fail(e, "head padding");
+      else rc = store_linear(m, last, tmp);
+    }
+  }
+  if (rc == SH_OK && m->wpe) {
+    hipError_t e = launch_fill_normal(s, tmp, (size_t)m->cfg.max_positions * m->cfg.hidden,
+                                      stream_id++, 0.0f, stddev);
+    if (e == hipSuccess)
+      e = launch_f32_to_f16(s, tmp, m->wpe, (size_t)m->cfg.max_positions * m->cfg.hidden);
+    if (e != hipSuccess) rc = hip_fail(e, "wpe");
+  }
+  hipError_t e = hipStreamSynchronize(s);
+  (void)hipFree(tmp);
+  if (rc == SH_OK && e != hipSuccess) rc = hip_fail(e, "init_random");
+  return rc;
+}
+
+SH_API int sh_llm_load_linear(sh_llm *m, const char *name, int layer, const float *W) {
+  if (!m || !name) return fail(SH_ERR_INVALID_ARGUMENT, "NULL argument");
+  int rc = enter(m->ctx);
+  if (rc != SH_OK) return rc;
+  Linear *l = find_linear(m, name, layer);
+  if (!l) return fail(SH_ERR_NOT_FOUND, "no linear '%s' in layer %d", name, layer);
+  if ((rc = check_range(m->ctx, W, (size_t)l->N * l->K * 4, "W")) != SH_OK) return rc;
+  return store_linear(m, *l, W);
+}
+
+SH_API int sh_llm_tensor(sh_llm *m, const char *name, int layer, void **ptr, size_t *bytes) {
+  if (!m || !name || !ptr || !bytes) return fail(SH_ERR_INVALID_ARGUMENT, "NULL argument");
+  const sh_llm_config &c = m->cfg;
+  std::string n(name);
+  *ptr = nullptr;
+  *bytes = 0;
+  auto set = [&](void *p, size_t b) {
+    *ptr = p;
+    *bytes = p ? b : 0;
+    return p ? SH_OK : fail(SH_ERR_NOT_FOUND, "tensor '%s' does not exist in this model", name);
+  };
+  const size_t dot = n.find('.');
+  if (dot != std::string::npos) {
+    const std::string base = n.substr(0, dot), field = n.substr(dot + 1);
+    Linear *l = find_linear(m, base, layer);
+    if (l) {
+      if (field == "w") return set(l->w, l->w_bytes);
+      if (field == "scale") return set(l->scale, (size_t)l->N * 4);
+      if (field == "bias") return set(l->bias, (size_t)l->N * 4);
+    }
+  }
+  if (n == "logits") return set(m->logits, (size_t)c.max_batch * m->vocab_pad * 4);
+  if (n == "hist") return set(m->hist, (size_t)c.max_batch * c.max_positions * 4);
+  if (n == "lens") return set(m->lens, (size_t)c.max_batch * 4);
+  if (n == "final.g") return set(m->final_g, (size_t)c.hidden * 4);
+  if (n == "final.b") return set(m->final_b, (size_t)c.hidden * 4);
+  if (n == "wpe") return set(m->wpe, (size_t)c.max_positions * c.hidden * 2);
+  if (n == "inv_freq") return set(m->inv_freq, (size_t)c.head_dim / 2 * 4);
+  if (layer < 0 || layer >= c.layers)
+    return fail(SH_ERR_NOT_FOUND, "tensor '%s' layer %d not found", name, layer);
+  Layer &L = m->layers[layer];
+  if (n == "norm1.g") return set(L.norm1_g, (size_t)c.hidden * 4);
+  if (n == "norm1.b") return set(L.norm1_b, (size_t)c.hidden * 4);
+  if (n == "norm2.g") return set(L.norm2_g, (size_t)c.hidden * 4);
+  if (n == "norm2.b") return set(L.norm2_b, (size_t)c.hidden * 4);
+  if (n == "q_norm") return set(L.q_norm, (size_t)c.head_dim * 4);
+  if (n == "k_norm") return set(L.k_norm, (size_t)c.head_dim * 4);
+  if (n == "kcache") return set(L.kcache, m->kv_layer_elems * 2);
+  if (n == "vcache") return set(L.vcache, m->kv_layer_elems * 2);
+  return fail(SH_ERR_NOT_FOUND, "tensor '%s' not found", name);
+}
+
+SH_API int sh_llm_reset(sh_llm *m, int batch) {
+  if (!m) return fail(SH_ERR_INVALID_ARGUMENT, "model is NULL");
+  int rc = enter(m->ctx);
+  if (rc != SH_OK) return rc;
+  if (batch < 1 || batch > m->cfg.max_batch)
+    return fail(SH_ERR_INVALID_ARGUMENT, "batch %d outside 1..%d", batch, m->cfg.max_batch);
+  hipStream_t s = stream_of(m->ctx);
+  SH_HIP_TRY(hipMemsetAsync(m->lens, 0, (size_t)m->cfg.max_batch * 4, s));
+  SH_HIP_TRY(hipMemsetAsync(m->keys, 0, (size_t)m->cfg.max_batch * 8, s));
+  SH_HIP_TRY(hipMemsetAsync(m->counters, 0, (size_t)m->cfg.max_batch * m->cfg.kv_heads * 4, s));
+  m->batch = batch;
+  m->splits = attention_splits(batch, m->cfg.kv_heads, m->cfg.max_positions);
+  m->steps_done = 0;
+  return SH_OK;
+}
+
+SH_API int sh_llm_step(sh_llm *m, const int32_t *tokens, int want_logits) {
+  if (!m) return fail(SH_ERR_INVALID_ARGUMENT, "model is NULL");
+  int rc = enter(m->ctx);
+  if (rc != SH_OK) return rc;
+  if (m->batch == 0) return fail(SH_ERR_INVALID_ARGUMENT, "sh_llm_reset was not called");
+  if (m->steps_done >= m->cfg.max_positions)
+    return fail(SH_ERR_INVALID_ARGUMENT, "KV cache full (%d positions)", m->cfg.max_positions);
+  hipStream_t s = stream_of(m->ctx);
+  if (tokens) {
+    unsigned long long keys[kMaxBatch];
+    for (int b = 0; b < m->batch; b++) {
+      if (tokens[b] < 0 || tokens[b] >= m->cfg.vocab)
+        return fail(SH_ERR_INVALID_ARGUMENT, "token %d of row %d outside the vocabulary", tokens[b], b);
+      keys[b] = (unsigned long long)(0xffffffffu - (uint32_t)tokens[b]);
+    }
+    SH_HIP_TRY(hipMemcpyAsync(m->keys, keys, (size_t)m->batch * 8, hipMemcpyHostToDevice, s));
+    SH_HIP_TRY(hipStreamSynchronize(s));  // `keys` is a stack array
+  }
+  const int g = want_logits ? 1 : 0;
+  if (m->graph_batch[g] != m->batch) {
+    if (m->graph[g]) (void)hipGraphExecDestroy(m->graph[g]);
+    m->graph[g] = nullptr;
+    m->graph_batch[g] = -1;
+    // first step of this batch size runs eagerly, and is captured for replay
+    if ((rc = enqueue_step(m, want_logits != 0)) != SH_OK) return rc;
+    hipGraph_t graph = nullptr;
+    SH_HIP_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    rc = enqueue_step(m, want_logits != 0);
+    hipError_t e = hipStreamEndCapture(s, &graph);
+    if (rc != SH_OK) {
+      if (graph) (void)hipGraphDestroy(graph);
+      return rc;
+    }
+    if (e != hipSuccess) return hip_fail(e, "capturing the decode step");
+    e = hipGraphInstantiate(&m->graph[g], graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) return hip_fail(e, "instantiating the decode graph");
+    m->graph_batch[g] = m->batch;
+  } else {
+    SH_HIP_TRY(hipGraphLaunch(m->graph[g], s));
+  }
+  m->steps_done++;
+  return SH_OK;
+}
+
+SH_API int sh_llm_next_tokens(sh_llm *m, int32_t *tokens) {
+  if (!m || !tokens) return fail(SH_ERR_INVALID_ARGUMENT, "NULL argument");
+  int rc = enter(m->ctx);
+  if (rc != SH_OK) return rc;
+  unsigned long long keys[kMaxBatch];
+  hipStream_t s = stream_of(m->ctx);
+  SH_HIP_TRY(hipMemcpyAsync(keys, m->keys, (size_t)m->batch * 8, hipMemcpyDeviceToHost, s));
+  SH_HIP_TRY(hipStreamSynchronize(s));
+  for (int b = 0; b < m->batch; b++) {
+    if (keys[b] == 0) return fail(SH_ERR_INVALID_ARGUMENT, "no greedy token yet (step without logits?)");
+    tokens[b] = (int32_t)(0xffffffffu - (uint32_t)(keys[b] & 0xffffffffu));
+  }
+  return SH_OK;
+}
+
+SH_API int sh_llm_generate(sh_llm *m, const int32_t *prompt, int prompt_len, int steps,
+                           int32_t *out) {
+  if (!m || !prompt || !out) return fail(SH_ERR_INVALID_ARGUMENT, "NULL argument");
+  if (m->batch == 0) return fail(SH_ERR_INVALID_ARGUMENT, "sh_llm_reset was not called");
+  if (prompt_len < 1 || steps < 1)
+    return fail(SH_ERR_INVALID_ARGUMENT, "prompt_len and steps must be >= 1");
+  if (m->steps_done + prompt_len + steps - 1 > m->cfg.max_positions)
+    return fail(SH_ERR_INVALID_ARGUMENT, "prompt + steps exceed max_positions %d", m->cfg.max_positions);
+  const int B = m->batch;
+  int rc;
+  std::vector<int32_t> col(B);
+  const int start = m->steps_done;
+  for (int i = 0; i < prompt_len; i++) {
+    for (int b = 0; b < B; b++) col[b] = prompt[(size_t)b * prompt_len + i];
+    if ((rc = sh_llm_step(m, col.data(), i == prompt_len - 1)) != SH_OK) return rc;
+  }
+  for (int j = 1; j < steps; j++)
+    if ((rc = sh_llm_step(m, nullptr, 1)) != SH_OK) return rc;
+  if ((rc = sh_llm_next_tokens(m, col.data())) != SH_OK) return rc;
+  // generated tokens 0 .. steps-2 were embedded (history), the last is the key
+  std::vector<int32_t> hist((size_t)B * m->cfg.max_positions);
+  hipStream_t s = stream_of(m->ctx);
+  SH_HIP_TRY(hipMemcpyAsync(hist.data(), m->hist, hist.size() * 4, hipMemcpyDeviceToHost, s));
+  SH_HIP_TRY(hipStreamSynchronize(s));
+  for (int b = 0; b < B; b++) {
+    for (int j = 0; j + 1 < steps; j++)
+      out[(size_t)b * steps + j] = hist[(size_t)b * m->cfg.max_positions + start + prompt_len + j];
+    out[(size_t)b * steps + steps - 1] = col[b];
+  }
+  return SH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,784 @@
+// Kernels of the LLM decode path (BASELINE configs[3] GPT-2 small fp16 and
+// configs[4] Qwen3-0.6B-shaped FP8): weight quantization / tiling, a fused
+// batched GEMV on MFMA, split-K decode attention and the embedding gather.
+// The reference has no implementation of any of these (SURVEY rows a14-a16
+// of the hot path are defined by BASELINE.json only).
+//
+// Weight layout ("tiled"): a linear layer W[N][K] (N outputs, K inputs) is
+// stored as 1 KiB tiles of 16 rows, tiles of one row group consecutive along
+// K. Within a tile, lane l of a wave owns 16 bytes: the 8-element K runs
+//   W[n0 + l%16][k0 + 8*(l/16) + e], e = 0..7
+// that a v_mfma_f32_16x16x32_f16 B operand holds. An FP8 tile spans 64 K
+// values (two MFMA k-steps: bytes 0-7 step 0, bytes 8-15 step 1); an fp16
+// tile spans 32 K values. One 16-byte load per lane then feeds the MFMA and a
+// wave reads each tile as 1 KiB contiguous.
+//
+// FP8 is OCP E4M3 (bias 7, max 448, no infinities), one fp32 scale per output
+// row: W ~= e4m3(q) * scale[n]. E4M3 values are exact in fp16, so the GEMV's
+// products x * q are exact and the scale is applied once to the fp32 sum.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+#include "llm.h"
+
+namespace sh {
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kThreads = 256;
+
+// ---- number formats ---------------------------------------------------------
+
+// fp32 -> OCP E4M3, round to nearest even, saturating to +-448 (NaN -> 0x7f).
+__device__ __forceinline__ uint8_t f32_to_e4m3(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  const uint8_t sign = (uint8_t)((u >> 24) & 0x80u);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return 0x7f;       // NaN
+  if (a >= 0x43E00000u) return sign | 0x7e;  // >= 448 (and inf): saturate
+  const int e = (int)(a >> 23) - 127;
+  if (e < -6) {
+    // subnormal range of E4M3: value = m * 2^-9, m = 0..7 (m = 8 rounds up to
+    // the smallest normal 0x08)
+    const float av = __builtin_bit_cast(float, a);
+    const float m = av * 512.0f;  // exact scaling by a power of two
+    const float r = __builtin_rintf(m);  // round half to even
+    return sign | (uint8_t)r;
+  }
+  // normal: keep 3 mantissa bits, RNE on the 20 dropped bits
+  uint32_t mant = a & 0x7fffffu;
+  uint32_t q = ((uint32_t)(e + 7) << 3) | (mant >> 20);
+  const uint32_t rest = mant & 0xfffffu;
+  if (rest > 0x80000u || (rest == 0x80000u && (q & 1u))) q += 1;  // may carry into exponent
+  if (q > 0x7e) q = 0x7e;  // 464 and up round to 448 after saturation
+  return sign | (uint8_t)q;
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// ---- tiled offsets -------------------------------------------------------
+
+// Byte offset of W[n][k] in an FP8 tiled matrix with K columns.
+__device__ __forceinline__ size_t fp8_tiled_offset(int n, int k, int K) {
+  const int kt = k >> 6, k64 = k & 63, half = k64 >> 5, kk = k64 & 31;
+  const int lane = (n & 15) + 16 * (kk >> 3);
+  return ((size_t)(n >> 4) * (size_t)(K >> 6) + (size_t)kt) * 1024 + (size_t)lane * 16 +
+         (size_t)(half * 8 + (kk & 7));
+}
+
+// Element offset of W[n][k] in an fp16 tiled matrix with K columns.
+__device__ __forceinline__ size_t f16_tiled_offset(int n, int k, int K) {
+  const int kt = k >> 5, kk = k & 31;
+  const int lane = (n & 15) + 16 * (kk >> 3);
+  return (((size_t)(n >> 4) * (size_t)(K >> 5) + (size_t)kt) * 64 + (size_t)lane) * 8 +
+         (size_t)(kk & 7);
+}
+
+// Source row of tiled row n when the layer is a gate/up pair stored with its
+// 16-row tiles interleaved (gate tile p, up tile p, ...): logical input is
+// [gate (I rows); up (I rows)].
+__device__ __forceinline__ int pair_source_row(int n, int interleave_rows) {
+  if (interleave_rows == 0) return n;
+  const int tile = n >> 4, p = tile >> 1;
+  return (tile & 1) ? interleave_rows + 16 * p + (n & 15) : 16 * p + (n & 15);
+}
+
+// ---- quantization / tiling kernels --------------------------------------
+
+// One wave per output row: scale = max|w| / 448 (1 when the row is zero),
+// q = e4m3(w / scale), written in the tiled layout (or row-major).
+__global__ __launch_bounds__(kThreads) void quantize_e4m3_kernel(
+    const float *__restrict__ w, int N, int K, int interleave_rows, uint8_t *__restrict__ q,
+    float *__restrict__ scales, int tiled) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const float *row = w + (size_t)pair_source_row(n, interleave_rows) * K;
+  float amax = 0.0f;
+  for (int k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(row[k]));
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
+  if (lane == 0) scales[n] = scale;
+  for (int k = lane; k < K; k += 64)
+    q[tiled ? fp8_tiled_offset(n, k, K) : (size_t)n * K + k] = f32_to_e4m3(row[k] / scale);
+}
+
+// Row-major E4M3 bytes -> tiled layout.
+__global__ __launch_bounds__(kThreads) void pack_e4m3_tiles_kernel(const uint8_t *__restrict__ q,
+                                                                   int N, int K,
+                                                                   uint8_t *__restrict__ out) {
+  const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= (size_t)N * K) return;
+  const int n = (int)(i / K), k = (int)(i % K);
+  out[fp8_tiled_offset(n, k, K)] = q[i];
+}
+
+// fp32 [N][K] -> fp16 tiled (round to nearest even).
+__global__ __launch_bounds__(kThreads) void tile_f16_kernel(const float *__restrict__ w, int N,
+                                                            int K, int interleave_rows,
+                                                            uint16_t *__restrict__ out) {
+  const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= (size_t)N * K) return;
+  const int n = (int)(i / K), k = (int)(i % K);
+  out[f16_tiled_offset(n, k, K)] = f32_to_f16_bits(w[(size_t)pair_source_row(n, interleave_rows) * K + k]);
+}
+
+// Counter-based N(mean, std) fill: SplitMix64 of (seed, index) -> two
+// uniforms -> Box-Muller. Used for synthetic weights.
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+__global__ __launch_bounds__(kThreads) void fill_normal_kernel(float *__restrict__ out, size_t n,
+                                                               uint64_t seed, float mean,
+                                                               float stddev) {
+  const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const uint64_t r = splitmix64(seed * 0x100000001B3ull + i);
+  const float u1 = ((float)(uint32_t)(r >> 40) + 0.5f) * (1.0f / 16777216.0f);  // (0, 1)
+  const float u2 = (float)((uint32_t)r & 0xffffffu) * (1.0f / 16777216.0f);
+  const float z = sqrtf(-2.0f * logf(u1)) * cospif(2.0f * u2);
+  out[i] = mean + stddev * z;
+}
+
+__global__ __launch_bounds__(kThreads) void fill_f32_kernel(float *out, size_t n, float v) {
+  const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i < n) out[i] = v;
+}
+
+__global__ __launch_bounds__(kThreads) void f32_to_f16_kernel(const float *in, uint16_t *out,
+                                                              size_t n) {
+  const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i < n) out[i] = f32_to_f16_bits(in[i]);
+}
+
+// ---- block reductions ------------------------------------------------------
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// ---- GEMV ---------------------------------------------------------------
+
+// Stages the MFMA A operand (activations of B rows, fp16, row stride K + 8
+// elements so that the 16 rows of a 16-lane LDS phase fall in 16 distinct
+// bank groups) from fp16 activations or from the fp32 residual stream after
+// RMSNorm / LayerNorm.
+template <int kPro>
+__device__ void stage_activations(const GemvArgs &a, _Float16 *xs, float *red) {
+  const int K = a.K, B = a.B, stride = K + 8;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  if (kPro == kProNone) {
+    const int chunks = K / 8;
+    for (int i = t; i < B * chunks; i += kThreads) {
+      const int b = i / chunks, c = i - b * chunks;
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(a.act + (size_t)b * a.act_ld + c * 8);
+      *reinterpret_cast<u32x4 *>(xs + b * stride + c * 8) = v;
+    }
+    __syncthreads();
+    return;
+  }
+  // statistics per row b (LayerNorm mean, then sum of squared deviations);
+  // red[0..3] is the cross-wave scratch, red[8 + b] / red[8 + kMaxBatch + b]
+  // hold mean / 1 / sqrt(var + eps) of row b
+  for (int b = 0; b < B; b++) {
+    const float *x = a.x + (size_t)b * a.x_ld;
+    float mean = 0.0f;
+    if (kPro == kProLayer) {
+      float s = 0.0f;
+      for (int k = t; k < K; k += kThreads) s += x[k];
+      s = wave_sum(s);
+      if (lane == 0) red[wave] = s;
+      __syncthreads();
+      mean = (red[0] + red[1] + red[2] + red[3]) / (float)K;
+      __syncthreads();
+    }
+    float ss = 0.0f;
+    for (int k = t; k < K; k += kThreads) {
+      const float d = x[k] - mean;
+      ss += d * d;
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    if (t == 0) {
+      red[8 + b] = mean;
+      red[8 + kMaxBatch + b] = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + a.eps);
+    }
+    __syncthreads();
+  }
+  for (int b = 0; b < B; b++) {
+    const float *x = a.x + (size_t)b * a.x_ld;
+    const float mean = red[8 + b], inv = red[8 + kMaxBatch + b];
+    for (int k = t; k < K; k += kThreads) {
+      float y = (x[k] - mean) * inv * a.gamma[k];
+      if (kPro == kProLayer) y += a.beta[k];
+      xs[b * stride + k] = (_Float16)y;
+    }
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float c = 0.7978845608028654f;  // sqrt(2 / pi)
+  return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+// Order-preserving key of an fp32 logit with its column: larger logits give
+// larger keys; among equal logits the smaller column wins (as argmax does).
+__device__ __forceinline__ unsigned long long argmax_key(float v, int n) {
+  uint32_t u = __builtin_bit_cast(uint32_t, v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)n);
+}
+
+// One workgroup handles kNT row tiles (two for the gate/up pair) at a time,
+// grid-striding over the tile groups. Its 4 waves split K in four; the four
+// partial 16x16 accumulators are summed in LDS and wave 0 runs the epilogue.
+template <int kW, int kPro, int kEpi>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  constexpr int kNT = kEpi == kEpiSwiGLU ? 2 : 1;
+  constexpr int kKPerLoad = kW == kWeightFp8 ? 64 : 32;
+  const int K = a.K, B = a.B;
+  const int stride = K + 8;
+  _Float16 *xs = reinterpret_cast<_Float16 *>(smem);
+  float *red = reinterpret_cast<float *>(smem + (size_t)B * stride * 2);  // 4*kNT*64*4 floats
+
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  stage_activations<kPro>(a, xs, red);
+
+  const int loads_per_row = K / kKPerLoad;      // 16-byte lane loads per tile row group
+  const int per_wave = loads_per_row / 4;       // K split over the 4 waves
+  const int groups = a.N / (16 * kNT);
+  const int arow = lane & 15, acol = 8 * (lane >> 4);
+  const bool arow_valid = arow < B;
+
+  unsigned long long best[4] = {0, 0, 0, 0};  // logits: running argmax keys per b row
+
+  for (int g = blockIdx.x; g < groups; g += gridDim.x) {
+    f32x4 acc[kNT];
+#pragma unroll
+    for (int j = 0; j < kNT; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int c0 = wave * per_wave;
+    for (int c = c0; c < c0 + per_wave; c += 4) {
+      u32x4 wv[4][kNT];
+#pragma unroll
+      for (int u = 0; u < 4; u++)
+#pragma unroll
+        for (int j = 0; j < kNT; j++) {
+          const size_t tile = (size_t)(g * kNT + j) * loads_per_row + (c + u);
+          if (c + u < c0 + per_wave)
+            wv[u][j] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4 *>(a.w + tile * 1024 + (size_t)lane * 16));
+        }
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        if (c + u >= c0 + per_wave) break;
+        const int kbase = (c + u) * kKPerLoad;
+#pragma unroll
+        for (int h = 0; h < kKPerLoad / 32; h++) {
+          f16x8 af = {};
+          if (arow_valid)
+            af = *reinterpret_cast<const f16x8 *>(xs + arow * stride + kbase + 32 * h + acol);
+#pragma unroll
+          for (int j = 0; j < kNT; j++) {
+            f16x8 bf;
+            if (kW == kWeightFp8) {
+              const uint32_t d0 = wv[u][j][2 * h], d1 = wv[u][j][2 * h + 1];
+              const f16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, false);
+              const f16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, true);
+              const f16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, false);
+              const f16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, true);
+              bf = f16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+            } else {
+              bf = __builtin_bit_cast(f16x8, wv[u][j]);
+            }
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[j], 0, 0, 0);
+          }
+        }
+      }
+    }
+    // ---- sum the four K quarters ----
+#pragma unroll
+    for (int j = 0; j < kNT; j++)
+      *reinterpret_cast<f32x4 *>(red + ((wave * kNT + j) * 64 + lane) * 4) = acc[j];
+    __syncthreads();
+    if (wave == 0) {
+      f32x4 y[kNT];
+#pragma unroll
+      for (int j = 0; j < kNT; j++) {
+        y[j] = *reinterpret_cast<const f32x4 *>(red + ((0 * kNT + j) * 64 + lane) * 4);
+#pragma unroll
+        for (int w = 1; w < 4; w++) y[j] += *reinterpret_cast<const f32x4 *>(red + ((w * kNT + j) * 64 + lane) * 4);
+      }
+      // lane holds column n = tile row (lane % 16) for batch rows 4*(lane/16) + r
+      const int col = lane & 15;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int b = 4 * (lane >> 4) + r;
+        if (b >= B) continue;
+        if (kEpi == kEpiSwiGLU) {
+          const int ng = (g * 2) * 16 + col, nu = ng + 16;  // tiled rows of gate / up
+          float gv = y[0][r], uv = y[kNT - 1][r];
+          if (a.scale) { gv *= a.scale[ng]; uv *= a.scale[nu]; }
+          if (a.bias) { gv += a.bias[ng]; uv += a.bias[nu]; }
+          const int n = g * 16 + col;  // output column
+          a.out16[(size_t)b * a.out_ld + n] = f32_to_f16_bits(silu(gv) * uv);
+        } else {
+          const int n = g * 16 + col;
+          float v = y[0][r];
+          if (a.scale) v *= a.scale[n];
+          if (a.bias) v += a.bias[n];
+          if (kEpi == kEpiStore) {
+            a.out[(size_t)b * a.out_ld + n] = v;
+          } else if (kEpi == kEpiResidual) {
+            a.out[(size_t)b * a.out_ld + n] += v;
+          } else if (kEpi == kEpiGelu) {
+            a.out16[(size_t)b * a.out_ld + n] = f32_to_f16_bits(gelu_tanh(v));
+          } else {  // logits
+            if (n < a.n_valid) {
+              a.out[(size_t)b * a.out_ld + n] = v;
+              const unsigned long long key = argmax_key(v, n);
+              best[r] = key > best[r] ? key : best[r];
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  if (kEpi == kEpiLogits && wave == 0) {
+    // reduce the running keys over the 16 columns held by each lane group
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      unsigned long long k = best[r];
+#pragma unroll
+      for (int off = 8; off >= 1; off >>= 1) {
+        const unsigned long long o = __shfl_xor(k, off, 64);
+        k = o > k ? o : k;
+      }
+      const int b = 4 * (lane >> 4) + r;
+      if ((lane & 15) == 0 && b < B && k != 0) atomicMax(a.argmax + b, k);
+    }
+  }
+}
+
+// ---- decode attention ------------------------------------------------------
+
+// Positions per split for a context of L tokens over `splits` workgroups
+// (multiple of 16, at least 16); every workgroup derives the same value.
+__device__ __forceinline__ int split_chunk(int L, int splits) {
+  int c = (L + splits - 1) / splits;
+  c = (c + 15) & ~15;
+  return c < 16 ? 16 : c;
+}
+
+// grid (splits, kv_heads, B); one workgroup scores positions [p0, p1) of one
+// KV head for its kG query heads, keeps (max, sum, unnormalised V sum) per
+// head, and the last workgroup of the (b, kv head) to finish merges all
+// splits. Qwen3 (kQwen): q and the new k get RMSNorm over the head and RoPE
+// (rotate-half) at position L-1 here; the workgroup whose split holds L-1
+// also appends the new k / v to the cache.
+template <int kD, int kG, bool kQwen>
+__global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a) {
+  constexpr int kLPP = kD / 8;        // lanes per position (8 dims each)
+  constexpr int kPPW = 64 / kLPP;     // positions per wave step
+  constexpr int kPPB = 4 * kPPW;      // positions per block step
+  __shared__ float qs[kG][kD];
+  __shared__ _Float16 knew[kD], vnew[kD];
+  __shared__ float scores[kG][kMaxSplitChunk];
+  __shared__ float red[4][kG][kD];
+  __shared__ float stat[kG][2];
+  __shared__ int is_last;
+
+  const int b = blockIdx.z, kvh = blockIdx.y, s = blockIdx.x;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int L = a.pos[b] + 1;  // context including the new token
+  const int chunk = split_chunk(L, a.splits);
+  const int active = (L + chunk - 1) / chunk;
+  // the host sizes `splits` so that chunk <= kMaxSplitChunk for every L up to
+  // max_pos; a longer context (never produced) would overrun `scores`
+  if (s >= active || chunk > kMaxSplitChunk || L > a.max_pos) return;
+  const int p0 = s * chunk, p1 = min(L, p0 + chunk), np = p1 - p0;
+  const int pos = L - 1;
+  const float *qkv = a.qkv + (size_t)b * a.qkv_ld;
+  const size_t cache_base = ((size_t)b * a.kv_heads + kvh) * (size_t)a.max_pos * kD;
+  const bool holds_new = p1 == L;
+
+  // ---- q (and the new k / v) ----
+  {
+    const int g = t / kD, i = t % kD;
+    const bool q_thread = t < kG * kD;
+    float qv = q_thread ? qkv[(kvh * kG + g) * kD + i] : 0.0f;
+    float kv = 0.0f, vv = 0.0f;
+    const bool kv_thread = holds_new && t < kD;
+    if (kv_thread) {
+      kv = qkv[a.heads * kD + kvh * kD + i];
+      vv = qkv[(a.heads + a.kv_heads) * kD + kvh * kD + i];
+    }
+    if (kQwen) {
+      // RMSNorm over the head (sums through LDS), then RoPE
+      if (q_thread) red[0][g][i] = qv * qv;
+      if (kv_thread) red[1][0][i] = kv * kv;
+      __syncthreads();
+      if (q_thread) {
+        float ss = 0.0f;
+        for (int j = 0; j < kD; j++) ss += red[0][g][j];
+        qv = qv * (1.0f / sqrtf(ss / kD + a.eps)) * a.q_norm[i];
+      }
+      if (kv_thread) {
+        float ss = 0.0f;
+        for (int j = 0; j < kD; j++) ss += red[1][0][j];
+        kv = kv * (1.0f / sqrtf(ss / kD + a.eps)) * a.k_norm[i];
+      }
+      __syncthreads();
+      if (q_thread) red[2][g][i] = qv;
+      if (kv_thread) red[3][0][i] = kv;
+      __syncthreads();
+      const int half = kD / 2, fi = i % half;
+      const float ang = (float)pos * a.inv_freq[fi];
+      float sn, cs;
+      sincosf(ang, &sn, &cs);
+      if (q_thread) {
+        const float other = red[2][g][i < half ? i + half : i - half];
+        qv = i < half ? qv * cs - other * sn : qv * cs + other * sn;
+      }
+      if (kv_thread) {
+        const float other = red[3][0][i < half ? i + half : i - half];
+        kv = i < half ? kv * cs - other * sn : kv * cs + other * sn;
+      }
+    }
+    if (q_thread) qs[g][i] = qv * a.scale;
+    if (kv_thread) {
+      const _Float16 k16 = (_Float16)kv, v16 = (_Float16)vv;
+      knew[i] = k16;
+      vnew[i] = v16;
+      a.kcache[cache_base + (size_t)pos * kD + i] = __builtin_bit_cast(uint16_t, k16);
+      a.vcache[cache_base + (size_t)pos * kD + i] = __builtin_bit_cast(uint16_t, v16);
+    }
+    __syncthreads();
+  }
+
+  const int seg = lane % kLPP, sub = lane / kLPP;
+  float q8[kG][8];
+#pragma unroll
+  for (int g = 0; g < kG; g++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) q8[g][e] = qs[g][seg * 8 + e];
+
+  // ---- scores ----
+  for (int base = 0; base < np; base += kPPB) {
+    const int pi = base + wave * kPPW + sub;
+    const int p = p0 + pi;
+    f16x8 k8 = {};
+    if (pi < np) {
+      if (p == pos)
+        k8 = *reinterpret_cast<const f16x8 *>(&knew[seg * 8]);
+      else
+        k8 = *reinterpret_cast<const f16x8 *>(a.kcache + cache_base + (size_t)p * kD + seg * 8);
+    }
+#pragma unroll
+    for (int g = 0; g < kG; g++) {
+      float d = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) d += q8[g][e] * (float)k8[e];
+#pragma unroll
+      for (int off = kLPP / 2; off >= 1; off >>= 1) d += __shfl_xor(d, off, 64);
+      if (seg == 0 && pi < np) scores[g][pi] = d;
+    }
+  }
+  __syncthreads();
+
+  // ---- softmax statistics (wave g for head g) ----
+  if (wave < kG) {
+    const int g = wave;
+    float m = -INFINITY;
+    for (int i = lane; i < np; i += 64) m = fmaxf(m, scores[g][i]);
+    m = wave_max(m);
+    float l = 0.0f;
+    for (int i = lane; i < np; i += 64) {
+      const float e = expf(scores[g][i] - m);
+      scores[g][i] = e;
+      l += e;
+    }
+    l = wave_sum(l);
+    if (lane == 0) {
+      stat[g][0] = m;
+      stat[g][1] = l;
+    }
+  }
+  __syncthreads();
+
+  // ---- unnormalised V sums ----
+  float acc[kG][8];
+#pragma unroll
+  for (int g = 0; g < kG; g++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc[g][e] = 0.0f;
+  for (int base = 0; base < np; base += kPPB) {
+    const int pi = base + wave * kPPW + sub;
+    const int p = p0 + pi;
+    if (pi < np) {
+      f16x8 v8;
+      if (p == pos)
+        v8 = *reinterpret_cast<const f16x8 *>(&vnew[seg * 8]);
+      else
+        v8 = *reinterpret_cast<const f16x8 *>(a.vcache + cache_base + (size_t)p * kD + seg * 8);
+#pragma unroll
+      for (int g = 0; g < kG; g++) {
+        const float w = scores[g][pi];
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[g][e] += w * (float)v8[e];
+      }
+    }
+  }
+  // across the position groups of the wave, then across waves
+#pragma unroll
+  for (int g = 0; g < kG; g++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      float v = acc[g][e];
+#pragma unroll
+      for (int off = kLPP; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+      acc[g][e] = v;
+    }
+  if (sub == 0) {
+#pragma unroll
+    for (int g = 0; g < kG; g++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) red[wave][g][seg * 8 + e] = acc[g][e];
+  }
+  __syncthreads();
+
+  const int h0 = kvh * kG;
+  if (active == 1) {  // one split: normalise and write the head output directly
+    if (t < kG * kD) {
+      const int g = t / kD, i = t % kD;
+      const float v = red[0][g][i] + red[1][g][i] + red[2][g][i] + red[3][g][i];
+      a.out[(size_t)b * a.out_ld + (h0 + g) * kD + i] = f32_to_f16_bits(v / stat[g][1]);
+    }
+    return;
+  }
+
+  // ---- partials, then the last workgroup merges ----
+  const size_t pstride = (size_t)kD + 2;
+  if (t < kG * kD) {
+    const int g = t / kD, i = t % kD;
+    float *pp = a.part + (((size_t)b * a.heads + h0 + g) * a.splits + s) * pstride;
+    pp[i] = red[0][g][i] + red[1][g][i] + red[2][g][i] + red[3][g][i];
+    if (i == 0) {
+      pp[kD] = stat[g][0];
+      pp[kD + 1] = stat[g][1];
+    }
+  }
+  __threadfence();
+  __syncthreads();
+  if (t == 0) {
+    const int prev = atomicAdd(a.counters + b * a.kv_heads + kvh, 1);
+    is_last = prev == active - 1;
+  }
+  __syncthreads();
+  if (!is_last) return;
+  __threadfence();
+  if (t < kG * kD) {
+    const int g = t / kD, i = t % kD;
+    const float *pp = a.part + ((size_t)b * a.heads + h0 + g) * a.splits * pstride;
+    float m = -INFINITY;
+    for (int j = 0; j < active; j++) m = fmaxf(m, pp[j * pstride + kD]);
+    float l = 0.0f, v = 0.0f;
+    for (int j = 0; j < active; j++) {
+      const float w = expf(pp[j * pstride + kD] - m);
+      l += w * pp[j * pstride + kD + 1];
+      v += w * pp[j * pstride + i];
+    }
+    a.out[(size_t)b * a.out_ld + (h0 + g) * kD + i] = f32_to_f16_bits(v / l);
+  }
+  if (t == 0) a.counters[b * a.kv_heads + kvh] = 0;  // ready for the next layer
+}
+
+// ---- embedding -------------------------------------------------------------
+
+// grid (B): reads the token of row b from its argmax key (the host writes
+// prompt tokens as keys too), records it in the history, clears the key for
+// this step's LM head, advances the row's position and writes the fp32
+// residual stream: Qwen3 dequantises the tied FP8 head row, GPT-2 adds the
+// fp16 token (tied head) and position rows.
+__global__ __launch_bounds__(kThreads) void embed_kernel(const EmbedArgs a) {
+  const int b = blockIdx.x, t = threadIdx.x;
+  __shared__ int tok_s, pos_s;
+  if (t == 0) {
+    const unsigned long long key = a.keys[b];
+    int tok = (int)(0xffffffffu - (uint32_t)(key & 0xffffffffu));
+    if (tok < 0 || tok >= a.vocab) tok = 0;
+    const int pos = a.lens[b];
+    tok_s = tok;
+    pos_s = pos;
+    if (pos < a.hist_len) a.hist[(size_t)b * a.hist_len + pos] = tok;
+    a.pos[b] = pos;
+    a.lens[b] = pos + 1;
+    a.keys[b] = 0;
+  }
+  __syncthreads();
+  const int tok = tok_s, pos = pos_s;
+  float *x = a.x + (size_t)b * a.x_ld;
+  for (int k = t; k < a.K; k += kThreads) {
+    float v;
+    if (a.fp8_head) {
+      const uint8_t q = a.head8[fp8_tiled_offset(tok, k, a.K)];
+      const f16x2 h = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((uint32_t)q, 1.0f, false);
+      v = (float)h[0] * a.head_scale[tok];
+    } else {
+      v = f16_bits_to_f32(a.head16[f16_tiled_offset(tok, k, a.K)]);
+      if (a.wpe) v += f16_bits_to_f32(a.wpe[(size_t)min(pos, a.max_pos - 1) * a.K + k]);
+    }
+    x[k] = v;
+  }
+}
+
+template <int kW, int kPro, int kEpi>
+hipError_t launch_gemv_t(hipStream_t s, const GemvArgs &a, int grid) {
+  const size_t lds = (size_t)a.B * (a.K + 8) * 2 + 4 * 2 * 64 * 4 * sizeof(float);
+  gemv_kernel<kW, kPro, kEpi><<<grid, kThreads, lds, s>>>(a);
+  return hipGetLastError();
+}
+
+template <int kW, int kPro, int kEpi>
+hipError_t allow_large_lds() {
+  return hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_kernel<kW, kPro, kEpi>),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+}
+
+template <int kW, int kPro>
+hipError_t allow_large_lds_pro() {
+  hipError_t e;
+  if ((e = allow_large_lds<kW, kPro, kEpiStore>()) != hipSuccess) return e;
+  if ((e = allow_large_lds<kW, kPro, kEpiResidual>()) != hipSuccess) return e;
+  if ((e = allow_large_lds<kW, kPro, kEpiSwiGLU>()) != hipSuccess) return e;
+  if ((e = allow_large_lds<kW, kPro, kEpiGelu>()) != hipSuccess) return e;
+  return allow_large_lds<kW, kPro, kEpiLogits>();
+}
+
+template <int kW, int kPro>
+hipError_t launch_gemv_epi(hipStream_t s, const GemvArgs &a, int epi, int grid) {
+  switch (epi) {
+    case kEpiStore: return launch_gemv_t<kW, kPro, kEpiStore>(s, a, grid);
+    case kEpiResidual: return launch_gemv_t<kW, kPro, kEpiResidual>(s, a, grid);
+    case kEpiSwiGLU: return launch_gemv_t<kW, kPro, kEpiSwiGLU>(s, a, grid);
+    case kEpiGelu: return launch_gemv_t<kW, kPro, kEpiGelu>(s, a, grid);
+    default: return launch_gemv_t<kW, kPro, kEpiLogits>(s, a, grid);
+  }
+}
+
+template <int kW>
+hipError_t launch_gemv_pro(hipStream_t s, const GemvArgs &a, int pro, int epi, int grid) {
+  switch (pro) {
+    case kProNone: return launch_gemv_epi<kW, kProNone>(s, a, epi, grid);
+    case kProRms: return launch_gemv_epi<kW, kProRms>(s, a, epi, grid);
+    default: return launch_gemv_epi<kW, kProLayer>(s, a, epi, grid);
+  }
+}
+
+unsigned blocks_for(size_t n) { return (unsigned)((n + kThreads - 1) / kThreads); }
+
+}  // namespace
+
+hipError_t launch_gemv(hipStream_t s, const GemvArgs &a, int weight_type, int pro, int epi,
+                       int max_grid) {
+  const int groups = a.N / (16 * (epi == kEpiSwiGLU ? 2 : 1));
+  const int grid = max_grid > 0 && groups > max_grid ? max_grid : groups;
+  if (weight_type == kWeightFp8) return launch_gemv_pro<kWeightFp8>(s, a, pro, epi, grid);
+  return launch_gemv_pro<kWeightFp16>(s, a, pro, epi, grid);
+}
+
+hipError_t prepare_gemv_kernels() {
+  hipError_t e;
+  if ((e = allow_large_lds_pro<kWeightFp8, kProNone>()) != hipSuccess) return e;
+  if ((e = allow_large_lds_pro<kWeightFp8, kProRms>()) != hipSuccess) return e;
+  if ((e = allow_large_lds_pro<kWeightFp8, kProLayer>()) != hipSuccess) return e;
+  if ((e = allow_large_lds_pro<kWeightFp16, kProNone>()) != hipSuccess) return e;
+  if ((e = allow_large_lds_pro<kWeightFp16, kProRms>()) != hipSuccess) return e;
+  return allow_large_lds_pro<kWeightFp16, kProLayer>();
+}
+
+hipError_t launch_attention(hipStream_t s, const AttnArgs &a, int head_dim, int group, bool qwen,
+                            int batch) {
+  dim3 grid(a.splits, a.kv_heads, batch);
+  if (head_dim == 128 && group == 2 && qwen)
+    attn_decode_kernel<128, 2, true><<<grid, kThreads, 0, s>>>(a);
+  else if (head_dim == 128 && group == 1 && qwen)
+    attn_decode_kernel<128, 1, true><<<grid, kThreads, 0, s>>>(a);
+  else if (head_dim == 64 && group == 1 && !qwen)
+    attn_decode_kernel<64, 1, false><<<grid, kThreads, 0, s>>>(a);
+  else if (head_dim == 128 && group == 1 && !qwen)
+    attn_decode_kernel<128, 1, false><<<grid, kThreads, 0, s>>>(a);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_embed(hipStream_t s, const EmbedArgs &a, int batch) {
+  embed_kernel<<<batch, kThreads, 0, s>>>(a);
+  return hipGetLastError();
+}
+
+hipError_t launch_quantize_e4m3_tiled(hipStream_t s, const float *w, int N, int K,
+                                      int interleave_rows, uint8_t *q, float *scales,
+                                      bool tiled) {
+  quantize_e4m3_kernel<<<(N + 3) / 4, kThreads, 0, s>>>(w, N, K, interleave_rows, q, scales,
+                                                        tiled ? 1 : 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_e4m3_tiles(hipStream_t s, const uint8_t *q, int N, int K, uint8_t *out) {
+  if ((size_t)N * K) pack_e4m3_tiles_kernel<<<blocks_for((size_t)N * K), kThreads, 0, s>>>(q, N, K, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_tile_f16(hipStream_t s, const float *w, int N, int K, int interleave_rows,
+                           uint16_t *out) {
+  tile_f16_kernel<<<blocks_for((size_t)N * K), kThreads, 0, s>>>(w, N, K, interleave_rows, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_normal(hipStream_t s, float *out, size_t n, uint64_t seed, float mean,
+                              float stddev) {
+  if (n) fill_normal_kernel<<<blocks_for(n), kThreads, 0, s>>>(out, n, seed, mean, stddev);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_value(hipStream_t s, float *out, size_t n, float v) {
+  if (n) fill_f32_kernel<<<blocks_for(n), kThreads, 0, s>>>(out, n, v);
+  return hipGetLastError();
+}
+
+hipError_t launch_f32_to_f16(hipStream_t s, const float *in, uint16_t *out, size_t n) {
+  if (n) f32_to_f16_kernel<<<blocks_for(n), kThreads, 0, s>>>(in, out, n);
+  return hipGetLastError();
+}
+
+}  // namespace sh
