@@ -36,6 +36,7 @@ struct GemvArgs {
   uint16_t *out16 = nullptr; // fp16 output rows (SwiGLU, GELU)
   int out_ld = 0;
   unsigned long long *argmax = nullptr;  // logits: per-row argmax keys (atomicMax)
+  int split_k = 1;  // set by launch_gemv: 4 waves split K (1) or one wave per tile (0)
 };
 
 struct AttnArgs {
@@ -46,7 +47,7 @@ struct AttnArgs {
   const int *pos = nullptr;  // [B] position of the new token (= tokens already cached)
   const float *q_norm = nullptr, *k_norm = nullptr;  // Qwen3 per-head RMSNorm gains [d]
   float eps = 0.0f;
-  const float *inv_freq = nullptr;  // Qwen3 RoPE inverse frequencies [d/2]
+  const float *rope = nullptr;      // Qwen3 RoPE of this step: [B][2][d/2] (cos, sin)
   float scale = 1.0f;               // 1 / sqrt(d)
   int heads = 0, kv_heads = 0;
   int splits = 1;                   // grid.x
@@ -69,6 +70,9 @@ struct EmbedArgs {
   const float *head_scale = nullptr;
   const uint16_t *head16 = nullptr;    // fp16 tiled head (GPT-2, tied wte)
   const uint16_t *wpe = nullptr;       // GPT-2 positions [max_pos][K] fp16
+  const float *inv_freq = nullptr;     // Qwen3 RoPE inverse frequencies [half]
+  float *rope = nullptr;               // [B][2][half]: cos, sin of pos * inv_freq
+  int half = 0;
 };
 
 // Lets every GEMV instantiation use up to 160 KiB of dynamic LDS (current device).

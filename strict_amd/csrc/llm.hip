@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -36,8 +37,12 @@ struct Layer {
   uint16_t *kcache = nullptr, *vcache = nullptr;
 };
 
+// Splits of the context per (sequence, KV head): about 256 workgroups in all
+// (one per CU; at the Qwen3 shape and b = 1 that is 128 positions per
+// workgroup, one batch of K loads per thread), at least enough that no split
+// exceeds kMaxSplitChunk positions, at most 64 (the merge kernel's limit).
 int attention_splits(int batch, int kv_heads, int max_pos) {
-  int s = 1024 / (batch * kv_heads);
+  int s = 256 / (batch * kv_heads);
   if (s > 64) s = 64;
   const int min_s = (max_pos + kMaxSplitChunk - 1) / kMaxSplitChunk;
   if (s < min_s) s = min_s;
@@ -59,7 +64,7 @@ struct sh_llm {
   uint16_t *wpe = nullptr;
   float *inv_freq = nullptr;
   // per-step state
-  float *x = nullptr, *qkv = nullptr, *logits = nullptr, *part = nullptr;
+  float *x = nullptr, *qkv = nullptr, *logits = nullptr, *part = nullptr, *rope = nullptr;
   uint16_t *attn = nullptr, *act = nullptr;
   int *counters = nullptr, *lens = nullptr, *pos = nullptr, *hist = nullptr;
   unsigned long long *keys = nullptr;
@@ -67,6 +72,7 @@ struct sh_llm {
   size_t kv_layer_elems = 0;
   hipGraphExec_t graph[2] = {nullptr, nullptr};
   int graph_batch[2] = {-1, -1};
+  bool use_graphs = true;  // STRICT_HIP_LLM_GRAPHS=0: enqueue every step eagerly
 };
 
 namespace {
@@ -151,6 +157,9 @@ int enqueue_step(sh_llm *m, bool logits) {
   e.head_scale = m->head.scale;
   e.head16 = reinterpret_cast<const uint16_t *>(m->head.w);
   e.wpe = m->wpe;
+  e.inv_freq = m->inv_freq;
+  e.rope = m->rope;
+  e.half = d / 2;
   SH_HIP_TRY(launch_embed(s, e, B));
 
   for (Layer &L : m->layers) {
@@ -180,7 +189,7 @@ int enqueue_step(sh_llm *m, bool logits) {
     a.q_norm = L.q_norm;
     a.k_norm = L.k_norm;
     a.eps = c.norm_eps;
-    a.inv_freq = m->inv_freq;
+    a.rope = m->rope;
     a.scale = 1.0f / std::sqrt((float)d);
     a.heads = c.heads;
     a.kv_heads = c.kv_heads;
@@ -250,7 +259,7 @@ int enqueue_step(sh_llm *m, bool logits) {
     h.out = m->logits;
     h.out_ld = m->vocab_pad;
     h.argmax = m->keys;
-    SH_HIP_TRY(launch_gemv(s, h, m->wtype, pro, kEpiLogits, 1024));
+    SH_HIP_TRY(launch_gemv(s, h, m->wtype, pro, kEpiLogits, 2048));
   }
   return SH_OK;
 }
@@ -366,6 +375,10 @@ SH_API int sh_llm_create(sh_ctx *ctx, const sh_llm_config *config, sh_llm **out)
   m->qwen = qwen;
   m->wtype = qwen ? kWeightFp8 : kWeightFp16;
   m->qkv_n = (c.heads + 2 * c.kv_heads) * c.head_dim;
+  {
+    const char *g = getenv("STRICT_HIP_LLM_GRAPHS");
+    m->use_graphs = !(g && g[0] == '0');
+  }
   m->vocab_pad = (c.vocab + 15) / 16 * 16;
   const int B = c.max_batch, H = c.hidden, d = c.head_dim;
   m->kv_layer_elems = (size_t)B * c.kv_heads * c.max_positions * d;
@@ -404,6 +417,7 @@ SH_API int sh_llm_create(sh_ctx *ctx, const sh_llm_config *config, sh_llm **out)
     return cleanup(rc);
   if (qwen) {
     if ((rc = alloc_n(m, d / 2, &m->inv_freq))) return cleanup(rc);
+    if ((rc = alloc_n(m, (size_t)B * d, &m->rope))) return cleanup(rc);
     std::vector<float> f(d / 2);
     for (int i = 0; i < d / 2; i++)
       f[i] = (float)std::pow((double)c.rope_theta, -2.0 * i / (double)d);
@@ -588,7 +602,9 @@ SH_API int sh_llm_step(sh_llm *m, const int32_t *tokens, int want_logits) {
     SH_HIP_TRY(hipStreamSynchronize(s));  // `keys` is a stack array
   }
   const int g = want_logits ? 1 : 0;
-  if (m->graph_batch[g] != m->batch) {
+  if (!m->use_graphs) {
+    if ((rc = enqueue_step(m, want_logits != 0)) != SH_OK) return rc;
+  } else if (m->graph_batch[g] != m->batch) {
     if (m->graph[g]) (void)hipGraphExecDestroy(m->graph[g]);
     m->graph[g] = nullptr;
     m->graph_batch[g] = -1;

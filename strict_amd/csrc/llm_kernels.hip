@@ -184,61 +184,100 @@ __device__ __forceinline__ float wave_max(float v) {
 // Stages the MFMA A operand (activations of B rows, fp16, row stride K + 8
 // elements so that the 16 rows of a 16-lane LDS phase fall in 16 distinct
 // bank groups) from fp16 activations or from the fp32 residual stream after
-// RMSNorm / LayerNorm.
+// RMSNorm / LayerNorm. Split in two so that the caller can issue its weight
+// loads in between: issue() starts the first kStage 16-byte loads of this
+// thread (activation rows, then gamma / beta), finish() stores them to LDS,
+// loads any remainder, and for the norms takes the statistics (one wave per
+// row) from an fp32 copy of the rows in LDS (`xf`, gamma / beta after it).
+constexpr int kStage = 4;
+
 template <int kPro>
-__device__ void stage_activations(const GemvArgs &a, _Float16 *xs, float *red) {
-  const int K = a.K, B = a.B, stride = K + 8;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  if (kPro == kProNone) {
-    const int chunks = K / 8;
-    for (int i = t; i < B * chunks; i += kThreads) {
-      const int b = i / chunks, c = i - b * chunks;
-      const u32x4 v = *reinterpret_cast<const u32x4 *>(a.act + (size_t)b * a.act_ld + c * 8);
-      *reinterpret_cast<u32x4 *>(xs + b * stride + c * 8) = v;
+struct Stager {
+  u32x4 v[kStage];
+  int total = 0, c4 = 0, rows4 = 0;
+
+  __device__ __forceinline__ u32x4 load_item(const GemvArgs &a, int i) const {
+    if (kPro == kProNone) {
+      const int chunks = a.K / 8, b = i / chunks, c = i - b * chunks;
+      return *reinterpret_cast<const u32x4 *>(a.act + (size_t)b * a.act_ld + c * 8);
     }
-    __syncthreads();
-    return;
+    if (i < rows4) {
+      const int b = i / c4, c = i - b * c4;
+      return *reinterpret_cast<const u32x4 *>(a.x + (size_t)b * a.x_ld + c * 4);
+    }
+    if (i < rows4 + c4) return *reinterpret_cast<const u32x4 *>(a.gamma + (i - rows4) * 4);
+    return *reinterpret_cast<const u32x4 *>(a.beta + (i - rows4 - c4) * 4);
   }
-  // statistics per row b (LayerNorm mean, then sum of squared deviations);
-  // red[0..3] is the cross-wave scratch, red[8 + b] / red[8 + kMaxBatch + b]
-  // hold mean / 1 / sqrt(var + eps) of row b
-  for (int b = 0; b < B; b++) {
-    const float *x = a.x + (size_t)b * a.x_ld;
-    float mean = 0.0f;
-    if (kPro == kProLayer) {
-      float s = 0.0f;
-      for (int k = t; k < K; k += kThreads) s += x[k];
-      s = wave_sum(s);
-      if (lane == 0) red[wave] = s;
-      __syncthreads();
-      mean = (red[0] + red[1] + red[2] + red[3]) / (float)K;
-      __syncthreads();
+
+  __device__ __forceinline__ void store_item(const GemvArgs &a, int i, u32x4 val, _Float16 *xs,
+                                             float *xf) const {
+    if (kPro == kProNone) {
+      const int chunks = a.K / 8, b = i / chunks, c = i - b * chunks;
+      *reinterpret_cast<u32x4 *>(xs + b * (a.K + 8) + c * 8) = val;
+    } else {
+      *reinterpret_cast<u32x4 *>(xf + (size_t)i * 4) = val;
     }
-    float ss = 0.0f;
-    for (int k = t; k < K; k += kThreads) {
-      const float d = x[k] - mean;
-      ss += d * d;
-    }
-    ss = wave_sum(ss);
-    if (lane == 0) red[wave] = ss;
-    __syncthreads();
-    if (t == 0) {
-      red[8 + b] = mean;
-      red[8 + kMaxBatch + b] = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + a.eps);
-    }
-    __syncthreads();
   }
-  for (int b = 0; b < B; b++) {
-    const float *x = a.x + (size_t)b * a.x_ld;
-    const float mean = red[8 + b], inv = red[8 + kMaxBatch + b];
-    for (int k = t; k < K; k += kThreads) {
-      float y = (x[k] - mean) * inv * a.gamma[k];
-      if (kPro == kProLayer) y += a.beta[k];
+
+  __device__ __forceinline__ void issue(const GemvArgs &a) {
+    const int t = threadIdx.x;
+    if (kPro == kProNone) {
+      total = a.B * (a.K / 8);
+    } else {
+      c4 = a.K / 4;
+      rows4 = a.B * c4;
+      total = rows4 + (kPro == kProLayer ? 2 : 1) * c4;
+    }
+#pragma unroll
+    for (int u = 0; u < kStage; u++) {
+      const int i = u * kThreads + t;
+      if (i < total) v[u] = load_item(a, i);
+    }
+  }
+
+  __device__ void finish(const GemvArgs &a, _Float16 *xs, float *red, float *xf) {
+    const int K = a.K, B = a.B, stride = K + 8;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+#pragma unroll
+    for (int u = 0; u < kStage; u++) {
+      const int i = u * kThreads + t;
+      if (i < total) store_item(a, i, v[u], xs, xf);
+    }
+    for (int i = kStage * kThreads + t; i < total; i += kThreads) store_item(a, i, load_item(a, i), xs, xf);
+    __syncthreads();
+    if (kPro == kProNone) return;
+    const float *gs = xf + (size_t)B * K, *bs = gs + K;
+    // statistics: wave w handles rows w, w + 4, ...; red[8 + b] = mean,
+    // red[8 + kMaxBatch + b] = 1 / sqrt(var + eps)
+    for (int b = wave; b < B; b += 4) {
+      const float *row = xf + (size_t)b * K;
+      float mean = 0.0f;
+      if (kPro == kProLayer) {
+        float sm = 0.0f;
+        for (int k = lane; k < K; k += 64) sm += row[k];
+        mean = wave_sum(sm) / (float)K;
+      }
+      float ss = 0.0f;
+      for (int k = lane; k < K; k += 64) {
+        const float d = row[k] - mean;
+        ss += d * d;
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) {
+        red[8 + b] = mean;
+        red[8 + kMaxBatch + b] = 1.0f / sqrtf(ss / (float)K + a.eps);
+      }
+    }
+    __syncthreads();
+    for (int i = t; i < B * K; i += kThreads) {
+      const int b = i / K, k = i - b * K;
+      float y = (xf[i] - red[8 + b]) * red[8 + kMaxBatch + b] * gs[k];
+      if (kPro == kProLayer) y += bs[k];
       xs[b * stride + k] = (_Float16)y;
     }
+    __syncthreads();
   }
-  __syncthreads();
-}
+};
 
 __device__ __forceinline__ float gelu_tanh(float x) {
   const float c = 0.7978845608028654f;  // sqrt(2 / pi)
@@ -255,124 +294,164 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int n) {
   return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)n);
 }
 
-// One workgroup handles kNT row tiles (two for the gate/up pair) at a time,
-// grid-striding over the tile groups. Its 4 waves split K in four; the four
-// partial 16x16 accumulators are summed in LDS and wave 0 runs the epilogue.
+// Two work splits, chosen by the host (GemvArgs::split_k):
+//  - split-K (few row tiles): a workgroup handles kNT row tiles (two for the
+//    gate/up pair) at a time, grid-striding over tile groups; its 4 waves
+//    split K in four and the partial 16x16 accumulators are summed in LDS,
+//    wave 0 running the epilogue;
+//  - wave-per-tile (many row tiles, e.g. the LM head): every wave owns whole
+//    tile groups over all of K and runs its own epilogue, no LDS reduction or
+//    barrier in the loop.
+// The first batch of weight loads is issued before the activation prologue
+// (the weights do not depend on it), so the two memory round trips overlap.
 template <int kW, int kPro, int kEpi>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   constexpr int kNT = kEpi == kEpiSwiGLU ? 2 : 1;
   constexpr int kKPerLoad = kW == kWeightFp8 ? 64 : 32;
+  constexpr int kU = 16 / kNT;  // 16-byte weight loads per lane in flight
   const int K = a.K, B = a.B;
   const int stride = K + 8;
   _Float16 *xs = reinterpret_cast<_Float16 *>(smem);
-  float *red = reinterpret_cast<float *>(smem + (size_t)B * stride * 2);  // 4*kNT*64*4 floats
+  float *red = reinterpret_cast<float *>(smem + (size_t)B * stride * 2);  // 4*2*64*4 floats
+  float *xf = red + 4 * 2 * 64 * 4;  // norm prologue: fp32 rows, gamma, beta
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  stage_activations<kPro>(a, xs, red);
-
-  const int loads_per_row = K / kKPerLoad;      // 16-byte lane loads per tile row group
-  const int per_wave = loads_per_row / 4;       // K split over the 4 waves
+  const bool split = a.split_k != 0;
+  const int loads_per_row = K / kKPerLoad;  // 16-byte lane loads per tile row group
+  const int per_wave = split ? loads_per_row / 4 : loads_per_row;
+  const int c0 = split ? wave * per_wave : 0;
   const int groups = a.N / (16 * kNT);
+  const int g_first = split ? blockIdx.x : blockIdx.x * 4 + wave;
+  const int g_step = split ? gridDim.x : gridDim.x * 4;
   const int arow = lane & 15, acol = 8 * (lane >> 4);
   const bool arow_valid = arow < B;
 
-  unsigned long long best[4] = {0, 0, 0, 0};  // logits: running argmax keys per b row
-
-  for (int g = blockIdx.x; g < groups; g += gridDim.x) {
-    f32x4 acc[kNT];
+  u32x4 wv[kU][kNT];
+  auto load_batch = [&](int g, int c) {
 #pragma unroll
-    for (int j = 0; j < kNT; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int c0 = wave * per_wave;
-    for (int c = c0; c < c0 + per_wave; c += 4) {
-      u32x4 wv[4][kNT];
-#pragma unroll
-      for (int u = 0; u < 4; u++)
-#pragma unroll
-        for (int j = 0; j < kNT; j++) {
-          const size_t tile = (size_t)(g * kNT + j) * loads_per_row + (c + u);
-          if (c + u < c0 + per_wave)
-            wv[u][j] = __builtin_nontemporal_load(
-                reinterpret_cast<const u32x4 *>(a.w + tile * 1024 + (size_t)lane * 16));
-        }
-#pragma unroll
-      for (int u = 0; u < 4; u++) {
-        if (c + u >= c0 + per_wave) break;
-        const int kbase = (c + u) * kKPerLoad;
-#pragma unroll
-        for (int h = 0; h < kKPerLoad / 32; h++) {
-          f16x8 af = {};
-          if (arow_valid)
-            af = *reinterpret_cast<const f16x8 *>(xs + arow * stride + kbase + 32 * h + acol);
-#pragma unroll
-          for (int j = 0; j < kNT; j++) {
-            f16x8 bf;
-            if (kW == kWeightFp8) {
-              const uint32_t d0 = wv[u][j][2 * h], d1 = wv[u][j][2 * h + 1];
-              const f16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, false);
-              const f16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, true);
-              const f16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, false);
-              const f16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, true);
-              bf = f16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-            } else {
-              bf = __builtin_bit_cast(f16x8, wv[u][j]);
-            }
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[j], 0, 0, 0);
-          }
-        }
-      }
-    }
-    // ---- sum the four K quarters ----
-#pragma unroll
-    for (int j = 0; j < kNT; j++)
-      *reinterpret_cast<f32x4 *>(red + ((wave * kNT + j) * 64 + lane) * 4) = acc[j];
-    __syncthreads();
-    if (wave == 0) {
-      f32x4 y[kNT];
+    for (int u = 0; u < kU; u++)
 #pragma unroll
       for (int j = 0; j < kNT; j++) {
-        y[j] = *reinterpret_cast<const f32x4 *>(red + ((0 * kNT + j) * 64 + lane) * 4);
-#pragma unroll
-        for (int w = 1; w < 4; w++) y[j] += *reinterpret_cast<const f32x4 *>(red + ((w * kNT + j) * 64 + lane) * 4);
+        const size_t tile = (size_t)(g * kNT + j) * loads_per_row + (c + u);
+        if (c + u < c0 + per_wave)
+          wv[u][j] = __builtin_nontemporal_load(
+              reinterpret_cast<const u32x4 *>(a.w + tile * 1024 + (size_t)lane * 16));
       }
-      // lane holds column n = tile row (lane % 16) for batch rows 4*(lane/16) + r
-      const int col = lane & 15;
+  };
+  auto mul_batch = [&](int c, f32x4 (&acc)[kNT]) {
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int b = 4 * (lane >> 4) + r;
-        if (b >= B) continue;
-        if (kEpi == kEpiSwiGLU) {
-          const int ng = (g * 2) * 16 + col, nu = ng + 16;  // tiled rows of gate / up
-          float gv = y[0][r], uv = y[kNT - 1][r];
-          if (a.scale) { gv *= a.scale[ng]; uv *= a.scale[nu]; }
-          if (a.bias) { gv += a.bias[ng]; uv += a.bias[nu]; }
-          const int n = g * 16 + col;  // output column
-          a.out16[(size_t)b * a.out_ld + n] = f32_to_f16_bits(silu(gv) * uv);
-        } else {
-          const int n = g * 16 + col;
-          float v = y[0][r];
-          if (a.scale) v *= a.scale[n];
-          if (a.bias) v += a.bias[n];
-          if (kEpi == kEpiStore) {
+    for (int u = 0; u < kU; u++) {
+      if (c + u >= c0 + per_wave) break;
+      const int kbase = (c + u) * kKPerLoad;
+#pragma unroll
+      for (int h = 0; h < kKPerLoad / 32; h++) {
+        f16x8 af = {};
+        if (arow_valid)
+          af = *reinterpret_cast<const f16x8 *>(xs + arow * stride + kbase + 32 * h + acol);
+#pragma unroll
+        for (int j = 0; j < kNT; j++) {
+          f16x8 bf;
+          if (kW == kWeightFp8) {
+            const uint32_t d0 = wv[u][j][2 * h], d1 = wv[u][j][2 * h + 1];
+            const f16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, false);
+            const f16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, true);
+            const f16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, false);
+            const f16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, true);
+            bf = f16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+          } else {
+            bf = __builtin_bit_cast(f16x8, wv[u][j]);
+          }
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[j], 0, 0, 0);
+        }
+      }
+    }
+  };
+
+  unsigned long long best[4] = {0, 0, 0, 0};  // logits: running argmax keys per b row
+  // lane holds column n = tile row (lane % 16) for batch rows 4*(lane/16) + r
+  auto epilogue = [&](int g, const f32x4 (&y)[kNT]) {
+    const int col = lane & 15;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int b = 4 * (lane >> 4) + r;
+      if (b >= B) continue;
+      if (kEpi == kEpiSwiGLU) {
+        const int ng = (g * 2) * 16 + col, nu = ng + 16;  // tiled rows of gate / up
+        float gv = y[0][r], uv = y[kNT - 1][r];
+        if (a.scale) { gv *= a.scale[ng]; uv *= a.scale[nu]; }
+        if (a.bias) { gv += a.bias[ng]; uv += a.bias[nu]; }
+        const int n = g * 16 + col;  // output column
+        a.out16[(size_t)b * a.out_ld + n] = f32_to_f16_bits(silu(gv) * uv);
+      } else {
+        const int n = g * 16 + col;
+        float v = y[0][r];
+        if (a.scale) v *= a.scale[n];
+        if (a.bias) v += a.bias[n];
+        if (kEpi == kEpiStore) {
+          a.out[(size_t)b * a.out_ld + n] = v;
+        } else if (kEpi == kEpiResidual) {
+          a.out[(size_t)b * a.out_ld + n] += v;
+        } else if (kEpi == kEpiGelu) {
+          a.out16[(size_t)b * a.out_ld + n] = f32_to_f16_bits(gelu_tanh(v));
+        } else {  // logits
+          if (n < a.n_valid) {
             a.out[(size_t)b * a.out_ld + n] = v;
-          } else if (kEpi == kEpiResidual) {
-            a.out[(size_t)b * a.out_ld + n] += v;
-          } else if (kEpi == kEpiGelu) {
-            a.out16[(size_t)b * a.out_ld + n] = f32_to_f16_bits(gelu_tanh(v));
-          } else {  // logits
-            if (n < a.n_valid) {
-              a.out[(size_t)b * a.out_ld + n] = v;
-              const unsigned long long key = argmax_key(v, n);
-              best[r] = key > best[r] ? key : best[r];
-            }
+            const unsigned long long key = argmax_key(v, n);
+            best[r] = key > best[r] ? key : best[r];
           }
         }
       }
     }
-    __syncthreads();
+  };
+
+  // activation loads, then the first weight batch (independent of them),
+  // then the prologue: waiting on the activations does not wait on weights
+  Stager<kPro> stager;
+  stager.issue(a);
+  if (g_first < groups) load_batch(g_first, c0);
+  stager.finish(a, xs, red, xf);
+
+  if (split) {
+    for (int g = g_first; g < groups; g += g_step) {
+      f32x4 acc[kNT];
+#pragma unroll
+      for (int j = 0; j < kNT; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int c = c0; c < c0 + per_wave; c += kU) {
+        if (g != g_first || c != c0) load_batch(g, c);
+        mul_batch(c, acc);
+      }
+#pragma unroll
+      for (int j = 0; j < kNT; j++)
+        *reinterpret_cast<f32x4 *>(red + ((wave * kNT + j) * 64 + lane) * 4) = acc[j];
+      __syncthreads();
+      if (wave == 0) {
+        f32x4 y[kNT];
+#pragma unroll
+        for (int j = 0; j < kNT; j++) {
+          y[j] = *reinterpret_cast<const f32x4 *>(red + (j * 64 + lane) * 4);
+#pragma unroll
+          for (int w = 1; w < 4; w++)
+            y[j] += *reinterpret_cast<const f32x4 *>(red + ((w * kNT + j) * 64 + lane) * 4);
+        }
+        epilogue(g, y);
+      }
+      __syncthreads();
+    }
+  } else {
+    for (int g = g_first; g < groups; g += g_step) {
+      f32x4 acc[kNT];
+#pragma unroll
+      for (int j = 0; j < kNT; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < per_wave; c += kU) {
+        if (g != g_first || c != 0) load_batch(g, c);
+        mul_batch(c, acc);
+      }
+      epilogue(g, acc);
+    }
   }
 
-  if (kEpi == kEpiLogits && wave == 0) {
+  if (kEpi == kEpiLogits && (!split || wave == 0)) {
     // reduce the running keys over the 16 columns held by each lane group
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -404,17 +483,23 @@ __device__ __forceinline__ int split_chunk(int L, int splits) {
 // splits. Qwen3 (kQwen): q and the new k get RMSNorm over the head and RoPE
 // (rotate-half) at position L-1 here; the workgroup whose split holds L-1
 // also appends the new k / v to the cache.
+//
+// Lane layout: kLPP = d/8 lanes per position, each holding 8 dims (16 bytes
+// of fp16 K or V); a wave covers kPPW positions per load. Every K (then V)
+// load of a thread for up to kBatch positions is issued before any is used.
 template <int kD, int kG, bool kQwen>
 __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a) {
   constexpr int kLPP = kD / 8;        // lanes per position (8 dims each)
   constexpr int kPPW = 64 / kLPP;     // positions per wave step
   constexpr int kPPB = 4 * kPPW;      // positions per block step
+  constexpr int kBatch = 8;           // block steps whose loads are in flight together
+  constexpr int kMaxSplits = 64;
   __shared__ float qs[kG][kD];
   __shared__ _Float16 knew[kD], vnew[kD];
   __shared__ float scores[kG][kMaxSplitChunk];
   __shared__ float red[4][kG][kD];
+  __shared__ float wsum[8];
   __shared__ float stat[kG][2];
-  __shared__ int is_last;
 
   const int b = blockIdx.z, kvh = blockIdx.y, s = blockIdx.x;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -422,94 +507,135 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
   const int chunk = split_chunk(L, a.splits);
   const int active = (L + chunk - 1) / chunk;
   // the host sizes `splits` so that chunk <= kMaxSplitChunk for every L up to
-  // max_pos; a longer context (never produced) would overrun `scores`
-  if (s >= active || chunk > kMaxSplitChunk || L > a.max_pos) return;
+  // max_pos (and splits <= kMaxSplits); anything else would overrun LDS
+  if (s >= active || chunk > kMaxSplitChunk || L > a.max_pos || a.splits > kMaxSplits) return;
   const int p0 = s * chunk, p1 = min(L, p0 + chunk), np = p1 - p0;
   const int pos = L - 1;
   const float *qkv = a.qkv + (size_t)b * a.qkv_ld;
   const size_t cache_base = ((size_t)b * a.kv_heads + kvh) * (size_t)a.max_pos * kD;
   const bool holds_new = p1 == L;
+  const int seg = lane % kLPP, sub = lane / kLPP;
+  const uint16_t *kbase = a.kcache + cache_base + seg * 8;
+  const uint16_t *vbase = a.vcache + cache_base + seg * 8;
+
+  // Small loads first (q, the new k / v, norm gains, RoPE of this step), then
+  // K and V of the first kBatch block steps, which do not depend on q: the
+  // q prologue then runs while K / V are in flight (vector-memory counters
+  // retire in issue order, so consuming q waits only for what precedes it).
+  const int gq = t / kD, iq = t % kD;
+  const bool q_thread = t < kG * kD;
+  const bool kv_thread = holds_new && t < kD;
+  const int half = kD / 2, fi = iq % half;
+  float qv = q_thread ? qkv[(kvh * kG + gq) * kD + iq] : 0.0f;
+  float kv = kv_thread ? qkv[a.heads * kD + kvh * kD + iq] : 0.0f;
+  const float vv = kv_thread ? qkv[(a.heads + a.kv_heads) * kD + kvh * kD + iq] : 0.0f;
+  float qn = 1.0f, kn = 1.0f, cs = 1.0f, sn = 0.0f;
+  if (kQwen) {
+    qn = q_thread ? a.q_norm[iq] : 1.0f;
+    kn = kv_thread ? a.k_norm[iq] : 1.0f;
+    cs = a.rope[(size_t)b * kD + fi];
+    sn = a.rope[(size_t)b * kD + half + fi];
+  }
+  f16x8 k8[kBatch], v8[kBatch];
+#pragma unroll
+  for (int u = 0; u < kBatch; u++) {
+    const int pi = u * kPPB + wave * kPPW + sub;
+    const int p = p0 + pi;
+    k8[u] = f16x8{};
+    v8[u] = f16x8{};
+    if (pi < np && p != pos) {
+      k8[u] = *reinterpret_cast<const f16x8 *>(kbase + (size_t)p * kD);
+      v8[u] = *reinterpret_cast<const f16x8 *>(vbase + (size_t)p * kD);
+    }
+  }
 
   // ---- q (and the new k / v) ----
   {
-    const int g = t / kD, i = t % kD;
-    const bool q_thread = t < kG * kD;
-    float qv = q_thread ? qkv[(kvh * kG + g) * kD + i] : 0.0f;
-    float kv = 0.0f, vv = 0.0f;
-    const bool kv_thread = holds_new && t < kD;
-    if (kv_thread) {
-      kv = qkv[a.heads * kD + kvh * kD + i];
-      vv = qkv[(a.heads + a.kv_heads) * kD + kvh * kD + i];
-    }
     if (kQwen) {
-      // RMSNorm over the head (sums through LDS), then RoPE
-      if (q_thread) red[0][g][i] = qv * qv;
-      if (kv_thread) red[1][0][i] = kv * kv;
+      // RMSNorm over each head: wave sums, then the kD / 64 waves of a head
+      // combined through LDS (q heads use waves 0..; k uses the first kD/64)
+      constexpr int kWavesPerHead = kD / 64;
+      const float qss = wave_sum(qv * qv);
+      const float kss = wave_sum(kv * kv);
+      if (lane == 0) {
+        wsum[wave] = qss;
+        wsum[4 + wave] = kss;
+      }
       __syncthreads();
       if (q_thread) {
         float ss = 0.0f;
-        for (int j = 0; j < kD; j++) ss += red[0][g][j];
-        qv = qv * (1.0f / sqrtf(ss / kD + a.eps)) * a.q_norm[i];
+#pragma unroll
+        for (int w = 0; w < kWavesPerHead; w++) ss += wsum[gq * kWavesPerHead + w];
+        qv = qv * (1.0f / sqrtf(ss / kD + a.eps)) * qn;
       }
       if (kv_thread) {
         float ss = 0.0f;
-        for (int j = 0; j < kD; j++) ss += red[1][0][j];
-        kv = kv * (1.0f / sqrtf(ss / kD + a.eps)) * a.k_norm[i];
+#pragma unroll
+        for (int w = 0; w < kWavesPerHead; w++) ss += wsum[4 + w];
+        kv = kv * (1.0f / sqrtf(ss / kD + a.eps)) * kn;
       }
+      if (q_thread) red[2][gq][iq] = qv;
+      if (kv_thread) red[3][0][iq] = kv;
       __syncthreads();
-      if (q_thread) red[2][g][i] = qv;
-      if (kv_thread) red[3][0][i] = kv;
-      __syncthreads();
-      const int half = kD / 2, fi = i % half;
-      const float ang = (float)pos * a.inv_freq[fi];
-      float sn, cs;
-      sincosf(ang, &sn, &cs);
       if (q_thread) {
-        const float other = red[2][g][i < half ? i + half : i - half];
-        qv = i < half ? qv * cs - other * sn : qv * cs + other * sn;
+        const float other = red[2][gq][iq < half ? iq + half : iq - half];
+        qv = iq < half ? qv * cs - other * sn : qv * cs + other * sn;
       }
       if (kv_thread) {
-        const float other = red[3][0][i < half ? i + half : i - half];
-        kv = i < half ? kv * cs - other * sn : kv * cs + other * sn;
+        const float other = red[3][0][iq < half ? iq + half : iq - half];
+        kv = iq < half ? kv * cs - other * sn : kv * cs + other * sn;
       }
     }
-    if (q_thread) qs[g][i] = qv * a.scale;
+    if (q_thread) qs[gq][iq] = qv * a.scale;
     if (kv_thread) {
       const _Float16 k16 = (_Float16)kv, v16 = (_Float16)vv;
-      knew[i] = k16;
-      vnew[i] = v16;
-      a.kcache[cache_base + (size_t)pos * kD + i] = __builtin_bit_cast(uint16_t, k16);
-      a.vcache[cache_base + (size_t)pos * kD + i] = __builtin_bit_cast(uint16_t, v16);
+      knew[iq] = k16;
+      vnew[iq] = v16;
+      a.kcache[cache_base + (size_t)pos * kD + iq] = __builtin_bit_cast(uint16_t, k16);
+      a.vcache[cache_base + (size_t)pos * kD + iq] = __builtin_bit_cast(uint16_t, v16);
     }
     __syncthreads();
   }
 
-  const int seg = lane % kLPP, sub = lane / kLPP;
   float q8[kG][8];
 #pragma unroll
   for (int g = 0; g < kG; g++)
 #pragma unroll
     for (int e = 0; e < 8; e++) q8[g][e] = qs[g][seg * 8 + e];
+#pragma unroll
+  for (int u = 0; u < kBatch; u++) {  // the new token's K / V, computed above
+    const int pi = u * kPPB + wave * kPPW + sub;
+    if (pi < np && p0 + pi == pos) {
+      k8[u] = *reinterpret_cast<const f16x8 *>(&knew[seg * 8]);
+      v8[u] = *reinterpret_cast<const f16x8 *>(&vnew[seg * 8]);
+    }
+  }
 
   // ---- scores ----
-  for (int base = 0; base < np; base += kPPB) {
-    const int pi = base + wave * kPPW + sub;
-    const int p = p0 + pi;
-    f16x8 k8 = {};
-    if (pi < np) {
-      if (p == pos)
-        k8 = *reinterpret_cast<const f16x8 *>(&knew[seg * 8]);
-      else
-        k8 = *reinterpret_cast<const f16x8 *>(a.kcache + cache_base + (size_t)p * kD + seg * 8);
+  for (int base = 0; base < np; base += kBatch * kPPB) {
+    if (base > 0) {
+#pragma unroll
+      for (int u = 0; u < kBatch; u++) {
+        const int pi = base + u * kPPB + wave * kPPW + sub;
+        const int p = p0 + pi;
+        k8[u] = f16x8{};
+        if (pi < np)
+          k8[u] = p == pos ? *reinterpret_cast<const f16x8 *>(&knew[seg * 8])
+                           : *reinterpret_cast<const f16x8 *>(kbase + (size_t)p * kD);
+      }
     }
 #pragma unroll
-    for (int g = 0; g < kG; g++) {
-      float d = 0.0f;
+    for (int u = 0; u < kBatch; u++) {
+      const int pi = base + u * kPPB + wave * kPPW + sub;
 #pragma unroll
-      for (int e = 0; e < 8; e++) d += q8[g][e] * (float)k8[e];
+      for (int g = 0; g < kG; g++) {
+        float d = 0.0f;
 #pragma unroll
-      for (int off = kLPP / 2; off >= 1; off >>= 1) d += __shfl_xor(d, off, 64);
-      if (seg == 0 && pi < np) scores[g][pi] = d;
+        for (int e = 0; e < 8; e++) d += q8[g][e] * (float)k8[u][e];
+#pragma unroll
+        for (int off = kLPP / 2; off >= 1; off >>= 1) d += __shfl_xor(d, off, 64);
+        if (seg == 0 && pi < np) scores[g][pi] = d;
+      }
     }
   }
   __syncthreads();
@@ -540,20 +666,28 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
   for (int g = 0; g < kG; g++)
 #pragma unroll
     for (int e = 0; e < 8; e++) acc[g][e] = 0.0f;
-  for (int base = 0; base < np; base += kPPB) {
-    const int pi = base + wave * kPPW + sub;
-    const int p = p0 + pi;
-    if (pi < np) {
-      f16x8 v8;
-      if (p == pos)
-        v8 = *reinterpret_cast<const f16x8 *>(&vnew[seg * 8]);
-      else
-        v8 = *reinterpret_cast<const f16x8 *>(a.vcache + cache_base + (size_t)p * kD + seg * 8);
+  for (int base = 0; base < np; base += kBatch * kPPB) {
+    if (base > 0) {
 #pragma unroll
-      for (int g = 0; g < kG; g++) {
-        const float w = scores[g][pi];
+      for (int u = 0; u < kBatch; u++) {
+        const int pi = base + u * kPPB + wave * kPPW + sub;
+        const int p = p0 + pi;
+        v8[u] = f16x8{};
+        if (pi < np)
+          v8[u] = p == pos ? *reinterpret_cast<const f16x8 *>(&vnew[seg * 8])
+                           : *reinterpret_cast<const f16x8 *>(vbase + (size_t)p * kD);
+      }
+    }
 #pragma unroll
-        for (int e = 0; e < 8; e++) acc[g][e] += w * (float)v8[e];
+    for (int u = 0; u < kBatch; u++) {
+      const int pi = base + u * kPPB + wave * kPPW + sub;
+      if (pi < np) {
+#pragma unroll
+        for (int g = 0; g < kG; g++) {
+          const float w = scores[g][pi];
+#pragma unroll
+          for (int e = 0; e < 8; e++) acc[g][e] += w * (float)v8[u][e];
+        }
       }
     }
   }
@@ -585,7 +719,9 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
     return;
   }
 
-  // ---- partials, then the last workgroup merges ----
+  // ---- partials: merged by attn_merge_kernel after this kernel ends (a
+  // kernel boundary publishes them to every XCD's L2 without per-workgroup
+  // device-scope fences, which write back and invalidate the whole L2) ----
   const size_t pstride = (size_t)kD + 2;
   if (t < kG * kD) {
     const int g = t / kD, i = t % kD;
@@ -596,29 +732,51 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
       pp[kD + 1] = stat[g][1];
     }
   }
-  __threadfence();
-  __syncthreads();
-  if (t == 0) {
-    const int prev = atomicAdd(a.counters + b * a.kv_heads + kvh, 1);
-    is_last = prev == active - 1;
+}
+
+// grid (heads, B), kD threads: combines the split partials of one head,
+//   out = sum_j exp(m_j - M) acc_j / sum_j exp(m_j - M) l_j,  M = max_j m_j.
+// Heads whose context fitted one split were written by the attention kernel.
+template <int kD>
+__global__ __launch_bounds__(kD) void attn_merge_kernel(const AttnArgs a) {
+  constexpr int kMaxSplits = 64;
+  __shared__ float w[kMaxSplits];
+  __shared__ float lsum[kD / 64];
+  const int b = blockIdx.y, h = blockIdx.x, i = threadIdx.x, lane = i & 63;
+  const int L = a.pos[b] + 1;
+  const int chunk = split_chunk(L, a.splits);
+  const int active = (L + chunk - 1) / chunk;
+  if (active <= 1 || active > kMaxSplits || L > a.max_pos) return;
+  const size_t pstride = (size_t)kD + 2;
+  const float *pp = a.part + ((size_t)b * a.heads + h) * a.splits * pstride;
+  // split statistics: thread j < active holds (m_j, l_j)
+  const float mj = i < active ? pp[(size_t)i * pstride + kD] : -INFINITY;
+  const float lj = i < active ? pp[(size_t)i * pstride + kD + 1] : 0.0f;
+  float M = wave_max(mj);
+  if (kD > 64) {  // splits never exceed 64: lanes of wave 0 hold them all
+    __shared__ float m0;
+    if (i == 0) m0 = M;
+    __syncthreads();
+    M = m0;
   }
+  const float wj = i < active ? expf(mj - M) : 0.0f;
+  if (i < kMaxSplits) w[i] = wj;
+  const float lw = wave_sum(wj * lj);
+  if (lane == 0) lsum[i >> 6] = lw;
   __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  if (t < kG * kD) {
-    const int g = t / kD, i = t % kD;
-    const float *pp = a.part + ((size_t)b * a.heads + h0 + g) * a.splits * pstride;
-    float m = -INFINITY;
-    for (int j = 0; j < active; j++) m = fmaxf(m, pp[j * pstride + kD]);
-    float l = 0.0f, v = 0.0f;
-    for (int j = 0; j < active; j++) {
-      const float w = expf(pp[j * pstride + kD] - m);
-      l += w * pp[j * pstride + kD + 1];
-      v += w * pp[j * pstride + i];
-    }
-    a.out[(size_t)b * a.out_ld + (h0 + g) * kD + i] = f32_to_f16_bits(v / l);
+  float ltot = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kD / 64; k++) ltot += lsum[k];
+  float v = 0.0f;
+  for (int j0 = 0; j0 < active; j0 += 16) {
+    float x[16];
+#pragma unroll
+    for (int u = 0; u < 16; u++) x[u] = j0 + u < active ? pp[(size_t)(j0 + u) * pstride + i] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < 16; u++)
+      if (j0 + u < active) v += w[j0 + u] * x[u];
   }
-  if (t == 0) a.counters[b * a.kv_heads + kvh] = 0;  // ready for the next layer
+  a.out[(size_t)b * a.out_ld + h * kD + i] = f32_to_f16_bits(v / ltot);
 }
 
 // ---- embedding -------------------------------------------------------------
@@ -645,6 +803,12 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const EmbedArgs a) {
   }
   __syncthreads();
   const int tok = tok_s, pos = pos_s;
+  if (a.rope && t < a.half) {  // RoPE of this step's position, shared by all layers
+    float sn, cs;
+    sincosf((float)pos * a.inv_freq[t], &sn, &cs);
+    a.rope[(size_t)b * 2 * a.half + t] = cs;
+    a.rope[(size_t)b * 2 * a.half + a.half + t] = sn;
+  }
   float *x = a.x + (size_t)b * a.x_ld;
   for (int k = t; k < a.K; k += kThreads) {
     float v;
@@ -660,10 +824,15 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const EmbedArgs a) {
   }
 }
 
+size_t gemv_lds_bytes(const GemvArgs &a, int pro) {
+  size_t lds = (size_t)a.B * (a.K + 8) * 2 + 4 * 2 * 64 * 4 * sizeof(float);
+  if (pro != kProNone) lds += (size_t)a.B * a.K * 4 + 2 * (size_t)a.K * 4;
+  return lds;
+}
+
 template <int kW, int kPro, int kEpi>
 hipError_t launch_gemv_t(hipStream_t s, const GemvArgs &a, int grid) {
-  const size_t lds = (size_t)a.B * (a.K + 8) * 2 + 4 * 2 * 64 * 4 * sizeof(float);
-  gemv_kernel<kW, kPro, kEpi><<<grid, kThreads, lds, s>>>(a);
+  gemv_kernel<kW, kPro, kEpi><<<grid, kThreads, gemv_lds_bytes(a, kPro), s>>>(a);
   return hipGetLastError();
 }
 
@@ -707,13 +876,22 @@ unsigned blocks_for(size_t n) { return (unsigned)((n + kThreads - 1) / kThreads)
 
 }  // namespace
 
-hipError_t launch_gemv(hipStream_t s, const GemvArgs &a, int weight_type, int pro, int epi,
+hipError_t launch_gemv(hipStream_t s, const GemvArgs &a_in, int weight_type, int pro, int epi,
                        int max_grid) {
+  GemvArgs a = a_in;
   const int groups = a.N / (16 * (epi == kEpiSwiGLU ? 2 : 1));
-  const int grid = max_grid > 0 && groups > max_grid ? max_grid : groups;
+  // many tile groups: every wave owns whole groups (about four each, so the
+  // per-workgroup prologue is paid ~600 times, not per tile);
+  // few: split K over the 4 waves of a workgroup
+  a.split_k = groups < 4 * 256 ? 1 : 0;
+  int grid = a.split_k ? groups : (groups + 15) / 16;
+  if (max_grid > 0 && grid > max_grid) grid = max_grid;
   if (weight_type == kWeightFp8) return launch_gemv_pro<kWeightFp8>(s, a, pro, epi, grid);
   return launch_gemv_pro<kWeightFp16>(s, a, pro, epi, grid);
 }
+
+hipError_t launch_attention_partials(hipStream_t s, const AttnArgs &a, int head_dim, int group,
+                                     bool qwen, dim3 grid);
 
 hipError_t prepare_gemv_kernels() {
   hipError_t e;
@@ -728,6 +906,18 @@ hipError_t prepare_gemv_kernels() {
 hipError_t launch_attention(hipStream_t s, const AttnArgs &a, int head_dim, int group, bool qwen,
                             int batch) {
   dim3 grid(a.splits, a.kv_heads, batch);
+  hipError_t e = launch_attention_partials(s, a, head_dim, group, qwen, grid);
+  if (e != hipSuccess || a.splits == 1) return e;
+  dim3 mgrid(a.heads, batch);
+  if (head_dim == 128)
+    attn_merge_kernel<128><<<mgrid, 128, 0, s>>>(a);
+  else
+    attn_merge_kernel<64><<<mgrid, 64, 0, s>>>(a);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_partials(hipStream_t s, const AttnArgs &a, int head_dim, int group,
+                                     bool qwen, dim3 grid) {
   if (head_dim == 128 && group == 2 && qwen)
     attn_decode_kernel<128, 2, true><<<grid, kThreads, 0, s>>>(a);
   else if (head_dim == 128 && group == 1 && qwen)
