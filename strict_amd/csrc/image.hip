@@ -388,7 +388,7 @@ int blur_groups() {
 
 template <int kMode, int kGroups>
 void launch_stream_fuse(hipStream_t s, const StreamArgs &a, int fuse) {
-  const int blocks = (a.total_waves + kBlock / 64 - 1) / (kBlock / 64);
+  const int blocks = a.xcd_blocks * 8;
   if (fuse == 1)
     blur_rgba_stream_kernel<kMode, 1, kGroups><<<blocks, kBlock, 0, s>>>(a);
   else if (fuse == 2)
@@ -408,8 +408,10 @@ void launch_blur_stream(hipStream_t s, const uint32_t *in, uint32_t *out, int wi
   a.strips_x = (width + kStripPx - 1) / kStripPx;
   const int bands = (height + 5 * kGroups - 1) / (5 * kGroups);
   a.total_waves = a.strips_x * bands;
-  const int blocks = (a.total_waves + kBlock / 64 - 1) / (kBlock / 64);
-  a.xcd_blocks = (blocks % 8 == 0) ? blocks / 8 : 0;
+  // padded to a multiple of 8 workgroups (the extra waves exit at once) so
+  // that every XCD gets an equal contiguous range of bands
+  const int blocks = ((a.total_waves + kBlock / 64 - 1) / (kBlock / 64) + 7) / 8 * 8;
+  a.xcd_blocks = blocks / 8;
   int f = 0;
   a.d_lo = a.d_hi = 0;
   if (fuse && delta != 0) {

@@ -36,7 +36,6 @@ struct GemvArgs {
   uint16_t *out16 = nullptr; // fp16 output rows (SwiGLU, GELU)
   int out_ld = 0;
   unsigned long long *argmax = nullptr;  // logits: per-row argmax keys (atomicMax)
-  int split_k = 1;  // set by launch_gemv: 4 waves split K (1) or one wave per tile (0)
 };
 
 struct AttnArgs {
@@ -51,6 +50,7 @@ struct AttnArgs {
   float scale = 1.0f;               // 1 / sqrt(d)
   int heads = 0, kv_heads = 0;
   int splits = 1;                   // grid.x
+  int chunk = 16;                   // positions per split (multiple of 16)
   float *part = nullptr;            // [B][heads][splits][d + 2]
   int *counters = nullptr;          // [B][kv_heads], zero between launches
   uint16_t *out = nullptr;          // [B][out_ld] fp16 head outputs
@@ -82,6 +82,8 @@ hipError_t launch_gemv(hipStream_t s, const GemvArgs &a, int weight_type, int pr
 hipError_t launch_attention(hipStream_t s, const AttnArgs &a, int head_dim, int group, bool qwen,
                             int batch);
 hipError_t launch_embed(hipStream_t s, const EmbedArgs &a, int batch);
+// fp16 out16[b] = norm(x[b]) (pro = kProRms or kProLayer), K <= 4096.
+hipError_t launch_norm_rows(hipStream_t s, const GemvArgs &a, int pro);
 hipError_t launch_quantize_e4m3_tiled(hipStream_t s, const float *w, int N, int K,
                                       int interleave_rows, uint8_t *q, float *scales,
                                       bool tiled);

@@ -37,12 +37,13 @@ struct Layer {
   uint16_t *kcache = nullptr, *vcache = nullptr;
 };
 
-// Splits of the context per (sequence, KV head): about 256 workgroups in all
-// (one per CU; at the Qwen3 shape and b = 1 that is 128 positions per
-// workgroup, one batch of K loads per thread), at least enough that no split
-// exceeds kMaxSplitChunk positions, at most 64 (the merge kernel's limit).
+// Splits of the context per (sequence, KV head): about 512 workgroups in all
+// (two per CU; at the Qwen3 shape and b = 1, 64 splits of <= 80 positions up
+// to 5120 tokens, so each workgroup's K and V fit one batch of loads issued
+// together), at least enough that no split exceeds kMaxSplitChunk positions,
+// at most 64 (the merge kernel's limit).
 int attention_splits(int batch, int kv_heads, int max_pos) {
-  int s = 256 / (batch * kv_heads);
+  int s = 512 / (batch * kv_heads);
   if (s > 64) s = 64;
   const int min_s = (max_pos + kMaxSplitChunk - 1) / kMaxSplitChunk;
   if (s < min_s) s = min_s;
@@ -68,7 +69,8 @@ struct sh_llm {
   uint16_t *attn = nullptr, *act = nullptr;
   int *counters = nullptr, *lens = nullptr, *pos = nullptr, *hist = nullptr;
   unsigned long long *keys = nullptr;
-  int batch = 0, splits = 1, steps_done = 0;
+  int batch = 0, splits = 1, chunk = 16, steps_done = 0;
+  uint16_t *hnorm = nullptr;  // final-norm output rows (fp16) fed to the LM head
   size_t kv_layer_elems = 0;
   hipGraphExec_t graph[2] = {nullptr, nullptr};
   int graph_batch[2] = {-1, -1};
@@ -194,6 +196,7 @@ int enqueue_step(sh_llm *m, bool logits) {
     a.heads = c.heads;
     a.kv_heads = c.kv_heads;
     a.splits = m->splits;
+    a.chunk = m->chunk;
     a.part = m->part;
     a.counters = m->counters;
     a.out = m->attn;
@@ -244,14 +247,22 @@ int enqueue_step(sh_llm *m, bool logits) {
   }
 
   if (logits) {
+    GemvArgs nrm;
+    nrm.x = m->x;
+    nrm.x_ld = H;
+    nrm.gamma = m->final_g;
+    nrm.beta = m->final_b;
+    nrm.eps = c.norm_eps;
+    nrm.B = B;
+    nrm.K = H;
+    nrm.out16 = m->hnorm;
+    nrm.out_ld = H;
+    SH_HIP_TRY(launch_norm_rows(s, nrm, pro));
     GemvArgs h;
     h.w = m->head.w;
     h.scale = m->head.scale;
-    h.x = m->x;
-    h.x_ld = H;
-    h.gamma = m->final_g;
-    h.beta = m->final_b;
-    h.eps = c.norm_eps;
+    h.act = m->hnorm;
+    h.act_ld = H;
     h.B = B;
     h.K = H;
     h.N = m->head.N;
@@ -259,7 +270,7 @@ int enqueue_step(sh_llm *m, bool logits) {
     h.out = m->logits;
     h.out_ld = m->vocab_pad;
     h.argmax = m->keys;
-    SH_HIP_TRY(launch_gemv(s, h, m->wtype, pro, kEpiLogits, 2048));
+    SH_HIP_TRY(launch_gemv(s, h, m->wtype, kProNone, kEpiLogits, 2048));
   }
   return SH_OK;
 }
@@ -426,6 +437,8 @@ SH_API int sh_llm_create(sh_ctx *ctx, const sh_llm_config *config, sh_llm **out)
     if (e == hipSuccess) e = hipStreamSynchronize(stream_of(ctx));
     if (e != hipSuccess) return cleanup(hip_fail(e, "uploading RoPE frequencies"));
   }
+  if (c.hidden > 4096) return cleanup(fail(SH_ERR_UNSUPPORTED, "hidden %d > 4096", c.hidden));
+  if ((rc = alloc_n(m, (size_t)B * H, &m->hnorm))) return cleanup(rc);
   if ((rc = alloc_n(m, (size_t)B * H, &m->x)) || (rc = alloc_n(m, (size_t)B * m->qkv_n, &m->qkv)) ||
       (rc = alloc_n(m, (size_t)B * c.heads * d, &m->attn)) ||
       (rc = alloc_n(m, (size_t)B * c.intermediate, &m->act)) ||
@@ -579,6 +592,7 @@ SH_API int sh_llm_reset(sh_llm *m, int batch) {
   SH_HIP_TRY(hipMemsetAsync(m->counters, 0, (size_t)m->cfg.max_batch * m->cfg.kv_heads * 4, s));
   m->batch = batch;
   m->splits = attention_splits(batch, m->cfg.kv_heads, m->cfg.max_positions);
+  m->chunk = ((m->cfg.max_positions + m->splits - 1) / m->splits + 15) / 16 * 16;
   m->steps_done = 0;
   return SH_OK;
 }

@@ -294,22 +294,19 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int n) {
   return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)n);
 }
 
-// Two work splits, chosen by the host (GemvArgs::split_k):
-//  - split-K (few row tiles): a workgroup handles kNT row tiles (two for the
-//    gate/up pair) at a time, grid-striding over tile groups; its 4 waves
-//    split K in four and the partial 16x16 accumulators are summed in LDS,
-//    wave 0 running the epilogue;
-//  - wave-per-tile (many row tiles, e.g. the LM head): every wave owns whole
-//    tile groups over all of K and runs its own epilogue, no LDS reduction or
-//    barrier in the loop.
+// A workgroup handles kNT row tiles (two for the gate/up pair) at a time,
+// grid-striding over tile groups; its 4 waves split K in four and the partial
+// 16x16 accumulators are summed in LDS, wave 0 running the epilogue.
 // The first batch of weight loads is issued before the activation prologue
 // (the weights do not depend on it), so the two memory round trips overlap.
-template <int kW, int kPro, int kEpi>
+template <int kW, int kPro, int kEpi, int kU>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   constexpr int kNT = kEpi == kEpiSwiGLU ? 2 : 1;
   constexpr int kKPerLoad = kW == kWeightFp8 ? 64 : 32;
-  constexpr int kU = 16 / kNT;  // 16-byte weight loads per lane in flight
+  // kU: 16-byte weight loads per lane per batch (per tile of a pair); the host
+  // picks it dividing the wave's loads, so every batch is full and its loads
+  // are unconditional
   const int K = a.K, B = a.B;
   const int stride = K + 8;
   _Float16 *xs = reinterpret_cast<_Float16 *>(smem);
@@ -317,32 +314,30 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvArgs a) {
   float *xf = red + 4 * 2 * 64 * 4;  // norm prologue: fp32 rows, gamma, beta
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const bool split = a.split_k != 0;
   const int loads_per_row = K / kKPerLoad;  // 16-byte lane loads per tile row group
-  const int per_wave = split ? loads_per_row / 4 : loads_per_row;
-  const int c0 = split ? wave * per_wave : 0;
+  const int per_wave = loads_per_row / 4;
+  const int c0 = wave * per_wave;
   const int groups = a.N / (16 * kNT);
-  const int g_first = split ? blockIdx.x : blockIdx.x * 4 + wave;
-  const int g_step = split ? gridDim.x : gridDim.x * 4;
+  const int g_first = blockIdx.x;
+  const int g_step = gridDim.x;
   const int arow = lane & 15, acol = 8 * (lane >> 4);
   const bool arow_valid = arow < B;
 
   u32x4 wv[kU][kNT];
-  auto load_batch = [&](int g, int c) {
+  auto load_into = [&](u32x4 (&r)[kU][kNT], int g, int c) {
 #pragma unroll
     for (int u = 0; u < kU; u++)
 #pragma unroll
       for (int j = 0; j < kNT; j++) {
         const size_t tile = (size_t)(g * kNT + j) * loads_per_row + (c + u);
-        if (c + u < c0 + per_wave)
-          wv[u][j] = __builtin_nontemporal_load(
-              reinterpret_cast<const u32x4 *>(a.w + tile * 1024 + (size_t)lane * 16));
+        r[u][j] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4 *>(a.w + tile * 1024 + (size_t)lane * 16));
       }
   };
-  auto mul_batch = [&](int c, f32x4 (&acc)[kNT]) {
+  auto load_batch = [&](int g, int c) { load_into(wv, g, c); };
+  auto mul_from = [&](const u32x4 (&r)[kU][kNT], int c, f32x4 (&acc)[kNT]) {
 #pragma unroll
     for (int u = 0; u < kU; u++) {
-      if (c + u >= c0 + per_wave) break;
       const int kbase = (c + u) * kKPerLoad;
 #pragma unroll
       for (int h = 0; h < kKPerLoad / 32; h++) {
@@ -353,20 +348,21 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvArgs a) {
         for (int j = 0; j < kNT; j++) {
           f16x8 bf;
           if (kW == kWeightFp8) {
-            const uint32_t d0 = wv[u][j][2 * h], d1 = wv[u][j][2 * h + 1];
+            const uint32_t d0 = r[u][j][2 * h], d1 = r[u][j][2 * h + 1];
             const f16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, false);
             const f16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, true);
             const f16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, false);
             const f16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, true);
             bf = f16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
           } else {
-            bf = __builtin_bit_cast(f16x8, wv[u][j]);
+            bf = __builtin_bit_cast(f16x8, r[u][j]);
           }
           acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[j], 0, 0, 0);
         }
       }
     }
   };
+  auto mul_batch = [&](int c, f32x4 (&acc)[kNT]) { mul_from(wv, c, acc); };
 
   unsigned long long best[4] = {0, 0, 0, 0};  // logits: running argmax keys per b row
   // lane holds column n = tile row (lane % 16) for batch rows 4*(lane/16) + r
@@ -410,48 +406,36 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvArgs a) {
   Stager<kPro> stager;
   stager.issue(a);
   if (g_first < groups) load_batch(g_first, c0);
+  __builtin_amdgcn_sched_barrier(0);  // keep every load above ahead of their uses
   stager.finish(a, xs, red, xf);
 
-  if (split) {
-    for (int g = g_first; g < groups; g += g_step) {
-      f32x4 acc[kNT];
+  for (int g = g_first; g < groups; g += g_step) {
+    f32x4 acc[kNT];
 #pragma unroll
-      for (int j = 0; j < kNT; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      for (int c = c0; c < c0 + per_wave; c += kU) {
-        if (g != g_first || c != c0) load_batch(g, c);
-        mul_batch(c, acc);
-      }
-#pragma unroll
-      for (int j = 0; j < kNT; j++)
-        *reinterpret_cast<f32x4 *>(red + ((wave * kNT + j) * 64 + lane) * 4) = acc[j];
-      __syncthreads();
-      if (wave == 0) {
-        f32x4 y[kNT];
-#pragma unroll
-        for (int j = 0; j < kNT; j++) {
-          y[j] = *reinterpret_cast<const f32x4 *>(red + (j * 64 + lane) * 4);
-#pragma unroll
-          for (int w = 1; w < 4; w++)
-            y[j] += *reinterpret_cast<const f32x4 *>(red + ((w * kNT + j) * 64 + lane) * 4);
-        }
-        epilogue(g, y);
-      }
-      __syncthreads();
+    for (int j = 0; j < kNT; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int c = c0; c < c0 + per_wave; c += kU) {
+      if (g != g_first || c != c0) load_batch(g, c);
+      mul_batch(c, acc);
     }
-  } else {
-    for (int g = g_first; g < groups; g += g_step) {
-      f32x4 acc[kNT];
 #pragma unroll
-      for (int j = 0; j < kNT; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      for (int c = 0; c < per_wave; c += kU) {
-        if (g != g_first || c != 0) load_batch(g, c);
-        mul_batch(c, acc);
+    for (int j = 0; j < kNT; j++)
+      *reinterpret_cast<f32x4 *>(red + ((wave * kNT + j) * 64 + lane) * 4) = acc[j];
+    __syncthreads();
+    if (wave == 0) {
+      f32x4 y[kNT];
+#pragma unroll
+      for (int j = 0; j < kNT; j++) {
+        y[j] = *reinterpret_cast<const f32x4 *>(red + (j * 64 + lane) * 4);
+#pragma unroll
+        for (int w = 1; w < 4; w++)
+          y[j] += *reinterpret_cast<const f32x4 *>(red + ((w * kNT + j) * 64 + lane) * 4);
       }
-      epilogue(g, acc);
+      epilogue(g, y);
     }
+    __syncthreads();
   }
 
-  if (kEpi == kEpiLogits && (!split || wave == 0)) {
+  if (kEpi == kEpiLogits && wave == 0) {
     // reduce the running keys over the 16 columns held by each lane group
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -469,14 +453,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvArgs a) {
 
 // ---- decode attention ------------------------------------------------------
 
-// Positions per split for a context of L tokens over `splits` workgroups
-// (multiple of 16, at least 16); every workgroup derives the same value.
-__device__ __forceinline__ int split_chunk(int L, int splits) {
-  int c = (L + splits - 1) / splits;
-  c = (c + 15) & ~15;
-  return c < 16 ? 16 : c;
-}
-
+// Positions per split: a fixed size for the model (multiple of 16, at least
+// 16) chosen by the host from max_positions and the split count, so that a
+// workgroup's K / V addresses depend on its block index only and can be
+// requested before the context length is known.
 // grid (splits, kv_heads, B); one workgroup scores positions [p0, p1) of one
 // KV head for its kG query heads, keeps (max, sum, unnormalised V sum) per
 // head, and the last workgroup of the (b, kv head) to finish merges all
@@ -503,51 +483,62 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
 
   const int b = blockIdx.z, kvh = blockIdx.y, s = blockIdx.x;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int L = a.pos[b] + 1;  // context including the new token
-  const int chunk = split_chunk(L, a.splits);
-  const int active = (L + chunk - 1) / chunk;
-  // the host sizes `splits` so that chunk <= kMaxSplitChunk for every L up to
-  // max_pos (and splits <= kMaxSplits); anything else would overrun LDS
-  if (s >= active || chunk > kMaxSplitChunk || L > a.max_pos || a.splits > kMaxSplits) return;
-  const int p0 = s * chunk, p1 = min(L, p0 + chunk), np = p1 - p0;
-  const int pos = L - 1;
+  const int chunk = a.chunk;
+  // the host sizes `splits` x `chunk` to cover max_pos with chunk <=
+  // kMaxSplitChunk and splits <= kMaxSplits; anything else would overrun LDS
+  if (chunk > kMaxSplitChunk || chunk < 16 || a.splits > kMaxSplits) return;
+  const int p0 = s * chunk;
+  if (p0 >= a.max_pos) return;
   const float *qkv = a.qkv + (size_t)b * a.qkv_ld;
   const size_t cache_base = ((size_t)b * a.kv_heads + kvh) * (size_t)a.max_pos * kD;
-  const bool holds_new = p1 == L;
   const int seg = lane % kLPP, sub = lane / kLPP;
   const uint16_t *kbase = a.kcache + cache_base + seg * 8;
   const uint16_t *vbase = a.vcache + cache_base + seg * 8;
-
-  // Small loads first (q, the new k / v, norm gains, RoPE of this step), then
-  // K and V of the first kBatch block steps, which do not depend on q: the
-  // q prologue then runs while K / V are in flight (vector-memory counters
-  // retire in issue order, so consuming q waits only for what precedes it).
   const int gq = t / kD, iq = t % kD;
   const bool q_thread = t < kG * kD;
-  const bool kv_thread = holds_new && t < kD;
   const int half = kD / 2, fi = iq % half;
-  float qv = q_thread ? qkv[(kvh * kG + gq) * kD + iq] : 0.0f;
-  float kv = kv_thread ? qkv[a.heads * kD + kvh * kD + iq] : 0.0f;
-  const float vv = kv_thread ? qkv[(a.heads + a.kv_heads) * kD + kvh * kD + iq] : 0.0f;
+
+  // Issue order: the position, this step's q / k / v, norm gains and RoPE,
+  // then K and V of the first kBatch block steps of the split (addresses
+  // from the block index only; positions past the context are loaded from
+  // the allocated cache and discarded). Vector-memory counters retire in
+  // issue order, so using the position and q waits only for what precedes
+  // them while K / V stay in flight through the q prologue.
+  // (unconditional loads at clamped in-bounds indices: no load sits in a
+  // branch, so the compiler cannot pull a conversion of it, and the wait it
+  // needs, ahead of the K / V loads below)
+  const int L = a.pos[b] + 1;  // context including the new token
+  const bool may_hold_new = t < kD;
+  float qv = qkv[(kvh * kG + min(gq, kG - 1)) * kD + iq];
+  float kv = qkv[a.heads * kD + kvh * kD + iq];
+  float vv = qkv[(a.heads + a.kv_heads) * kD + kvh * kD + iq];
   float qn = 1.0f, kn = 1.0f, cs = 1.0f, sn = 0.0f;
   if (kQwen) {
-    qn = q_thread ? a.q_norm[iq] : 1.0f;
-    kn = kv_thread ? a.k_norm[iq] : 1.0f;
+    qn = a.q_norm[iq];
+    kn = a.k_norm[iq];
     cs = a.rope[(size_t)b * kD + fi];
     sn = a.rope[(size_t)b * kD + half + fi];
   }
+  // positions of this split inside the cache; slots past them reload its
+  // last position (unconditional loads: no register merge forces a wait)
+  const int cap = min(chunk, a.max_pos - p0);
   f16x8 k8[kBatch], v8[kBatch];
 #pragma unroll
   for (int u = 0; u < kBatch; u++) {
-    const int pi = u * kPPB + wave * kPPW + sub;
-    const int p = p0 + pi;
-    k8[u] = f16x8{};
-    v8[u] = f16x8{};
-    if (pi < np && p != pos) {
-      k8[u] = *reinterpret_cast<const f16x8 *>(kbase + (size_t)p * kD);
-      v8[u] = *reinterpret_cast<const f16x8 *>(vbase + (size_t)p * kD);
-    }
+    const int pi = min(u * kPPB + wave * kPPW + sub, cap - 1);
+    k8[u] = *reinterpret_cast<const f16x8 *>(kbase + (size_t)(p0 + pi) * kD);
+    v8[u] = *reinterpret_cast<const f16x8 *>(vbase + (size_t)(p0 + pi) * kD);
   }
+  __builtin_amdgcn_sched_barrier(0);  // keep every load above ahead of their uses
+
+  const int active = (L + chunk - 1) / chunk;
+  if (s >= active || L > a.max_pos) return;
+  const int p1 = min(L, p0 + chunk), np = p1 - p0;
+  const int pos = L - 1;
+  const bool holds_new = p1 == L;
+  const bool kv_thread = holds_new && may_hold_new;
+  if (!q_thread) qv = 0.0f;
+  if (!kv_thread) kv = vv = 0.0f;
 
   // ---- q (and the new k / v) ----
   {
@@ -744,8 +735,7 @@ __global__ __launch_bounds__(kD) void attn_merge_kernel(const AttnArgs a) {
   __shared__ float lsum[kD / 64];
   const int b = blockIdx.y, h = blockIdx.x, i = threadIdx.x, lane = i & 63;
   const int L = a.pos[b] + 1;
-  const int chunk = split_chunk(L, a.splits);
-  const int active = (L + chunk - 1) / chunk;
+  const int active = (L + a.chunk - 1) / a.chunk;
   if (active <= 1 || active > kMaxSplits || L > a.max_pos) return;
   const size_t pstride = (size_t)kD + 2;
   const float *pp = a.part + ((size_t)b * a.heads + h) * a.splits * pstride;
@@ -767,16 +757,66 @@ __global__ __launch_bounds__(kD) void attn_merge_kernel(const AttnArgs a) {
   float ltot = 0.0f;
 #pragma unroll
   for (int k = 0; k < kD / 64; k++) ltot += lsum[k];
+  // every split's column value in one batch of loads (active <= 64)
+  float x[kMaxSplits];
+#pragma unroll
+  for (int u = 0; u < kMaxSplits; u++) x[u] = u < active ? pp[(size_t)u * pstride + i] : 0.0f;
   float v = 0.0f;
-  for (int j0 = 0; j0 < active; j0 += 16) {
-    float x[16];
 #pragma unroll
-    for (int u = 0; u < 16; u++) x[u] = j0 + u < active ? pp[(size_t)(j0 + u) * pstride + i] : 0.0f;
-#pragma unroll
-    for (int u = 0; u < 16; u++)
-      if (j0 + u < active) v += w[j0 + u] * x[u];
-  }
+  for (int u = 0; u < kMaxSplits; u++)
+    if (u < active) v += w[u] * x[u];
   a.out[(size_t)b * a.out_ld + h * kD + i] = f32_to_f16_bits(v / ltot);
+}
+
+// ---- row norm ----------------------------------------------------------------
+
+// grid (B): fp16 out[b] = RMSNorm / LayerNorm of the fp32 row x[b] (the final
+// norm before the LM head, done once instead of in every head workgroup).
+template <int kPro>
+__global__ __launch_bounds__(kThreads) void norm_rows_kernel(const GemvArgs a) {
+  constexpr int kPer = 16;  // K <= 4096
+  __shared__ float red[4];
+  const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const float *x = a.x + (size_t)b * a.x_ld;
+  float v[kPer], g[kPer], be[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; u++) {
+    const int k = u * kThreads + t;
+    v[u] = k < a.K ? x[k] : 0.0f;
+    g[u] = k < a.K ? a.gamma[k] : 0.0f;
+    be[u] = (kPro == kProLayer && k < a.K) ? a.beta[k] : 0.0f;
+  }
+  float mean = 0.0f;
+  if (kPro == kProLayer) {
+    float sm = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kPer; u++) sm += v[u];
+    sm = wave_sum(sm);
+    if (lane == 0) red[wave] = sm;
+    __syncthreads();
+    mean = (red[0] + red[1] + red[2] + red[3]) / (float)a.K;
+    __syncthreads();
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int u = 0; u < kPer; u++) {
+    const int k = u * kThreads + t;
+    const float d = k < a.K ? v[u] - mean : 0.0f;
+    ss += d * d;
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  const float inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)a.K + a.eps);
+#pragma unroll
+  for (int u = 0; u < kPer; u++) {
+    const int k = u * kThreads + t;
+    if (k < a.K) {
+      float y = (v[u] - mean) * inv * g[u];
+      if (kPro == kProLayer) y += be[u];
+      a.out16[(size_t)b * a.out_ld + k] = f32_to_f16_bits(y);
+    }
+  }
 }
 
 // ---- embedding -------------------------------------------------------------
@@ -830,46 +870,50 @@ size_t gemv_lds_bytes(const GemvArgs &a, int pro) {
   return lds;
 }
 
-template <int kW, int kPro, int kEpi>
+template <int kW, int kPro, int kEpi, int kU>
 hipError_t launch_gemv_t(hipStream_t s, const GemvArgs &a, int grid) {
-  gemv_kernel<kW, kPro, kEpi><<<grid, kThreads, gemv_lds_bytes(a, kPro), s>>>(a);
+  gemv_kernel<kW, kPro, kEpi, kU><<<grid, kThreads, gemv_lds_bytes(a, kPro), s>>>(a);
   return hipGetLastError();
 }
 
 template <int kW, int kPro, int kEpi>
+hipError_t launch_gemv_u(hipStream_t s, const GemvArgs &a, int grid, int u) {
+  switch (u) {
+    case 8: return launch_gemv_t<kW, kPro, kEpi, 8>(s, a, grid);
+    case 6: return launch_gemv_t<kW, kPro, kEpi, 6>(s, a, grid);
+    case 4: return launch_gemv_t<kW, kPro, kEpi, 4>(s, a, grid);
+    case 2: return launch_gemv_t<kW, kPro, kEpi, 2>(s, a, grid);
+    default: return launch_gemv_t<kW, kPro, kEpi, 1>(s, a, grid);
+  }
+}
+
+// The (weights, prologue, epilogue) combinations the runners and
+// sh_gemv_w8a16 use; anything else is rejected.
+#define SH_GEMV_COMBOS(X)                \
+  X(kWeightFp8, kProNone, kEpiStore)     \
+  X(kWeightFp8, kProNone, kEpiResidual)  \
+  X(kWeightFp8, kProNone, kEpiLogits)    \
+  X(kWeightFp8, kProRms, kEpiStore)      \
+  X(kWeightFp8, kProRms, kEpiSwiGLU)     \
+  X(kWeightFp16, kProNone, kEpiStore)    \
+  X(kWeightFp16, kProNone, kEpiResidual) \
+  X(kWeightFp16, kProNone, kEpiLogits)   \
+  X(kWeightFp16, kProLayer, kEpiStore)   \
+  X(kWeightFp16, kProLayer, kEpiGelu)
+
+template <int kW, int kPro, int kEpi>
 hipError_t allow_large_lds() {
-  return hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_kernel<kW, kPro, kEpi>),
-                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-}
-
-template <int kW, int kPro>
-hipError_t allow_large_lds_pro() {
-  hipError_t e;
-  if ((e = allow_large_lds<kW, kPro, kEpiStore>()) != hipSuccess) return e;
-  if ((e = allow_large_lds<kW, kPro, kEpiResidual>()) != hipSuccess) return e;
-  if ((e = allow_large_lds<kW, kPro, kEpiSwiGLU>()) != hipSuccess) return e;
-  if ((e = allow_large_lds<kW, kPro, kEpiGelu>()) != hipSuccess) return e;
-  return allow_large_lds<kW, kPro, kEpiLogits>();
-}
-
-template <int kW, int kPro>
-hipError_t launch_gemv_epi(hipStream_t s, const GemvArgs &a, int epi, int grid) {
-  switch (epi) {
-    case kEpiStore: return launch_gemv_t<kW, kPro, kEpiStore>(s, a, grid);
-    case kEpiResidual: return launch_gemv_t<kW, kPro, kEpiResidual>(s, a, grid);
-    case kEpiSwiGLU: return launch_gemv_t<kW, kPro, kEpiSwiGLU>(s, a, grid);
-    case kEpiGelu: return launch_gemv_t<kW, kPro, kEpiGelu>(s, a, grid);
-    default: return launch_gemv_t<kW, kPro, kEpiLogits>(s, a, grid);
+  const void *fns[5] = {reinterpret_cast<const void *>(&gemv_kernel<kW, kPro, kEpi, 1>),
+                        reinterpret_cast<const void *>(&gemv_kernel<kW, kPro, kEpi, 2>),
+                        reinterpret_cast<const void *>(&gemv_kernel<kW, kPro, kEpi, 4>),
+                        reinterpret_cast<const void *>(&gemv_kernel<kW, kPro, kEpi, 6>),
+                        reinterpret_cast<const void *>(&gemv_kernel<kW, kPro, kEpi, 8>)};
+  for (const void *f : fns) {
+    const hipError_t e =
+        hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
   }
-}
-
-template <int kW>
-hipError_t launch_gemv_pro(hipStream_t s, const GemvArgs &a, int pro, int epi, int grid) {
-  switch (pro) {
-    case kProNone: return launch_gemv_epi<kW, kProNone>(s, a, epi, grid);
-    case kProRms: return launch_gemv_epi<kW, kProRms>(s, a, epi, grid);
-    default: return launch_gemv_epi<kW, kProLayer>(s, a, epi, grid);
-  }
+  return hipSuccess;
 }
 
 unsigned blocks_for(size_t n) { return (unsigned)((n + kThreads - 1) / kThreads); }
@@ -880,27 +924,35 @@ hipError_t launch_gemv(hipStream_t s, const GemvArgs &a_in, int weight_type, int
                        int max_grid) {
   GemvArgs a = a_in;
   const int groups = a.N / (16 * (epi == kEpiSwiGLU ? 2 : 1));
-  // many tile groups: every wave owns whole groups (about four each, so the
-  // per-workgroup prologue is paid ~600 times, not per tile);
-  // few: split K over the 4 waves of a workgroup
-  a.split_k = groups < 4 * 256 ? 1 : 0;
-  int grid = a.split_k ? groups : (groups + 15) / 16;
+  // split K over the 4 waves of a workgroup, one tile group per workgroup
+  // (grid-striding past max_grid)
+  int grid = groups;
   if (max_grid > 0 && grid > max_grid) grid = max_grid;
-  if (weight_type == kWeightFp8) return launch_gemv_pro<kWeightFp8>(s, a, pro, epi, grid);
-  return launch_gemv_pro<kWeightFp16>(s, a, pro, epi, grid);
+  const int per_wave = a.K / (weight_type == kWeightFp8 ? 64 : 32) / 4;
+  // the deepest batch that divides the wave's share (small K: down to 1)
+  if (per_wave < 1) return hipErrorInvalidValue;  // callers check K alignment first
+  const int u = per_wave % 8 == 0   ? 8
+                : per_wave % 6 == 0 ? 6
+                : per_wave % 4 == 0 ? 4
+                : per_wave % 2 == 0 ? 2
+                                    : 1;
+#define SH_DISPATCH(W, P, E) \
+  if (weight_type == W && pro == P && epi == E) return launch_gemv_u<W, P, E>(s, a, grid, u);
+  SH_GEMV_COMBOS(SH_DISPATCH)
+#undef SH_DISPATCH
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_attention_partials(hipStream_t s, const AttnArgs &a, int head_dim, int group,
                                      bool qwen, dim3 grid);
 
 hipError_t prepare_gemv_kernels() {
-  hipError_t e;
-  if ((e = allow_large_lds_pro<kWeightFp8, kProNone>()) != hipSuccess) return e;
-  if ((e = allow_large_lds_pro<kWeightFp8, kProRms>()) != hipSuccess) return e;
-  if ((e = allow_large_lds_pro<kWeightFp8, kProLayer>()) != hipSuccess) return e;
-  if ((e = allow_large_lds_pro<kWeightFp16, kProNone>()) != hipSuccess) return e;
-  if ((e = allow_large_lds_pro<kWeightFp16, kProRms>()) != hipSuccess) return e;
-  return allow_large_lds_pro<kWeightFp16, kProLayer>();
+  hipError_t e = hipSuccess;
+#define SH_ALLOW(W, P, E) \
+  if (e == hipSuccess) e = allow_large_lds<W, P, E>();
+  SH_GEMV_COMBOS(SH_ALLOW)
+#undef SH_ALLOW
+  return e;
 }
 
 hipError_t launch_attention(hipStream_t s, const AttnArgs &a, int head_dim, int group, bool qwen,
@@ -928,6 +980,15 @@ hipError_t launch_attention_partials(hipStream_t s, const AttnArgs &a, int head_
     attn_decode_kernel<128, 1, false><<<grid, kThreads, 0, s>>>(a);
   else
     return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_norm_rows(hipStream_t s, const GemvArgs &a, int pro) {
+  if (a.K > 16 * kThreads) return hipErrorInvalidValue;
+  if (pro == kProLayer)
+    norm_rows_kernel<kProLayer><<<a.B, kThreads, 0, s>>>(a);
+  else
+    norm_rows_kernel<kProRms><<<a.B, kThreads, 0, s>>>(a);
   return hipGetLastError();
 }
 
