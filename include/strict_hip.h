@@ -132,6 +132,60 @@ SH_API int sh_module_unload(sh_module *module);
 SH_API int sh_launch(sh_function *function, const unsigned grid[3], const unsigned block[3],
                      unsigned shared_bytes, void **args, float *elapsed_ms);
 
+/* ---- kernel source generation: replaces InstructionsToCuda.BuildCudaKernel
+ *      (Strict.Compiler.Cuda/InstructionsToCuda.cs:19-74) ------------------- */
+
+/* Instruction types, numbered as Strict.Bytecode's InstructionType
+ * (Strict.Bytecode/InstructionType.cs:9-47); only those the generator reads
+ * are named. Register ids are Strict.Bytecode's Register values (R0 = 0 ...,
+ * Register.cs:8-26). */
+enum {
+  SH_BC_LOAD_CONSTANT = 0, /* LoadConstantInstruction: registers[0] = number */
+  SH_BC_LOAD_VARIABLE = 1, /* LoadVariableToRegister: registers[0] = identifier */
+  SH_BC_ADD = 11,          /* BinaryInstruction: registers[2] = [0] op [1] */
+  SH_BC_SUBTRACT = 12,
+  SH_BC_MULTIPLY = 13,
+  SH_BC_DIVIDE = 14,
+  SH_BC_MODULO = 15,       /* no kernel operator: rejected as the reference does */
+  SH_BC_EQUAL = 21,        /* 21..24: conditional binaries, skipped */
+  SH_BC_GREATER_THAN = 24,
+  SH_BC_RETURN = 32        /* ReturnInstruction: the output is registers[0] */
+};
+
+/* One bytecode instruction, flattened from the C# Instruction objects. */
+typedef struct sh_bc_instruction {
+  int type;               /* SH_BC_* / InstructionType value; others are ignored */
+  int register_count;     /* registers in use: 1 for loads and return, 3 for binaries */
+  int registers[3];
+  const char *identifier; /* SH_BC_LOAD_VARIABLE */
+  double number;          /* SH_BC_LOAD_CONSTANT */
+} sh_bc_instruction;
+
+/* Writes the HIP source of an elementwise kernel named `method_name` that
+ * evaluates the instructions per element, as BuildCudaKernel does:
+ * `parameters` are the method's parameter names, all Strict Numbers (width and
+ * height become int scalars, initialDepth a float scalar, every other name a
+ * float array indexed per element); `float *output` follows, then
+ * `const int count` when add_count_parameter is non-zero. The bounds check is
+ * `idx >= count`, or `x >= width || y >= height` when both are parameters and
+ * no count is added. Two deliberate differences from the reference, which
+ * produce the same values wherever the reference's text is correct:
+ *  - the element index is the true row-major one (y * gridDim.x * blockDim.x
+ *    + x, or y * width + x), where the reference's `y * blockDim.x + x` aliases
+ *    rows once gridDim.x > 1;
+ *  - an operand that is itself a binary expression is parenthesised where C's
+ *    precedence would regroup it, where the reference concatenates without
+ *    parentheses ((a + b) * c would otherwise print as a + b * c).
+ * Constants print as .NET's invariant-culture double.ToString() does.
+ * `*length` always receives the source length (excluding the NUL); the text
+ * is written only when `capacity` > length, else SH_ERR_INVALID_ARGUMENT.
+ * A Modulo (or other non-arithmetic) binary gives SH_ERR_UNSUPPORTED, the
+ * reference's NotSupportedException (InstructionsToCuda.cs:101-109). */
+SH_API int sh_instructions_to_hip(const char *method_name, const char *const *parameters,
+                                  int parameter_count, int add_count_parameter,
+                                  const sh_bc_instruction *instructions, int instruction_count,
+                                  char *source, size_t capacity, size_t *length);
+
 /* ---- typed ops: elementwise ------------------------------------------------ */
 
 typedef enum sh_binary_op {

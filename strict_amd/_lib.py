@@ -46,6 +46,17 @@ class DeviceInfo(ctypes.Structure):
     ]
 
 
+class BcInstruction(ctypes.Structure):
+    """sh_bc_instruction: one flattened Strict bytecode instruction."""
+    _fields_ = [
+        ("type", ctypes.c_int),
+        ("register_count", ctypes.c_int),
+        ("registers", ctypes.c_int * 3),
+        ("identifier", ctypes.c_char_p),
+        ("number", ctypes.c_double),
+    ]
+
+
 class LlmConfig(ctypes.Structure):
     _fields_ = [
         ("arch", ctypes.c_int),
@@ -99,6 +110,8 @@ SIGNATURES = {
     "sh_program_code": (_I, [_P, _PP, ctypes.POINTER(_SZ)]),
     "sh_program_log": (ctypes.c_char_p, [_P]),
     "sh_program_destroy": (_I, [_P]),
+    "sh_instructions_to_hip": (_I, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p), _I, _I,
+                                    _P, _I, ctypes.c_char_p, _SZ, ctypes.POINTER(_SZ)]),
     "sh_module_load": (_I, [_P, _P, _SZ, _PP]),
     "sh_module_function": (_I, [_P, ctypes.c_char_p, _PP]),
     "sh_module_unload": (_I, [_P]),
