@@ -308,7 +308,10 @@ SH_API int sh_llm_load_linear(sh_llm *model, const char *name, int layer, const 
 /* Device address and size of a named tensor, for uploads and read-back:
  * "<linear>.w" (tiled layout), "<linear>.scale", "<linear>.bias", "norm1.g",
  * "norm1.b", "norm2.g", "norm2.b", "q_norm", "k_norm", "final.g", "final.b",
- * "wpe", "inv_freq", "kcache", "vcache" (per layer), "logits", "hist", "lens". */
+ * "wpe", "inv_freq", "kcache", "vcache" (per layer), "logits", "hist", "lens";
+ * "layers.err" exists only when the persistent decode-layers kernel runs the
+ * layers (Qwen3 shapes it is built for, cooperative launch available, and
+ * STRICT_HIP_LLM_LAYERS not "0" when the model is created). */
 SH_API int sh_llm_tensor(sh_llm *model, const char *name, int layer, void **device_ptr,
                          size_t *bytes);
 /* Starts `batch` empty sequences (clears the KV lengths). */

@@ -73,7 +73,53 @@ struct EmbedArgs {
   const float *inv_freq = nullptr;     // Qwen3 RoPE inverse frequencies [half]
   float *rope = nullptr;               // [B][2][half]: cos, sin of pos * inv_freq
   int half = 0;
+  unsigned *epoch = nullptr;           // step counter of the decode-layers kernel (+1 here)
 };
+
+// ---- persistent decode-layers kernel (Qwen3, FP8 weights, head_dim 128) ----
+
+// Device pointers of one layer, read by the kernel from a device array.
+struct LayerPtrs {
+  const uint8_t *wqkv, *wo, *wup, *wdown;  // FP8 tiled (gate/up tiles interleaved)
+  const float *sqkv, *so, *sup, *sdown;    // per-row scales
+  const float *norm1, *norm2, *q_norm, *k_norm;
+  uint16_t *kcache, *vcache;               // [max_batch][kv_heads][max_pos][128] fp16
+};
+
+// Everything the kernel exchanges between workgroups within a step lives in
+// uncached device memory (x, qkv, part, attn, act, flags, counters, err):
+// a value stored there is visible to every CU once the store has completed,
+// without the whole-L2 write-back a device-scope fence costs.
+struct LayersArgs {
+  const LayerPtrs *layers = nullptr;  // [n_layers]
+  int n_layers = 0, B = 0, H = 0, heads = 0, kv_heads = 0, inter = 0, qkv_n = 0;
+  int max_pos = 0, splits = 1, chunk = 16;
+  float eps = 1e-6f, scale = 1.0f;     // RMSNorm epsilon, attention 1 / sqrt(d)
+  const int *pos = nullptr;            // [B] this step's position (embed kernel)
+  const float *rope = nullptr;         // [B][128]: cos | sin (embed kernel)
+  const unsigned *epoch = nullptr;     // this step's number (embed kernel)
+  float *x = nullptr;                  // [2][kMaxBatch][H]: layer input / output, after attention
+  float *qkv = nullptr;                // [kMaxBatch][qkv_n]
+  float *part = nullptr;               // [kMaxBatch][heads][splits][130] attention partials
+  uint16_t *attn = nullptr;            // [kMaxBatch][heads * 128]
+  uint16_t *act = nullptr;             // [kMaxBatch][inter]
+  unsigned *flags = nullptr;           // per layer: qkv | attention | o | gate_up | down items
+  int flags_per_layer = 0, fB = 0, fC = 0, fD = 0, fE = 0;
+  unsigned *counters = nullptr;        // [n_layers][kMaxBatch][kv_heads] split arrivals
+  unsigned *err = nullptr;             // set when a wait timed out (sticky)
+  unsigned long long spin_ticks = 0;   // wall-clock ticks a wait may take
+  int lds_misc = 0;                    // byte offset of the small LDS scratch words
+};
+
+// Model shapes the kernel is instantiated for (16-byte weight loads per lane
+// of the qkv, o, gate/up and down items) and the query heads per KV head.
+// Returns false for any other shape (the runner then keeps per-op kernels).
+bool decode_layers_supported(int H, int heads, int kv_heads, int head_dim, int inter);
+size_t decode_layers_lds(int B, int H, int heads, int inter, int *misc_offset);
+// Workgroups of the kernel resident per CU with `lds` bytes of LDS (>= 1 to use it).
+hipError_t decode_layers_occupancy(const LayersArgs &a, size_t lds, int *blocks_per_cu);
+// Cooperative launch (all `grid` workgroups resident together) on stream s.
+hipError_t launch_decode_layers(hipStream_t s, const LayersArgs &a, int grid, size_t lds);
 
 // Lets every GEMV instantiation use up to 160 KiB of dynamic LDS (current device).
 hipError_t prepare_gemv_kernels();

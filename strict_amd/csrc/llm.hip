@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -75,6 +76,14 @@ struct sh_llm {
   hipGraphExec_t graph[2] = {nullptr, nullptr};
   int graph_batch[2] = {-1, -1};
   bool use_graphs = true;  // STRICT_HIP_LLM_GRAPHS=0: enqueue every step eagerly
+  // persistent decode-layers kernel (Qwen3 shapes it is built for;
+  // STRICT_HIP_LLM_LAYERS=0 keeps the per-op kernels)
+  bool layers_kernel = false;
+  LayersArgs la{};
+  int layers_grid = 0;
+  size_t layers_lds = 0;
+  unsigned *epoch = nullptr;
+  std::vector<void *> uc_blocks;  // uncached blocks taken from the process pool
 };
 
 namespace {
@@ -90,6 +99,61 @@ int llm_alloc(sh_llm *m, size_t bytes, void **p) {
   if (rc != SH_OK) return rc;
   SH_HIP_TRY(hipMemsetAsync(*p, 0, bytes, stream_of(m->ctx)));
   return SH_OK;
+}
+
+// Uncached device memory backs the decode-layers kernel's exchange buffers.
+// It is never freed (freeing uncached memory that kernels have read has
+// corrupted later allocations on this platform): a destroyed model returns
+// its blocks to this per-process pool, and the next model on the same device
+// takes them from it.
+struct UcBlock {
+  int device;
+  void *p;
+  size_t bytes;
+  bool used;
+};
+std::mutex g_uc_mu;
+std::vector<UcBlock> g_uc_pool;
+
+int uc_alloc(sh_llm *m, size_t bytes, void **p) {
+  *p = nullptr;
+  bytes = (bytes + 255) / 256 * 256;
+  const int dev = device_of(m->ctx);
+  {
+    std::lock_guard<std::mutex> lock(g_uc_mu);
+    UcBlock *best = nullptr;
+    for (UcBlock &b : g_uc_pool)
+      if (!b.used && b.device == dev && b.bytes >= bytes && (!best || b.bytes < best->bytes)) best = &b;
+    if (best) {
+      best->used = true;
+      *p = best->p;
+      bytes = best->bytes;
+    }
+  }
+  if (!*p) {
+    SH_HIP_TRY(hipExtMallocWithFlags(p, bytes, hipDeviceMallocUncached));
+    std::lock_guard<std::mutex> lock(g_uc_mu);
+    g_uc_pool.push_back(UcBlock{dev, *p, bytes, true});
+  }
+  m->uc_blocks.push_back(*p);
+  SH_HIP_TRY(hipMemsetAsync(*p, 0, bytes, stream_of(m->ctx)));
+  return SH_OK;
+}
+
+template <class T>
+int uc_alloc_n(sh_llm *m, size_t n, T **p) {
+  void *v = nullptr;
+  int rc = uc_alloc(m, n * sizeof(T), &v);
+  *p = static_cast<T *>(v);
+  return rc;
+}
+
+void uc_release(sh_llm *m) {
+  std::lock_guard<std::mutex> lock(g_uc_mu);
+  for (void *p : m->uc_blocks)
+    for (UcBlock &b : g_uc_pool)
+      if (b.p == p) b.used = false;
+  m->uc_blocks.clear();
 }
 
 template <class T>
@@ -162,9 +226,17 @@ int enqueue_step(sh_llm *m, bool logits) {
   e.inv_freq = m->inv_freq;
   e.rope = m->rope;
   e.half = d / 2;
+  float *x_final = m->x;
+  if (m->layers_kernel) {
+    e.x = m->la.x;  // layer input buffer of the decode-layers kernel
+    e.epoch = m->epoch;
+    x_final = m->la.x;
+  }
   SH_HIP_TRY(launch_embed(s, e, B));
 
+  if (m->layers_kernel) SH_HIP_TRY(launch_decode_layers(s, m->la, m->layers_grid, m->layers_lds));
   for (Layer &L : m->layers) {
+    if (m->layers_kernel) break;  // every layer ran in the kernel above
     GemvArgs g;
     g.w = L.qkv.w;
     g.scale = L.qkv.scale;
@@ -248,7 +320,7 @@ int enqueue_step(sh_llm *m, bool logits) {
 
   if (logits) {
     GemvArgs nrm;
-    nrm.x = m->x;
+    nrm.x = x_final;
     nrm.x_ld = H;
     nrm.gamma = m->final_g;
     nrm.beta = m->final_b;
@@ -272,6 +344,73 @@ int enqueue_step(sh_llm *m, bool logits) {
     h.argmax = m->keys;
     SH_HIP_TRY(launch_gemv(s, h, m->wtype, kProNone, kEpiLogits, 2048));
   }
+  return SH_OK;
+}
+
+// Sets up the decode-layers kernel when the model's shape and the device
+// allow it; otherwise the per-op kernels stay in use.
+int setup_layers_kernel(sh_llm *m) {
+  const sh_llm_config &c = m->cfg;
+  const char *env = getenv("STRICT_HIP_LLM_LAYERS");
+  if (env && env[0] == '0') return SH_OK;
+  if (!m->qwen ||
+      !decode_layers_supported(c.hidden, c.heads, c.kv_heads, c.head_dim, c.intermediate))
+    return SH_OK;
+  const int dev = device_of(m->ctx);
+  int coop = 0, cus = 0, clock_khz = 0;
+  SH_HIP_TRY(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
+  SH_HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  SH_HIP_TRY(hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeWallClockRate, dev));
+  if (!coop || cus <= 0 || clock_khz <= 0) return SH_OK;
+  LayersArgs &a = m->la;
+  a.n_layers = c.layers;
+  a.H = c.hidden;
+  a.heads = c.heads;
+  a.kv_heads = c.kv_heads;
+  a.inter = c.intermediate;
+  a.qkv_n = m->qkv_n;
+  a.max_pos = c.max_positions;
+  a.eps = c.norm_eps;
+  a.scale = 1.0f / std::sqrt((float)c.head_dim);
+  a.pos = m->pos;
+  a.rope = m->rope;
+  a.spin_ticks = (unsigned long long)clock_khz * 50;  // 50 ms per wait
+  int misc = 0;
+  const size_t lds = decode_layers_lds(c.max_batch, c.hidden, c.heads, c.intermediate, &misc);
+  int per_cu = 0;
+  SH_HIP_TRY(decode_layers_occupancy(a, lds, &per_cu));
+  if (per_cu < 1) return SH_OK;
+  const int nA = m->qkv_n / 16, nC = c.hidden / 16, nD = c.intermediate / 16;
+  a.fB = nA;
+  a.fC = a.fB + kMaxBatch * c.kv_heads;
+  a.fD = a.fC + nC;
+  a.fE = a.fD + nD;
+  a.flags_per_layer = a.fE + nC;
+  int rc;
+  if ((rc = uc_alloc_n(m, (size_t)2 * kMaxBatch * c.hidden, &a.x)) ||
+      (rc = uc_alloc_n(m, (size_t)kMaxBatch * m->qkv_n, &a.qkv)) ||
+      (rc = uc_alloc_n(m, (size_t)kMaxBatch * c.heads * 64 * (c.head_dim + 2), &a.part)) ||
+      (rc = uc_alloc_n(m, (size_t)kMaxBatch * c.heads * c.head_dim, &a.attn)) ||
+      (rc = uc_alloc_n(m, (size_t)kMaxBatch * c.intermediate, &a.act)) ||
+      (rc = uc_alloc_n(m, (size_t)c.layers * a.flags_per_layer, &a.flags)) ||
+      (rc = uc_alloc_n(m, (size_t)c.layers * kMaxBatch * c.kv_heads, &a.counters)) ||
+      (rc = uc_alloc_n(m, 64, &a.err)) || (rc = alloc_n(m, 64, &m->epoch)))
+    return rc;
+  LayerPtrs *dl = nullptr;
+  if ((rc = alloc_n(m, (size_t)c.layers, &dl))) return rc;
+  std::vector<LayerPtrs> hl(c.layers);
+  for (int i = 0; i < c.layers; i++) {
+    const Layer &L = m->layers[i];
+    hl[i] = LayerPtrs{L.qkv.w, L.o.w, L.up.w, L.down.w, L.qkv.scale, L.o.scale, L.up.scale,
+                      L.down.scale, L.norm1_g, L.norm2_g, L.q_norm, L.k_norm, L.kcache, L.vcache};
+  }
+  SH_HIP_TRY(hipMemcpyAsync(dl, hl.data(), hl.size() * sizeof(LayerPtrs), hipMemcpyHostToDevice,
+                            stream_of(m->ctx)));
+  SH_HIP_TRY(hipStreamSynchronize(stream_of(m->ctx)));
+  a.layers = dl;
+  a.epoch = m->epoch;
+  m->layers_grid = cus;
+  m->layers_kernel = true;
   return SH_OK;
 }
 
@@ -396,10 +535,12 @@ SH_API int sh_llm_create(sh_ctx *ctx, const sh_llm_config *config, sh_llm **out)
   const int max_splits = attention_splits(1, c.kv_heads, c.max_positions);
 
   auto cleanup = [&](int status) {
+    (void)hipStreamSynchronize(stream_of(ctx));
     for (void *p : m->allocs) {
       (void)sh_unregister_external(ctx, p);
       (void)hipFree(p);
     }
+    uc_release(m);
     delete m;
     return status;
   };
@@ -459,6 +600,7 @@ SH_API int sh_llm_create(sh_ctx *ctx, const sh_llm_config *config, sh_llm **out)
   hipError_t e = prepare_gemv_kernels();
   if (e == hipSuccess) e = hipStreamSynchronize(stream_of(ctx));
   if (e != hipSuccess) return cleanup(hip_fail(e, "preparing the model"));
+  if ((rc = setup_layers_kernel(m)) != SH_OK) return cleanup(rc);
   *out = m;
   return SH_OK;
 }
@@ -472,6 +614,7 @@ SH_API int sh_llm_destroy(sh_llm *m) {
     (void)sh_unregister_external(m->ctx, p);
     (void)hipFree(p);
   }
+  uc_release(m);
   delete m;
   return SH_OK;
 }
@@ -566,6 +709,8 @@ SH_API int sh_llm_tensor(sh_llm *m, const char *name, int layer, void **ptr, siz
   if (n == "final.b") return set(m->final_b, (size_t)c.hidden * 4);
   if (n == "wpe") return set(m->wpe, (size_t)c.max_positions * c.hidden * 2);
   if (n == "inv_freq") return set(m->inv_freq, (size_t)c.head_dim / 2 * 4);
+  // present only when the decode-layers kernel runs the layers
+  if (n == "layers.err") return set(m->layers_kernel ? m->la.err : nullptr, 4);
   if (layer < 0 || layer >= c.layers)
     return fail(SH_ERR_NOT_FOUND, "tensor '%s' layer %d not found", name, layer);
   Layer &L = m->layers[layer];
@@ -594,6 +739,23 @@ SH_API int sh_llm_reset(sh_llm *m, int batch) {
   m->splits = attention_splits(batch, m->cfg.kv_heads, m->cfg.max_positions);
   m->chunk = ((m->cfg.max_positions + m->splits - 1) / m->splits + 15) / 16 * 16;
   m->steps_done = 0;
+  if (m->layers_kernel) {
+    // splits per (row, KV head): as many as give every workgroup one item at
+    // batch 1, no split longer than kMaxSplitChunk, at most 64; independent
+    // of the batch, so a row's arithmetic does not depend on its batch
+    LayersArgs &a = m->la;
+    const sh_llm_config &c = m->cfg;
+    int sp = (m->layers_grid + c.kv_heads - 1) / c.kv_heads;
+    const int min_sp = (c.max_positions + kMaxSplitChunk - 1) / kMaxSplitChunk;
+    if (sp < min_sp) sp = min_sp;
+    if (sp > 64) sp = 64;
+    a.B = batch;
+    a.splits = sp;
+    a.chunk = ((c.max_positions + sp - 1) / sp + 15) / 16 * 16;
+    m->layers_lds = decode_layers_lds(batch, c.hidden, c.heads, c.intermediate, &a.lds_misc);
+    SH_HIP_TRY(hipMemsetAsync(a.counters, 0, (size_t)c.layers * kMaxBatch * c.kv_heads * 4, s));
+    SH_HIP_TRY(hipMemsetAsync(a.err, 0, 4, s));
+  }
   return SH_OK;
 }
 
@@ -616,7 +778,7 @@ SH_API int sh_llm_step(sh_llm *m, const int32_t *tokens, int want_logits) {
     SH_HIP_TRY(hipStreamSynchronize(s));  // `keys` is a stack array
   }
   const int g = want_logits ? 1 : 0;
-  if (!m->use_graphs) {
+  if (!m->use_graphs || m->layers_kernel) {
     if ((rc = enqueue_step(m, want_logits != 0)) != SH_OK) return rc;
   } else if (m->graph_batch[g] != m->batch) {
     if (m->graph[g]) (void)hipGraphExecDestroy(m->graph[g]);
@@ -651,7 +813,12 @@ SH_API int sh_llm_next_tokens(sh_llm *m, int32_t *tokens) {
   unsigned long long keys[kMaxBatch];
   hipStream_t s = stream_of(m->ctx);
   SH_HIP_TRY(hipMemcpyAsync(keys, m->keys, (size_t)m->batch * 8, hipMemcpyDeviceToHost, s));
+  unsigned err = 0;
+  if (m->layers_kernel)
+    SH_HIP_TRY(hipMemcpyAsync(&err, m->la.err, 4, hipMemcpyDeviceToHost, s));
   SH_HIP_TRY(hipStreamSynchronize(s));
+  if (err)
+    return fail(SH_ERR_HIP, "decode-layers kernel: a wait between workgroups timed out (step state lost; reset the model)");
   for (int b = 0; b < m->batch; b++) {
     if (keys[b] == 0) return fail(SH_ERR_INVALID_ARGUMENT, "no greedy token yet (step without logits?)");
     tokens[b] = (int32_t)(0xffffffffu - (uint32_t)(keys[b] & 0xffffffffu));

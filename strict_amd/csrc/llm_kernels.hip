@@ -20,12 +20,11 @@
 
 #include "common.h"
 #include "llm.h"
+#include "llm_device.h"
 
 namespace sh {
 namespace {
 
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kThreads = 256;
@@ -55,14 +54,6 @@ __device__ __forceinline__ uint8_t f32_to_e4m3(float f) {
   if (rest > 0x80000u || (rest == 0x80000u && (q & 1u))) q += 1;  // may carry into exponent
   if (q > 0x7e) q = 0x7e;  // 464 and up round to 448 after saturation
   return sign | (uint8_t)q;
-}
-
-__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
-  return __builtin_bit_cast(uint16_t, (_Float16)f);
-}
-
-__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
-  return (float)__builtin_bit_cast(_Float16, h);
 }
 
 // ---- tiled offsets -------------------------------------------------------
@@ -165,20 +156,6 @@ __global__ __launch_bounds__(kThreads) void f32_to_f16_kernel(const float *in, u
   if (i < n) out[i] = f32_to_f16_bits(in[i]);
 }
 
-// ---- block reductions ------------------------------------------------------
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
-}
-
 // ---- GEMV ---------------------------------------------------------------
 
 // Stages the MFMA A operand (activations of B rows, fp16, row stride K + 8
@@ -279,13 +256,6 @@ struct Stager {
   }
 };
 
-__device__ __forceinline__ float gelu_tanh(float x) {
-  const float c = 0.7978845608028654f;  // sqrt(2 / pi)
-  return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));
-}
-
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
-
 // Order-preserving key of an fp32 logit with its column: larger logits give
 // larger keys; among equal logits the smaller column wins (as argmax does).
 __device__ __forceinline__ unsigned long long argmax_key(float v, int n) {
@@ -348,12 +318,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvArgs a) {
         for (int j = 0; j < kNT; j++) {
           f16x8 bf;
           if (kW == kWeightFp8) {
-            const uint32_t d0 = r[u][j][2 * h], d1 = r[u][j][2 * h + 1];
-            const f16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, false);
-            const f16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, true);
-            const f16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, false);
-            const f16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, true);
-            bf = f16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+            bf = e4m3x8_to_f16(r[u][j][2 * h], r[u][j][2 * h + 1]);
           } else {
             bf = __builtin_bit_cast(f16x8, r[u][j]);
           }
@@ -837,6 +802,7 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const EmbedArgs a) {
     tok_s = tok;
     pos_s = pos;
     if (pos < a.hist_len) a.hist[(size_t)b * a.hist_len + pos] = tok;
+    if (a.epoch && b == 0) a.epoch[0] += 1u;
     a.pos[b] = pos;
     a.lens[b] = pos + 1;
     a.keys[b] = 0;

@@ -116,6 +116,14 @@ class Model:
                                      ctypes.byref(n)))
         return p.value, n.value
 
+    @property
+    def uses_layers_kernel(self) -> bool:
+        """True when one persistent kernel runs all layers of a step."""
+        p, n = ctypes.c_void_p(), ctypes.c_size_t()
+        status = self._l.sh_llm_tensor(self.handle, b"layers.err", 0, ctypes.byref(p),
+                                       ctypes.byref(n))
+        return status == 0
+
     def read(self, name: str, layer: int = 0, dtype=np.uint8) -> np.ndarray:
         ptr, nbytes = self.tensor(name, layer)
         out = np.empty(nbytes // np.dtype(dtype).itemsize, dtype)

@@ -170,10 +170,23 @@ def _greedy_check(model, prompt, steps, label):
 
 def test_qwen3_small_greedy_256(ctx):
     with llm.Model(ctx, QWEN_SMALL) as m:
+        assert m.uses_layers_kernel  # a shape the persistent kernel is built for
         m.init_random(seed=7, stddev=0.02)
         _randomize_small_params(m, 1)
         prompt = np.random.default_rng(3).integers(0, QWEN_SMALL.vocab, 16)
         _greedy_check(m, prompt, 256, "qwen3-small")
+
+
+def test_qwen3_small_per_op_kernels_greedy(ctx, monkeypatch):
+    # the per-op path (one kernel per GEMV / attention / merge), which shapes
+    # the persistent kernel is not built for take
+    monkeypatch.setenv("STRICT_HIP_LLM_LAYERS", "0")
+    with llm.Model(ctx, QWEN_SMALL) as m:
+        assert not m.uses_layers_kernel
+        m.init_random(seed=7, stddev=0.02)
+        _randomize_small_params(m, 1)
+        prompt = np.random.default_rng(3).integers(0, QWEN_SMALL.vocab, 16)
+        _greedy_check(m, prompt, 96, "qwen3-small-per-op")
 
 
 def test_gpt2_small_shape_greedy_256(ctx):
@@ -199,6 +212,7 @@ def test_qwen3_config4_greedy(ctx):
     # 4096-token KV cache is covered by test_qwen3_long_context_step)
     cfg = llm.QWEN3_0_6B.with_(max_positions=512)
     with llm.Model(ctx, cfg) as m:
+        assert m.uses_layers_kernel
         m.init_random(seed=42, stddev=0.02)
         prompt = np.random.default_rng(42).integers(0, cfg.vocab, 32)
         _greedy_check(m, prompt, 32, "qwen3-config4")
