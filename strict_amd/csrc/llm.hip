@@ -136,6 +136,8 @@ int uc_alloc(sh_llm *m, size_t bytes, void **p) {
     g_uc_pool.push_back(UcBlock{dev, *p, bytes, true});
   }
   m->uc_blocks.push_back(*p);
+  const int rc = sh_register_external(m->ctx, *p, bytes);  // readable with sh_download
+  if (rc != SH_OK) return rc;
   SH_HIP_TRY(hipMemsetAsync(*p, 0, bytes, stream_of(m->ctx)));
   return SH_OK;
 }
@@ -149,6 +151,7 @@ int uc_alloc_n(sh_llm *m, size_t n, T **p) {
 }
 
 void uc_release(sh_llm *m) {
+  for (void *p : m->uc_blocks) (void)sh_unregister_external(m->ctx, p);
   std::lock_guard<std::mutex> lock(g_uc_mu);
   for (void *p : m->uc_blocks)
     for (UcBlock &b : g_uc_pool)
@@ -389,7 +392,7 @@ int setup_layers_kernel(sh_llm *m) {
   int rc;
   if ((rc = uc_alloc_n(m, (size_t)2 * kMaxBatch * c.hidden, &a.x)) ||
       (rc = uc_alloc_n(m, (size_t)kMaxBatch * m->qkv_n, &a.qkv)) ||
-      (rc = uc_alloc_n(m, (size_t)kMaxBatch * c.heads * 64 * (c.head_dim + 2), &a.part)) ||
+      (rc = uc_alloc_n(m, (size_t)kMaxBatch * c.heads * 64 * (c.head_dim + 4), &a.part)) ||
       (rc = uc_alloc_n(m, (size_t)kMaxBatch * c.heads * c.head_dim, &a.attn)) ||
       (rc = uc_alloc_n(m, (size_t)kMaxBatch * c.intermediate, &a.act)) ||
       (rc = uc_alloc_n(m, (size_t)c.layers * a.flags_per_layer, &a.flags)) ||
