@@ -278,13 +278,13 @@ struct Lds {
   Misc *misc;
 };
 
-// A: qkv[b][16 i + c] = scale * (W_qkv RMSNorm(x))
+// A: qkv[b][16 i + c] = scale * (W_qkv RMSNorm(x)); w holds the item's
+// weights (load_weights, issued by the caller)
 template <int kL>
 __device__ bool qkv_item(const LayersArgs &a, const LayerPtrs &P, int i, unsigned epoch,
-                         const unsigned *wait_f, int wait_n, unsigned *flag, const Lds &s) {
+                         const unsigned *wait_f, int wait_n, unsigned *flag, const Lds &s,
+                         const u32x4 (&w)[kL][1]) {
   const int lane = threadIdx.x & 63, col = lane & 15;
-  u32x4 w[kL][1];
-  load_weights<kL, 1>(w, P.wqkv, a.H, i);
   const float sc = P.sqkv[i * 16 + col];
   __builtin_amdgcn_sched_barrier(0);
   if (!wait_flags(a, wait_f, wait_n, epoch, s.misc)) return false;
@@ -659,44 +659,43 @@ __device__ bool attn_item(const LayersArgs &a, const LayerPtrs &P, int l, int it
   __syncthreads();
   if (!misc->last) return true;
 
-  // merge (active <= splits <= kMaxSplits): split weights per head (wave g),
-  // then kGroups split groups of 16-byte column loads per thread
-  if (wave < kG) {
-    const int g = wave;
-    const size_t pp = ((size_t)b * a.heads + h0 + g) * splits * kPStride;
-    const int j = min(lane, active - 1);
-    float mj = xld_f32(a.part, pp + (size_t)j * kPStride + kD);
-    float lj = xld_f32(a.part, pp + (size_t)j * kPStride + kD + 1);
-    if (lane >= active) {
-      mj = -INFINITY;
-      lj = 0.0f;
-    }
-    const float M = wave_max_rows(mj);
-    const float wj = lane < active ? expf(mj - M) : 0.0f;
-    const float lw = wave_sum_rows(wj * lj);
-    S.mw[g][lane] = wj;
-    if (lane == 0) S.msum[g] = lw;
-  }
-  __syncthreads();
+  // merge (active <= splits <= kMaxSplits): every thread requests its split
+  // group's 16-byte columns and waves g < kG the split statistics together;
+  // then the split weights per head (wave g) and the weighted sums
   {
     constexpr int kQuads = kD / 4;               // 16-byte column groups per head
     constexpr int kGroups = kT / (kG * kQuads);  // split groups (4 for kG = 2, 8 for kG = 1)
+    constexpr int kPer = kMaxSplits / kGroups;   // splits per group at most
     const int g = t / (kGroups * kQuads), rem = t % (kGroups * kQuads);
     const int q = rem % kQuads, sg = rem / kQuads;
-    const size_t pp = ((size_t)b * a.heads + h0 + g) * splits * kPStride + q * 4;
+    const size_t base = ((size_t)b * a.heads + h0 + g) * splits * kPStride;
     const int n_my = (active - sg + kGroups - 1) / kGroups;  // splits sg, sg + kGroups, ...
-    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
-    for (int u0 = 0; u0 < n_my; u0 += 8) {
-      f32x4 xv[8];
+    f32x4 xv[kPer];
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const int j = min(sg + (u0 + u) * kGroups, active - 1);
-        xv[u] = __builtin_bit_cast(f32x4, xld16(a.part, (pp + (size_t)j * kPStride) * 4));
-      }
-#pragma unroll
-      for (int u = 0; u < 8; u++)
-        if (u0 + u < n_my) sum += S.mw[g][sg + (u0 + u) * kGroups] * xv[u];
+    for (int u = 0; u < kPer; u++) {
+      const int j = min(sg + u * kGroups, active - 1);  // unused slots reload a valid split
+      xv[u] = __builtin_bit_cast(f32x4, xld16(a.part, (base + (size_t)j * kPStride + q * 4) * 4));
     }
+    if (wave < kG) {
+      const size_t pw = ((size_t)b * a.heads + h0 + wave) * splits * kPStride;
+      const int j = min(lane, active - 1);
+      float mj = xld_f32(a.part, pw + (size_t)j * kPStride + kD);
+      float lj = xld_f32(a.part, pw + (size_t)j * kPStride + kD + 1);
+      if (lane >= active) {
+        mj = -INFINITY;
+        lj = 0.0f;
+      }
+      const float M = wave_max_rows(mj);
+      const float wj = lane < active ? expf(mj - M) : 0.0f;
+      const float lw = wave_sum_rows(wj * lj);
+      S.mw[wave][lane] = wj;
+      if (lane == 0) S.msum[wave] = lw;
+    }
+    __syncthreads();
+    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kPer; u++)
+      if (u < n_my) sum += S.mw[g][sg + u * kGroups] * xv[u];
     S.macc[sg][g][q] = sum;
     __syncthreads();
     if (sg == 0) {
@@ -734,13 +733,17 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
   const int nA = a.qkv_n / 16, nB = B * a.kv_heads * a.splits, nC = H / 16;
   const int nD = a.inter / 16, nE = H / 16;
   AttnKV kv;
+  u32x4 wa[kLA][1];  // this workgroup's first QKV item's weights
+  if (w < nA) load_weights<kLA, 1>(wa, a.layers[0].wqkv, H, w);
   for (int l = 0; l < a.n_layers; l++) {
     const LayerPtrs P = a.layers[l];
     unsigned *F = a.flags + (size_t)l * a.flags_per_layer;
     const unsigned *prevE = a.flags + (size_t)(l > 0 ? l - 1 : 0) * a.flags_per_layer + a.fE;
     if (w < nB) attn_prefetch(a, P, w, kv);  // streams while the QKV items run
-    for (int i = w; i < nA; i += G)
-      if (!qkv_item<kLA>(a, P, i, epoch, prevE, l > 0 ? nE : 0, F + i, lds)) return;
+    for (int i = w; i < nA; i += G) {
+      if (i != w) load_weights<kLA, 1>(wa, P.wqkv, H, i);
+      if (!qkv_item<kLA>(a, P, i, epoch, prevE, l > 0 ? nE : 0, F + i, lds, wa)) return;
+    }
     for (int i = w; i < nB; i += G) {
       if (i != w) attn_prefetch(a, P, i, kv);
       if (!attn_item<kG>(a, P, l, i, epoch, F, F + a.fB, smem, misc, kv)) return;
@@ -749,6 +752,8 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
       if (!o_item<kLC>(a, P, i, epoch, F + a.fB, B * a.kv_heads, F + a.fC + i, lds)) return;
     for (int i = (w + G - nC % G) % G; i < nD; i += G)
       if (!up_item<kLD>(a, P, i, epoch, F + a.fC, nC, F + a.fD + i, lds)) return;
+    // the next layer's first QKV weights, before the down items wait
+    if (l + 1 < a.n_layers && w < nA) load_weights<kLA, 1>(wa, a.layers[l + 1].wqkv, H, w);
     for (int i = w; i < nE; i += G)
       if (!down_item<kLE>(a, P, i, epoch, F + a.fD, nD, F + a.fE + i, lds)) return;
   }

@@ -345,7 +345,7 @@ int enqueue_step(sh_llm *m, bool logits) {
     h.out = m->logits;
     h.out_ld = m->vocab_pad;
     h.argmax = m->keys;
-    SH_HIP_TRY(launch_gemv(s, h, m->wtype, kProNone, kEpiLogits, 2048));
+    SH_HIP_TRY(launch_gemv(s, h, m->wtype, kProNone, kEpiLogits, 0));
   }
   return SH_OK;
 }

@@ -411,7 +411,12 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvArgs a) {
         k = o > k ? o : k;
       }
       const int b = 4 * (lane >> 4) + r;
-      if ((lane & 15) == 0 && b < B && k != 0) atomicMax(a.argmax + b, k);
+      // most workgroups finish below the running maximum: read it first and
+      // only those above it update (one device-scope read instead of an
+      // atomic that serialises with every other workgroup's)
+      if ((lane & 15) == 0 && b < B && k != 0 &&
+          k > __hip_atomic_load(a.argmax + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+        atomicMax(a.argmax + b, k);
     }
   }
 }
