@@ -40,6 +40,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, published
 BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA, published
+FP8_PEAK_TFLOPS = 5000.0    # MI355X dense fp8 MFMA, published
 IMG_W = IMG_H = 4096
 IMG_BYTES = IMG_W * IMG_H * 4
 SIGMOID_N = 1 << 24
@@ -221,6 +222,31 @@ def gemm_kernel(ctx, rng):
     e = {"kernel": "gemm_bf16 4096^3 (configs[2])", "alg_flop": flop, "avg_ms": round(avg, 5),
          "TFLOP/s": round(tflops, 1), "frac_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4)}
     log(f"gemm: {e}")
+    return e
+
+
+def gemm_fp8_kernel(ctx, rng):
+    """FP8 E4M3 GEMM 4096^3, per-row / per-column scales, bf16 output."""
+    qa = rng.integers(0, 256, (GEMM_N, GEMM_N), dtype=np.uint8)
+    qa[(qa & 0x7f) == 0x7f] = 0  # no NaN codes
+    qb = rng.integers(0, 256, (GEMM_N, GEMM_N), dtype=np.uint8)
+    qb[(qb & 0x7f) == 0x7f] = 0
+    s = rng.uniform(0.5, 1.5, GEMM_N).astype(np.float32)
+    dA, dB, dS = ctx.upload(qa), ctx.upload(qb), ctx.upload(s)
+    dC = ctx.empty((GEMM_N, GEMM_N), np.uint16)
+
+    def gemm(k):
+        ctx.gemm_fp8(dA, dS, dB, dS, dC, GEMM_N, GEMM_N, GEMM_N)
+
+    _, avg, _ = time_launches(ctx, gemm, 20, 3)
+    for v in (dA, dB, dS, dC):
+        v.free()
+    flop = 2.0 * GEMM_N ** 3
+    tflops = flop / (avg * 1e-3) / 1e12
+    e = {"kernel": "gemm_fp8 e4m3 4096^3, row/column scales", "alg_flop": flop,
+         "avg_ms": round(avg, 5), "TFLOP/s": round(tflops, 1),
+         "frac_fp8_peak": round(tflops / FP8_PEAK_TFLOPS, 4)}
+    log(f"gemm_fp8: {e}")
     return e
 
 
@@ -430,6 +456,7 @@ def main() -> int:
         kernels.append(sig[0])
     if not args.no_extra:
         kernels.append(gemm_kernel(ctx, rng))
+        kernels.append(gemm_fp8_kernel(ctx, rng))
         kernels.append(gemv_kernel(ctx, rng, table_steps))
 
     if args.workload == "image":

@@ -249,6 +249,19 @@ SH_API int sh_brightness_blur5_u8(sh_ctx *ctx, const uint8_t *in, uint8_t *out, 
 SH_API int sh_gemm_bf16(sh_ctx *ctx, const uint16_t *A, const uint16_t *B, uint16_t *C, int M,
                         int N, int K, int lda, int ldb, int ldc);
 
+/* C[m,n] = bf16(sa[m] * sb[n] * sum_k e4m3(A[m,k]) * e4m3(Bt[n,k])): OCP E4M3
+ * bytes, fp32 accumulation, bf16 result (round to nearest even). A is
+ * row-major [M][K] (lda >= K bytes), B arrives transposed as Bt [N][K]
+ * (ldb >= K bytes; a weight matrix W[N][K]), C row-major (ldc >= N
+ * elements); sa (M floats) and sb (N floats) are the per-row / per-column
+ * scales sh_quantize_e4m3 produces. K == 0 writes zeros. The MFMA path needs
+ * M, N multiples of 256, K of 128, lda / ldb multiples of 16, 16-byte aligned
+ * A, Bt and sb; other shapes run a slower exact-fp32 kernel. No counterpart in
+ * the reference (BASELINE's FP8 GEMM measurement). */
+SH_API int sh_gemm_fp8(sh_ctx *ctx, const uint8_t *A, const float *sa, const uint8_t *Bt,
+                       const float *sb, uint16_t *C, int M, int N, int K, int lda, int ldb,
+                       int ldc);
+
 /* ---- weight quantization ------------------------------------------------------
  * No reference counterpart: BASELINE configs[4] fixes the format. */
 

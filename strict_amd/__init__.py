@@ -394,6 +394,14 @@ class Context:
                                     n if ldc is None else ldc))
 
 
+    def gemm_fp8(self, a, sa, bt, sb, c, m: int, n: int, k: int, lda: int | None = None,
+                 ldb: int | None = None, ldc: int | None = None) -> None:
+        """C[m,n] = sa[m] sb[n] (A[m,:] . Bt[n,:]); OCP E4M3 bytes A [m,k] and
+        Bt [n,k] (B transposed), fp32 scales, fp32 accumulation, bf16 result."""
+        _check(self._l.sh_gemm_fp8(self.handle, _ptr(a), _ptr(sa), _ptr(bt), _ptr(sb), _ptr(c),
+                                   m, n, k, k if lda is None else lda, k if ldb is None else ldb,
+                                   n if ldc is None else ldc))
+
     def quantize_e4m3(self, w, q, scales, n: int, k: int) -> None:
         """Per-row OCP E4M3 quantization of a device fp32 [n, k] matrix."""
         _check(self._l.sh_quantize_e4m3(self.handle, _ptr(w), n, k, _ptr(q), _ptr(scales)))

@@ -125,6 +125,7 @@ SIGNATURES = {
     "sh_box_blur5_u8": (_I, [_P, _P, _P, _I, _I, _I, _I]),
     "sh_brightness_blur5_u8": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I]),
     "sh_gemm_bf16": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I]),
+    "sh_gemm_fp8": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I]),
     "sh_quantize_e4m3": (_I, [_P, _P, _I, _I, _P, _P]),
     "sh_pack_e4m3_tiles": (_I, [_P, _P, _I, _I, _P]),
     "sh_gemv_w8a16": (_I, [_P, _P, _P, _P, _P, _I, _I, _I]),

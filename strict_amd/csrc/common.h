@@ -44,6 +44,11 @@ hipError_t launch_gemm_bf16(hipStream_t s, const uint16_t *A, const uint16_t *B,
                             int M, int N, int K, int lda, int ldb, int ldc);
 bool gemm_bf16_uses_mfma(int M, int N, int K, int lda, int ldb, int ldc, const void *A,
                          const void *B, const void *C);
+hipError_t launch_gemm_fp8(hipStream_t s, const uint8_t *A, const float *sa, const uint8_t *Bt,
+                           const float *sb, uint16_t *C, int M, int N, int K, int lda, int ldb,
+                           int ldc);
+bool gemm_fp8_uses_mfma(int M, int N, int K, int lda, int ldb, int ldc, const void *A,
+                        const void *Bt, const void *C, const void *sb);
 
 hipError_t launch_brightness_u8(hipStream_t s, const uint8_t *in, uint8_t *out, size_t bytes,
                                 int channels, int delta, int all_channels);

@@ -644,4 +644,28 @@ SH_API int sh_gemm_bf16(sh_ctx *ctx, const uint16_t *A, const uint16_t *B, uint1
   return launched(launch_gemm_bf16(ctx->stream, A, B, C, M, N, K, lda, ldb, ldc), "gemm_bf16");
 }
 
+SH_API int sh_gemm_fp8(sh_ctx *ctx, const uint8_t *A, const float *sa, const uint8_t *Bt,
+                       const float *sb, uint16_t *C, int M, int N, int K, int lda, int ldb,
+                       int ldc) {
+  SH_CHECK(enter(ctx));
+  if (M < 0 || N < 0 || K < 0)
+    return fail(SH_ERR_INVALID_ARGUMENT, "negative GEMM size M=%d N=%d K=%d", M, N, K);
+  if (lda < K || ldb < K || ldc < N)
+    return fail(SH_ERR_INVALID_ARGUMENT,
+                "leading dimensions too small: lda=%d (K=%d) ldb=%d (K=%d) ldc=%d (N=%d)", lda, K,
+                ldb, K, ldc, N);
+  if (M == 0 || N == 0) return SH_OK;
+  SH_CHECK(check_range(ctx, C, span_elems(M, N, ldc) * 2, "C"));
+  if (K == 0) {  // empty sum: C = 0
+    for (int m = 0; m < M; m++) SH_HIP_TRY(hipMemsetAsync(C + (size_t)m * ldc, 0, (size_t)N * 2, ctx->stream));
+    return SH_OK;
+  }
+  SH_CHECK(check_range(ctx, A, span_elems(M, K, lda), "A"));
+  SH_CHECK(check_range(ctx, Bt, span_elems(N, K, ldb), "Bt"));
+  SH_CHECK(check_range(ctx, sa, (size_t)M * 4, "sa"));
+  SH_CHECK(check_range(ctx, sb, (size_t)N * 4, "sb"));
+  return launched(launch_gemm_fp8(ctx->stream, A, sa, Bt, sb, C, M, N, K, lda, ldb, ldc),
+                  "gemm_fp8");
+}
+
 }  // extern "C"
