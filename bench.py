@@ -205,6 +205,22 @@ def sigmoid_kernel(ctx, rng, steps):
     return e, total, wall
 
 
+def library_gemm_ms(ctx, gemm):
+    """The same GEMM through hipBLASLt (STRICT_HIP_GEMM=blaslt), as a yardstick
+    for the hand-written kernel; None when the library has no algorithm."""
+    import strict_amd
+
+    os.environ["STRICT_HIP_GEMM"] = "blaslt"
+    try:
+        _, avg, _ = time_launches(ctx, gemm, 20, 3)
+        return round(avg, 5)
+    except strict_amd.StrictHipError as exc:
+        log(f"hipBLASLt GEMM: {exc}")
+        return None
+    finally:
+        del os.environ["STRICT_HIP_GEMM"]
+
+
 def gemm_kernel(ctx, rng):
     a = rng.normal(0, 0.02, (GEMM_N, GEMM_N)).astype(np.float32)
     b = rng.normal(0, 0.02, (GEMM_N, GEMM_N)).astype(np.float32)
@@ -215,12 +231,14 @@ def gemm_kernel(ctx, rng):
         ctx.gemm_bf16(dA, dB, dC, GEMM_N, GEMM_N, GEMM_N)
 
     _, avg, _ = time_launches(ctx, gemm, 20, 3)
+    lib = library_gemm_ms(ctx, gemm)
     for v in (dA, dB, dC):
         v.free()
     flop = 2.0 * GEMM_N ** 3
     tflops = flop / (avg * 1e-3) / 1e12
     e = {"kernel": "gemm_bf16 4096^3 (configs[2])", "alg_flop": flop, "avg_ms": round(avg, 5),
-         "TFLOP/s": round(tflops, 1), "frac_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4)}
+         "TFLOP/s": round(tflops, 1), "frac_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4),
+         "hipblaslt_avg_ms": lib}
     log(f"gemm: {e}")
     return e
 
@@ -239,13 +257,14 @@ def gemm_fp8_kernel(ctx, rng):
         ctx.gemm_fp8(dA, dS, dB, dS, dC, GEMM_N, GEMM_N, GEMM_N)
 
     _, avg, _ = time_launches(ctx, gemm, 20, 3)
+    lib = library_gemm_ms(ctx, gemm)
     for v in (dA, dB, dS, dC):
         v.free()
     flop = 2.0 * GEMM_N ** 3
     tflops = flop / (avg * 1e-3) / 1e12
     e = {"kernel": "gemm_fp8 e4m3 4096^3, row/column scales", "alg_flop": flop,
          "avg_ms": round(avg, 5), "TFLOP/s": round(tflops, 1),
-         "frac_fp8_peak": round(tflops / FP8_PEAK_TFLOPS, 4)}
+         "frac_fp8_peak": round(tflops / FP8_PEAK_TFLOPS, 4), "hipblaslt_avg_ms": lib}
     log(f"gemm_fp8: {e}")
     return e
 

@@ -50,6 +50,16 @@ hipError_t launch_gemm_fp8(hipStream_t s, const uint8_t *A, const float *sa, con
 bool gemm_fp8_uses_mfma(int M, int N, int K, int lda, int ldb, int ldc, const void *A,
                         const void *Bt, const void *C, const void *sb);
 
+// hipBLASLt backend (blas.cpp), used only with STRICT_HIP_GEMM=blaslt:
+// SH_OK when it ran the product, SH_ERR_UNSUPPORTED when the caller should
+// launch its own kernel, another status on a library failure.
+int blaslt_gemm_bf16(sh_ctx *ctx, hipStream_t s, const uint16_t *A, const uint16_t *B, uint16_t *C,
+                     int M, int N, int K, int lda, int ldb, int ldc);
+int blaslt_gemm_fp8(sh_ctx *ctx, hipStream_t s, const uint8_t *A, const float *sa,
+                    const uint8_t *Bt, const float *sb, uint16_t *C, int M, int N, int K, int lda,
+                    int ldb, int ldc);
+void blaslt_release(sh_ctx *ctx);
+
 hipError_t launch_brightness_u8(hipStream_t s, const uint8_t *in, uint8_t *out, size_t bytes,
                                 int channels, int delta, int all_channels);
 hipError_t launch_blur5_u8(hipStream_t s, const uint8_t *in, uint8_t *out, int width, int height,

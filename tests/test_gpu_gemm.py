@@ -109,3 +109,13 @@ def test_gemm_rejects_bad_arguments(ctx):
     with pytest.raises(strict_amd.StrictHipError):
         ctx.gemm_bf16(buf, buf, buf, 128, 64, 64)  # A does not fit its buffer
     buf.free()
+
+
+@pytest.mark.parametrize("m,n,k", [(4096, 4096, 4096), (512, 768, 384)])
+def test_gemm_hipblaslt_backend(ctx, monkeypatch, m, n, k):
+    # the library yardstick behind STRICT_HIP_GEMM=blaslt, same bar
+    monkeypatch.setenv("STRICT_HIP_GEMM", "blaslt")
+    a, b = _bf16_operands(m, n, k, seed=11)
+    c = _run(ctx, a, b, m, n, k)
+    rows = np.random.default_rng(2).choice(m, 48, replace=False)
+    _check(c[rows], oracle.gemm_f32(oracle.bf16_to_f32(a)[rows], oracle.bf16_to_f32(b)))

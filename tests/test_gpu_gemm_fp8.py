@@ -121,3 +121,13 @@ def test_gemm_fp8_k0_and_bad_arguments(ctx):
     with pytest.raises(strict_amd.StrictHipError) as e:
         ctx.gemm_fp8(a, s, a, s, c, m, n, 64, 32, 64, n)  # lda < K
     assert e.value.status == strict_amd._lib.SH_ERR_INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("m,n,k", [(4096, 4096, 4096), (512, 768, 384)])
+def test_gemm_fp8_hipblaslt_backend(ctx, monkeypatch, m, n, k):
+    # the library yardstick behind STRICT_HIP_GEMM=blaslt, same bar
+    monkeypatch.setenv("STRICT_HIP_GEMM", "blaslt")
+    qa, sa, qb, sb = _operands(m, n, k, seed=13)
+    c = _run(ctx, qa, sa, qb, sb, m, n, k)
+    rows = np.random.default_rng(2).choice(m, 48, replace=False)
+    _check(c[rows], _reference(qa[rows], sa[rows], qb, sb))
