@@ -8,7 +8,11 @@ from __future__ import annotations
 import ctypes
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libstrict_hip.so"
+import os
+
+# STRICT_HIP_LIBRARY names another build of the library (e.g. a diagnostic one)
+LIB_PATH = Path(os.environ.get("STRICT_HIP_LIBRARY") or
+                Path(__file__).resolve().parent / "libstrict_hip.so")
 
 SH_OK = 0
 SH_ERR_INVALID_ARGUMENT = 1

@@ -5,23 +5,34 @@
 //
 // Work per layer, as items spread over the workgroups:
 //   A  QKV     one 16-row tile of W_qkv each      (RMSNorm of x in every item)
-//   B  attn    one (row, KV head, split) each      (q/k norm, RoPE, cache append;
-//              the last split of a (row, KV head) to arrive merges the partials)
+//   B  attn    one (row, KV head, split) each      (q/k norm, RoPE, cache append)
+//   M  merge   one (row, query head) each          (combines the split partials)
 //   C  O       one 16-row tile of W_o each         (x_mid = x + W_o attn)
 //   D  gate/up one gate tile + up tile pair each   (RMSNorm of x_mid, SwiGLU)
 //   E  down    one 16-row tile of W_down each      (x = x_mid + W_down act)
-// An item publishes its output with device-coherent stores, waits for them
-// to complete, then stores the step number into its flag word; an item that
-// needs it polls those flags (one wave, one vector load per poll) before
-// reading. Weights and K / V do not depend on the step's activations, so they
-// are requested before the wait: an item's weights when it starts, a
-// workgroup's first attention item's K / V at the start of the layer (they
-// then stream while the QKV items run).
+//
+// Exchange between workgroups: every value an item hands on travels in an
+// 8-byte cell of uncached device memory, payload in the low word and the
+// producing (step, layer) tag in the high word, written by one 8-byte (or
+// 16-byte, two-cell) store. A consumer loads the cells it needs until each
+// carries the tag it expects. The data is its own completion flag: a
+// producer never waits for its stores to complete, and a consumer needs one
+// memory round trip once the data has landed (a flag word would cost the
+// producer's store-completion wait, the flag poll and then the data read).
+// Relaxed 64-bit agent-scope atomic loads do the polling: the compiler
+// neither hoists them out of the spin loop nor waits after each one.
+//
+// Weights and K / V do not depend on the step's activations, so each
+// workgroup requests them for its next items right after it has finished
+// polling for the current one (the loads then arrive while the previous
+// phase's producers run). Loads complete in issue order, so a poll issued
+// after a bulk request returns no earlier than that request: requests are
+// placed where the workgroup's next poll is at least one exchange away.
+//
 // Every wait is bounded by a wall-clock limit; a timeout sets the sticky
 // error word, after which every other wait fails at once, so the grid always
-// drains. Items of C and E sit on workgroups 0.., those of D after them, so
-// the workgroups without an o / down item prefetch gate/up and next-layer
-// QKV weights while those run.
+// drains. Items of C and E sit on workgroups 0.., those of D after them and
+// the merge items on the last workgroups.
 //
 // With one wave per SIMD nothing hides an instruction's latency, so the item
 // code avoids runtime integer division, LDS-based lane shuffles in its
@@ -38,94 +49,135 @@ namespace {
 constexpr int kT = 256;         // threads per workgroup (4 waves)
 constexpr int kD = 128;         // head dim
 constexpr int kAttnBatch = 10;  // 16-position block steps of K / V requested ahead
-constexpr int kMaxSplits = 64;  // the merge reads one split per lane
-constexpr int kPStride = kD + 4;  // floats per attention partial: acc[128], m, l, pad
-constexpr int kRowsPerPass = 4;   // batch rows staged together
+constexpr int kMaxSplits = 64;  // splits per (row, KV head) a merge item combines
+constexpr int kMaxRowsPerPass = 4;  // batch rows staged together (1 at batch 1)
 
-__device__ __forceinline__ unsigned ld_flag(const unsigned *p) {
+// ---- exchange cells ------------------------------------------------------------
+
+// Tag of the values layer l of step `epoch` produces (epoch >= 1, l < 63, so
+// never 0, the value of never-written cells).
+__device__ __forceinline__ unsigned tag_of(unsigned epoch, int l) {
+  return epoch * 64u + (unsigned)l + 1u;
+}
+
+__device__ __forceinline__ uint64_t cld(const uint64_t *base, size_t cell) {
+  return __hip_atomic_load(base + cell, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ unsigned ld_err(const unsigned *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void st_flag(unsigned *p, unsigned v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Cell stores are relaxed agent-scope atomics (global stores with the
+// device-scope cache policy): once complete they are visible to every CU.
+__device__ __forceinline__ void cst1(uint64_t *base, size_t cell, uint32_t v, unsigned tag) {
+  __hip_atomic_store(base + cell, (uint64_t)v | ((uint64_t)tag << 32), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Accesses to the exchange buffers (x, qkv, part, attn, act) go through
-// buffer instructions with the device-scope cache policy (sc1), like the
-// flags: a load never returns a stale copy held by this CU's vector cache or
-// this XCD's L2, and a store is visible to every CU once it has completed.
-// Offsets are bytes from the buffer start (the buffers are far below 2 GiB).
-constexpr int kDeviceScope = 16;  // cache-policy bit sc1
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t xrsrc(const void *base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7fffffff,
-                                           0x00020000);
+__device__ __forceinline__ void cst2(uint64_t *base, size_t cell, uint32_t v0, uint32_t v1,
+                                     unsigned tag) {
+  cst1(base, cell, v0, tag);
+  cst1(base, cell + 1, v1, tag);
 }
 
-__device__ __forceinline__ u32x4 xld16(const void *base, size_t byte_off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(xrsrc(base), (int)byte_off, 0, kDeviceScope);
+__device__ __forceinline__ float f32_of(uint32_t u) { return __builtin_bit_cast(float, u); }
+__device__ __forceinline__ uint32_t bits_of(float f) { return __builtin_bit_cast(uint32_t, f); }
+
+// Loads the cells base[at(k)], k < kN, until each one with bit k of mask
+// set carries `tag`; c[k] receives them (payload in the low word). at(k)
+// must name a valid cell for every k (callers clamp the unused ones onto
+// used cells, so the loads need no branches). False when the wait exceeded
+// the limit or another wait has failed.
+template <int kN, class At>
+__device__ __forceinline__ bool spin_cells(const LayersArgs &a, const uint64_t *base, At at,
+                                           uint64_t mask, unsigned tag, uint64_t (&c)[kN]) {
+  unsigned long long t0 = 0;
+  for (int it = 0;; it++) {
+#pragma unroll
+    for (int k = 0; k < kN; k++) c[k] = cld(base, at(k));
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < kN; k++) ok = ok && ((mask >> k & 1) == 0 || (uint32_t)(c[k] >> 32) == tag);
+    if (ok) return true;
+    if (it == 0) {
+      t0 = wall_clock64();
+    } else if ((it & 7) == 0 && (ld_err(a.err) != 0 || wall_clock64() - t0 > a.spin_ticks)) {
+      return false;
+    }
+  }
 }
 
-__device__ __forceinline__ float xld_f32(const float *base, size_t i) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_raw_buffer_load_b32(xrsrc(base), (int)(i * 4), 0, kDeviceScope));
-}
+__device__ __forceinline__ float cell_f32(uint64_t c) { return __builtin_bit_cast(float, (uint32_t)c); }
 
-__device__ __forceinline__ void xst_f32(float *base, size_t i, float v) {
-  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), xrsrc(base), (int)(i * 4),
-                                        0, kDeviceScope);
-}
-
-__device__ __forceinline__ void xst_u16(uint16_t *base, size_t i, uint16_t v) {
-  __builtin_amdgcn_raw_buffer_store_b16(v, xrsrc(base), (int)(i * 2), 0, kDeviceScope);
-}
-
-__device__ __forceinline__ void xst_u64(void *base, size_t byte_off, uint64_t v) {
-  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), xrsrc(base), (int)byte_off,
-                                        0, kDeviceScope);
+// One cell already requested as `c`: polls it again until it carries `tag`.
+__device__ __forceinline__ bool finish_cell(const LayersArgs &a, const uint64_t *base, size_t cell,
+                                            unsigned tag, uint64_t &c) {
+  unsigned long long t0 = 0;
+  for (int it = 0; (uint32_t)(c >> 32) != tag; it++) {
+    if (it == 0) {
+      t0 = wall_clock64();
+    } else if ((it & 7) == 0 && (ld_err(a.err) != 0 || wall_clock64() - t0 > a.spin_ticks)) {
+      return false;
+    }
+    c = cld(base, cell);
+  }
+  return true;
 }
 
 // Small LDS words after the phase areas.
 struct Misc {
-  int ok;                               // result of the last wait
-  int last;                             // this attention item merges
-  float part[4][kRowsPerPass];          // per-wave partial sums of squares
+  float part[4][kMaxRowsPerPass];          // per-wave partial sums of squares
+#ifdef SH_DECODE_TRACE
+  unsigned long long t_wait;            // when the last wait ended
+#endif
 };
 
-// True once flags [f, f + n) all hold `epoch`. Wave 0 polls; the result is
-// shared through LDS, so all threads return the same value.
-__device__ bool wait_flags(const LayersArgs &a, const unsigned *f, int n, unsigned epoch,
-                           Misc *misc) {
-  if (n <= 0) return true;
-  const int t = threadIdx.x, lane = t & 63;
-  __syncthreads();  // every thread has read the previous wait's result
-  if (t < 64) {
-    const unsigned long long t0 = wall_clock64();
-    int ok = 1;
-    for (int it = 1;; it++) {
-      int mine = 1;
-      for (int i = lane; i < n; i += 64) mine &= ld_flag(f + i) == epoch ? 1 : 0;
-      if (__all(mine)) break;
-      if ((it & 15) == 0 && (ld_flag(a.err) != 0 || wall_clock64() - t0 > a.spin_ticks)) {
-        ok = 0;
-        break;
-      }
-    }
-    if (lane == 0) {
-      misc->ok = ok;
-      if (!ok) atomicOr(a.err, 1u);
-    }
+// Every thread's wait succeeded (block-uniform); otherwise marks the error.
+__device__ __forceinline__ bool waits_ok(const LayersArgs &a, bool ok, Misc *misc) {
+  if (__syncthreads_or(ok ? 0 : 1)) {
+    if (threadIdx.x == 0) atomicOr(a.err, 1u);
+    return false;
   }
-  __syncthreads();
-  return misc->ok != 0;
+#ifdef SH_DECODE_TRACE
+  if (threadIdx.x == 0) misc->t_wait = wall_clock64();
+#else
+  (void)misc;
+#endif
+  return true;
 }
 
-// Completes this workgroup's stores, then marks the item done.
-__device__ __forceinline__ void publish(unsigned *flag, unsigned epoch) {
-  __builtin_amdgcn_s_waitcnt(0);  // every store of this thread has completed
-  __syncthreads();
-  if (threadIdx.x == 0) st_flag(flag, epoch);
+#ifdef SH_DECODE_TRACE
+// Timeline of one step (diagnostic builds only): per workgroup and layer,
+// the wall clock at each phase's start (even slots 0..8: QKV, attention, O,
+// gate/up, down) and end (odd slots), when its wait ended (10..14) and when
+// the merge item ended (15).
+constexpr int kTraceWgs = 256, kTraceLayers = 32, kTraceSlots = 16;
+__device__ unsigned long long g_decode_trace[kTraceWgs][kTraceLayers][kTraceSlots];
+__device__ __forceinline__ void trace_mark(int l, int slot) {
+  if (threadIdx.x == 0 && blockIdx.x < kTraceWgs && l < kTraceLayers)
+    g_decode_trace[blockIdx.x][l][slot] = wall_clock64();
 }
+// Finer marks inside items: QKV 0..3 (staged, MFMA, reduced, stored), down
+// 4..7, attention 8..13 (q/k/v polled, RoPE, scores, softmax, V sums,
+// stored), merge 14..15 (polled, stored).
+__device__ unsigned long long g_decode_trace2[kTraceWgs][kTraceLayers][kTraceSlots];
+__device__ __forceinline__ void trace_mark2(int l, int slot) {
+  if (threadIdx.x == 0 && blockIdx.x < kTraceWgs && l < kTraceLayers)
+    g_decode_trace2[blockIdx.x][l][slot] = wall_clock64();
+}
+#define SH_MARK(l, slot) trace_mark2(l, slot)
+#define SH_TRACE(l, slot) trace_mark(l, slot)
+#define SH_TRACE_WAIT(l, ph, misc)                                                        \
+  do {                                                                                    \
+    if (threadIdx.x == 0 && blockIdx.x < kTraceWgs && (l) < kTraceLayers)                 \
+      g_decode_trace[blockIdx.x][l][10 + (ph)] = (misc)->t_wait;                          \
+  } while (0)
+#else
+#define SH_TRACE(l, slot) ((void)0)
+#define SH_MARK(l, slot) ((void)0)
+#define SH_TRACE_WAIT(l, ph, misc) ((void)0)
+#endif
 
 // ---- GEMV items ----------------------------------------------------------------
 
@@ -190,58 +242,61 @@ __device__ __forceinline__ void reduce_waves(f32x4 (&acc)[kNT], float *red) {
   }
 }
 
-// fp16 rows [B][K] of an exchange buffer (row stride ld) -> xs (row stride
-// K + 8); kChunks >= K / 8 / 256 16-byte chunks per thread and row.
-template <int kChunks>
-__device__ void stage_f16(const uint16_t *src, int ld, int B, int K, _Float16 *xs) {
-  const int c8 = K >> 3, t = threadIdx.x;
-  for (int b0 = 0; b0 < B; b0 += kRowsPerPass) {
-    u32x4 v[kRowsPerPass][kChunks];
-#pragma unroll
-    for (int r = 0; r < kRowsPerPass; r++)
-#pragma unroll
-      for (int j = 0; j < kChunks; j++) {
-        const int c = min(t + kT * j, c8 - 1);
-        v[r][j] = u32x4{0u, 0u, 0u, 0u};
-        if (b0 + r < B) v[r][j] = xld16(src, ((size_t)(b0 + r) * ld + c * 8) * 2);  // uniform
-      }
-#pragma unroll
-    for (int r = 0; r < kRowsPerPass; r++)
-#pragma unroll
-      for (int j = 0; j < kChunks; j++) {
-        const int b = b0 + r, c = t + kT * j;
-        if (b < B && c < c8) *reinterpret_cast<u32x4 *>(xs + b * (K + 8) + c * 8) = v[r][j];
-      }
-  }
-  __syncthreads();
-}
-
-// fp32 rows [B][K] at element x_off of the exchange buffer x (row stride ld)
-// -> RMSNorm with gains g -> xs (fp16, row stride K + 8). Each thread keeps
-// its 4-float chunks in registers; the per-row sums of squares are combined
-// across the four waves through LDS. kChunks >= K / 4 / 256.
-template <int kChunks>
-__device__ void stage_rms(const float *x, size_t x_off, int ld, const float *g, int B, int K,
-                          float eps, _Float16 *xs, Misc *misc) {
+// Rows [B][K] of fp32 x -> RMSNorm with gains g -> xs (fp16, row stride
+// K + 8), kRows rows per pass. The rows come from cells xc tagged `tag` or,
+// for the first layer, from the plain buffer xp the embedding kernel wrote
+// before this launch. Each thread keeps its 4-value chunks in registers;
+// the per-row sums of squares are combined across the four waves through
+// LDS. kChunks >= K / 4 / 256.
+template <int kChunks, int kRows>
+__device__ bool stage_rms(const LayersArgs &a, const uint64_t *xc, const float *xp, unsigned tag,
+                          const float *g, int K, _Float16 *xs, Misc *misc) {
   typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-  const int c4 = K >> 2, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  constexpr int kN = kRows * kChunks * 4;
+  static_assert(kN <= 64, "cells per thread");
+  const int B = a.B, c4 = K >> 2, t = threadIdx.x, lane = t & 63, wave = t >> 6;
   f32x4 gv[kChunks];
 #pragma unroll
   for (int j = 0; j < kChunks; j++)
     gv[j] = *reinterpret_cast<const f32x4 *>(g + min(t + kT * j, c4 - 1) * 4);
-  for (int b0 = 0; b0 < B; b0 += kRowsPerPass) {
-    f32x4 v[kRowsPerPass][kChunks];
+  for (int b0 = 0; b0 < B; b0 += kRows) {
+    f32x4 v[kRows][kChunks];
+    bool ok = true;
+    if (xp) {
 #pragma unroll
-    for (int r = 0; r < kRowsPerPass; r++)
+      for (int r = 0; r < kRows; r++)
 #pragma unroll
-      for (int j = 0; j < kChunks; j++) {
-        const int c = min(t + kT * j, c4 - 1);
-        v[r][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (b0 + r < B)  // uniform
-          v[r][j] = __builtin_bit_cast(f32x4, xld16(x, (x_off + (size_t)(b0 + r) * ld + c * 4) * 4));
-      }
+        for (int j = 0; j < kChunks; j++) {
+          const int c = min(t + kT * j, c4 - 1), b = min(b0 + r, B - 1);
+          v[r][j] = *reinterpret_cast<const f32x4 *>(xp + (size_t)b * K + c * 4);
+        }
+    } else {
+      // cells of chunk (r, j): row b0 + r, values 4 c .. 4 c + 3, c = t + 256 j
+      // (rows past B and chunks past the row re-read the last ones)
+      uint64_t cv[kN];
+      uint64_t mask = 0;
 #pragma unroll
-    for (int r = 0; r < kRowsPerPass; r++) {
+      for (int r = 0; r < kRows; r++)
+#pragma unroll
+        for (int j = 0; j < kChunks; j++)
+          if (b0 + r < B && t + kT * j < c4) mask |= 15ull << ((r * kChunks + j) * 4);
+      ok = spin_cells(a, xc,
+                      [&](int k) {
+                        const int r = k / (kChunks * 4), j = (k / 4) % kChunks, e = k % 4;
+                        return (size_t)min(b0 + r, B - 1) * K + min(t + kT * j, c4 - 1) * 4 + e;
+                      },
+                      mask, tag, cv);
+#pragma unroll
+      for (int r = 0; r < kRows; r++)
+#pragma unroll
+        for (int j = 0; j < kChunks; j++) {
+          const int k = (r * kChunks + j) * 4;
+          v[r][j] = f32x4{cell_f32(cv[k]), cell_f32(cv[k + 1]), cell_f32(cv[k + 2]), cell_f32(cv[k + 3])};
+        }
+    }
+    if (!waits_ok(a, ok, misc)) return false;
+#pragma unroll
+    for (int r = 0; r < kRows; r++) {
       float ss = 0.0f;
 #pragma unroll
       for (int j = 0; j < kChunks; j++)
@@ -253,11 +308,11 @@ __device__ void stage_rms(const float *x, size_t x_off, int ld, const float *g, 
     }
     __syncthreads();
 #pragma unroll
-    for (int r = 0; r < kRowsPerPass; r++) {
+    for (int r = 0; r < kRows; r++) {
       const int b = b0 + r;
       if (b >= B) break;
       const float ss = (misc->part[0][r] + misc->part[1][r]) + (misc->part[2][r] + misc->part[3][r]);
-      const float inv = 1.0f / sqrtf(ss / (float)K + eps);
+      const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
 #pragma unroll
       for (int j = 0; j < kChunks; j++) {
         const int c = t + kT * j;
@@ -270,6 +325,46 @@ __device__ void stage_rms(const float *x, size_t x_off, int ld, const float *g, 
     }
     __syncthreads();
   }
+  return true;
+}
+
+// Rows [B][K] of fp16 values packed two per cell (K / 2 cells per row,
+// tagged `tag`) -> xs (row stride K + 8), kRows rows per pass. kChunks >=
+// K / 4 / 256 two-cell chunks per thread and row.
+template <int kChunks, int kRows>
+__device__ bool stage_f16(const LayersArgs &a, const uint64_t *cells, unsigned tag, int K,
+                          _Float16 *xs, Misc *misc) {
+  constexpr int kN = kRows * kChunks * 2;
+  static_assert(kN <= 64, "cells per thread");
+  const int B = a.B, c4 = K >> 2, t = threadIdx.x, row_cells = K >> 1;
+  for (int b0 = 0; b0 < B; b0 += kRows) {
+    // cells of chunk (r, j): row b0 + r, cells 2 c, 2 c + 1, c = t + 256 j
+    uint64_t cv[kN];
+    uint64_t mask = 0;
+#pragma unroll
+    for (int r = 0; r < kRows; r++)
+#pragma unroll
+      for (int j = 0; j < kChunks; j++)
+        if (b0 + r < B && t + kT * j < c4) mask |= 3ull << ((r * kChunks + j) * 2);
+    const bool ok = spin_cells(a, cells,
+                               [&](int k) {
+                                 const int r = k / (kChunks * 2), j = (k / 2) % kChunks, e = k % 2;
+                                 return (size_t)min(b0 + r, B - 1) * row_cells +
+                                        min(t + kT * j, c4 - 1) * 2 + e;
+                               },
+                               mask, tag, cv);
+    if (!waits_ok(a, ok, misc)) return false;
+#pragma unroll
+    for (int r = 0; r < kRows; r++)
+#pragma unroll
+      for (int j = 0; j < kChunks; j++) {
+        const int b = b0 + r, c = t + kT * j, k = (r * kChunks + j) * 2;
+        if (b < B && c < c4)
+          *reinterpret_cast<u32x2 *>(xs + b * (K + 8) + c * 4) = u32x2{(uint32_t)cv[k], (uint32_t)cv[k + 1]};
+      }
+  }
+  __syncthreads();
+  return true;
 }
 
 struct Lds {
@@ -278,135 +373,185 @@ struct Lds {
   Misc *misc;
 };
 
+// Requests x[b][col] of the four batch rows b = 4 (lane / 16) + r this
+// lane's accumulator holds (lanes of wave 0): plain values of the first
+// layer's input, or cells (checked by finish_residual).
+__device__ __forceinline__ void request_residual(const LayersArgs &a, const uint64_t *xc,
+                                                 const float *xp, int col, float (&rv)[4],
+                                                 uint64_t (&rc)[4]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int b = min(4 * (lane >> 4) + r, a.B - 1);
+    rv[r] = 0.0f;
+    rc[r] = 0;
+    if (xp) rv[r] = xp[(size_t)b * a.H + col];
+    else if (threadIdx.x < 64) rc[r] = cld(xc, (size_t)b * a.H + col);
+  }
+}
+
+// The residual cells of request_residual carry `tag` (they were produced a
+// phase before the current inputs, so this normally returns at once).
+__device__ __forceinline__ bool finish_residual(const LayersArgs &a, const uint64_t *xc, int col,
+                                                unsigned tag, float (&rv)[4], uint64_t (&rc)[4]) {
+  const int lane = threadIdx.x & 63;
+  bool ok = true;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int b = min(4 * (lane >> 4) + r, a.B - 1);
+    ok = ok && finish_cell(a, xc, (size_t)b * a.H + col, tag, rc[r]);
+    rv[r] = f32_of((uint32_t)rc[r]);
+  }
+  if (!ok) atomicOr(a.err, 1u);  // consumers of this item then fail their waits
+  return ok;
+}
+
 // A: qkv[b][16 i + c] = scale * (W_qkv RMSNorm(x)); w holds the item's
 // weights (load_weights, issued by the caller)
-template <int kL>
-__device__ bool qkv_item(const LayersArgs &a, const LayerPtrs &P, int i, unsigned epoch,
-                         const unsigned *wait_f, int wait_n, unsigned *flag, const Lds &s,
-                         const u32x4 (&w)[kL][1]) {
+template <int kL, int kRows>
+__device__ bool qkv_item(const LayersArgs &a, const LayerPtrs &P, int l, int i, unsigned ep,
+                         const Lds &s, const u32x4 (&w)[kL][1]) {
   const int lane = threadIdx.x & 63, col = lane & 15;
   const float sc = P.sqkv[i * 16 + col];
   __builtin_amdgcn_sched_barrier(0);
-  if (!wait_flags(a, wait_f, wait_n, epoch, s.misc)) return false;
-  stage_rms<(kL + 3) / 4>(a.x, 0, a.H, P.norm1, a.B, a.H, a.eps, s.xs, s.misc);
+  if (!stage_rms<(kL + 3) / 4, kRows>(a, a.x0c, l == 0 ? a.x_in : nullptr, tag_of(ep, l - 1), P.norm1,
+                               a.H, s.xs, s.misc))
+    return false;
+  SH_MARK(l, 0);
   f32x4 acc[1];
   mfma_weights<kL, 1>(w, s.xs, a.H + 8, a.B, acc);
+  SH_MARK(l, 1);
   reduce_waves<1>(acc, s.red);
+  SH_MARK(l, 2);
   if (threadIdx.x < 64) {
+    const unsigned tag = tag_of(ep, l);
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const int b = 4 * (lane >> 4) + r;
-      if (b < a.B) xst_f32(a.qkv, (size_t)b * a.qkv_n + i * 16 + col, acc[0][r] * sc);
+      if (b < a.B) cst1(a.qkvc, (size_t)b * a.qkv_n + i * 16 + col, bits_of(acc[0][r] * sc), tag);
     }
   }
-  publish(flag, epoch);
+  SH_MARK(l, 3);
   return true;
 }
 
 // C: x_mid[b][16 i + c] = x[b][.] + scale * (W_o attn)
-template <int kL>
-__device__ bool o_item(const LayersArgs &a, const LayerPtrs &P, int i, unsigned epoch,
-                       const unsigned *wait_f, int wait_n, unsigned *flag, const Lds &s) {
+template <int kL, int kRows>
+__device__ bool o_item(const LayersArgs &a, const LayerPtrs &P, int l, int i, unsigned ep,
+                       const Lds &s) {
   const int lane = threadIdx.x & 63, col = lane & 15, K = a.heads * kD;
   u32x4 w[kL][1];
   load_weights<kL, 1>(w, P.wo, K, i);
   const float sc = P.so[i * 16 + col];
-  __builtin_amdgcn_sched_barrier(0);
-  if (!wait_flags(a, wait_f, wait_n, epoch, s.misc)) return false;
   float rv[4];
-#pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const int b = min(4 * (lane >> 4) + r, a.B - 1);
-    rv[r] = xld_f32(a.x, (size_t)b * a.H + i * 16 + col);
-  }
-  stage_f16<(kL + 7) / 8>(a.attn, K, a.B, K, s.xs);
+  uint64_t rc[4];
+  request_residual(a, a.x0c, l == 0 ? a.x_in : nullptr, i * 16 + col, rv, rc);
+  __builtin_amdgcn_sched_barrier(0);
+  if (!stage_f16<(kL + 3) / 4, kRows>(a, a.attnc, tag_of(ep, l), K, s.xs, s.misc)) return false;
   f32x4 acc[1];
   mfma_weights<kL, 1>(w, s.xs, K + 8, a.B, acc);
   reduce_waves<1>(acc, s.red);
   if (threadIdx.x < 64) {
+    if (l > 0) finish_residual(a, a.x0c, i * 16 + col, tag_of(ep, l - 1), rv, rc);
+    const unsigned tag = tag_of(ep, l);
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const int b = 4 * (lane >> 4) + r;
-      if (b < a.B) xst_f32(a.x, (size_t)(kMaxBatch + b) * a.H + i * 16 + col, rv[r] + acc[0][r] * sc);
+      if (b < a.B) cst1(a.x1c, (size_t)b * a.H + i * 16 + col, bits_of(rv[r] + acc[0][r] * sc), tag);
     }
   }
-  publish(flag, epoch);
   return true;
 }
 
-// D: act[b][16 p + c] = silu(scale_g * gate) * (scale_u * up) of RMSNorm(x_mid)
-template <int kL>
-__device__ bool up_item(const LayersArgs &a, const LayerPtrs &P, int p, unsigned epoch,
-                        const unsigned *wait_f, int wait_n, unsigned *flag, const Lds &s) {
+// D: act[b][16 p + c] = silu(scale_g * gate) * (scale_u * up) of RMSNorm(x_mid),
+// two adjacent columns per cell
+template <int kL, int kRows>
+__device__ bool up_item(const LayersArgs &a, const LayerPtrs &P, int l, int p, unsigned ep,
+                        const Lds &s) {
   const int lane = threadIdx.x & 63, col = lane & 15;
   u32x4 w[kL][2];
   load_weights<kL, 2>(w, P.wup, a.H, p);
   const int ng = 2 * p * 16 + col;  // tiled rows of the gate and up tiles of pair p
   const float sg = P.sup[ng], su = P.sup[ng + 16];
   __builtin_amdgcn_sched_barrier(0);
-  if (!wait_flags(a, wait_f, wait_n, epoch, s.misc)) return false;
-  stage_rms<(kL + 3) / 4>(a.x, (size_t)kMaxBatch * a.H, a.H, P.norm2, a.B, a.H, a.eps, s.xs, s.misc);
+  if (!stage_rms<(kL + 3) / 4, kRows>(a, a.x1c, nullptr, tag_of(ep, l), P.norm2, a.H, s.xs, s.misc))
+    return false;
   f32x4 acc[2];
   mfma_weights<kL, 2>(w, s.xs, a.H + 8, a.B, acc);
   reduce_waves<2>(acc, s.red);
   if (threadIdx.x < 64) {
+    const unsigned tag = tag_of(ep, l);
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const int b = 4 * (lane >> 4) + r;
-      if (b < a.B)
-        xst_u16(a.act, (size_t)b * a.inter + p * 16 + col,
-                f32_to_f16_bits(silu(acc[0][r] * sg) * (acc[1][r] * su)));
+      const uint32_t h = f32_to_f16_bits(silu(acc[0][r] * sg) * (acc[1][r] * su));
+      const uint32_t nb = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)h, 0xB1, 0xf, 0xf, false);
+      if (b < a.B && (col & 1) == 0)
+        cst1(a.actc, (size_t)b * (a.inter / 2) + (p * 16 + col) / 2, h | (nb << 16), tag);
     }
   }
-  publish(flag, epoch);
   return true;
 }
 
-// E: x[b][16 i + c] = x_mid[b][.] + scale * (W_down act)
-template <int kL>
-__device__ bool down_item(const LayersArgs &a, const LayerPtrs &P, int i, unsigned epoch,
-                          const unsigned *wait_f, int wait_n, unsigned *flag, const Lds &s) {
+// E: x[b][16 i + c] = x_mid[b][.] + scale * (W_down act); the last layer
+// writes the plain buffer the final norm reads
+template <int kL, int kRows>
+__device__ bool down_item(const LayersArgs &a, const LayerPtrs &P, int l, int i, unsigned ep,
+                          const Lds &s) {
   const int lane = threadIdx.x & 63, col = lane & 15, K = a.inter;
   u32x4 w[kL][1];
   load_weights<kL, 1>(w, P.wdown, K, i);
   const float sc = P.sdown[i * 16 + col];
-  __builtin_amdgcn_sched_barrier(0);
-  if (!wait_flags(a, wait_f, wait_n, epoch, s.misc)) return false;
+  const unsigned tag = tag_of(ep, l);
   float rv[4];
-#pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const int b = min(4 * (lane >> 4) + r, a.B - 1);
-    rv[r] = xld_f32(a.x, (size_t)(kMaxBatch + b) * a.H + i * 16 + col);
-  }
-  stage_f16<(kL + 7) / 8>(a.act, K, a.B, K, s.xs);
+  uint64_t rc[4];
+  request_residual(a, a.x1c, nullptr, i * 16 + col, rv, rc);
+  __builtin_amdgcn_sched_barrier(0);
+  if (!stage_f16<(kL + 3) / 4, kRows>(a, a.actc, tag, K, s.xs, s.misc)) return false;
+  SH_MARK(l, 4);
   f32x4 acc[1];
   mfma_weights<kL, 1>(w, s.xs, K + 8, a.B, acc);
+  SH_MARK(l, 5);
   reduce_waves<1>(acc, s.red);
+  SH_MARK(l, 6);
   if (threadIdx.x < 64) {
+    finish_residual(a, a.x1c, i * 16 + col, tag, rv, rc);
+    const bool last = l + 1 == a.n_layers;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const int b = 4 * (lane >> 4) + r;
-      if (b < a.B) xst_f32(a.x, (size_t)b * a.H + i * 16 + col, rv[r] + acc[0][r] * sc);
+      const float v = rv[r] + acc[0][r] * sc;
+      if (b < a.B) {
+        if (last) a.x_in[(size_t)b * a.H + i * 16 + col] = v;
+        else cst1(a.x0c, (size_t)b * a.H + i * 16 + col, bits_of(v), tag);
+      }
     }
   }
-  publish(flag, epoch);
+  SH_MARK(l, 7);
   return true;
 }
 
-// ---- attention item -------------------------------------------------------------
+// ---- attention and merge items -------------------------------------------------
+
+constexpr int kPStride = kD + 4;  // cells per attention partial: acc[128], m, l, pad
 
 // LDS of an attention item, from the start of the dynamic area.
 template <int kG>
 struct AttnLds {
+  float raw[(kG + 2) * kD];  // this row's q (kG heads), new k and new v as produced
   float qs[kG][kD];
   _Float16 knew[kD], vnew[kD];
   float scores[kG][kMaxSplitChunk];
   float red[4][kG][kD];
   float wsum[8];
   float stat[kG][2];
-  float mw[kG][kMaxSplits];
-  float msum[kG];
-  f32x4 macc[8][kG][kD / 4];  // merge: split-group partial sums
+};
+
+// LDS of a merge item.
+struct MergeLds {
+  float m[kMaxSplits], l[kMaxSplits], w[kMaxSplits];
+  float lsum;
+  float acc[4][64][2];
 };
 
 constexpr int kLPP = kD / 8;     // lanes per position (8 dims each)
@@ -443,14 +588,12 @@ __device__ __forceinline__ void attn_prefetch(const LayersArgs &a, const LayerPt
 // Scores positions [p0, p0 + chunk) of the context for the kG query heads
 // of the KV head (Qwen3: RMSNorm of q and of the new k over the head, RoPE
 // rotate-half at this step's position; the split holding it appends the new
-// k / v to the cache), writes the partial (unnormalised V sum, max, sum) per
-// head, then counts its arrival. The split that arrives last merges all
-// partials of the (b, KV head):
-//   out = sum_j exp(m_j - M) acc_j / sum_j exp(m_j - M) l_j,  M = max_j m_j.
+// k / v to the cache) and writes the partial (unnormalised V sum, max, sum)
+// of each head as cells. Splits past the context write nothing.
 template <int kG>
-__device__ bool attn_item(const LayersArgs &a, const LayerPtrs &P, int l, int item,
-                          unsigned epoch, const unsigned *fA, unsigned *fB, uint8_t *smem,
-                          Misc *misc, AttnKV &kv) {
+__device__ bool attn_item(const LayersArgs &a, const LayerPtrs &P, int l, int item, unsigned ep,
+                          uint8_t *smem, Misc *misc, AttnKV &kv) {
+  static_assert((kG + 2) * kD / 2 <= kT, "one pair of q / k / v cells per thread");
   AttnLds<kG> &S = *reinterpret_cast<AttnLds<kG> *>(smem);
   const int splits = a.splits, kvn = a.kv_heads;
   const int s = item % splits, kvh = (item / splits) % kvn, b = item / (splits * kvn);
@@ -462,26 +605,38 @@ __device__ bool attn_item(const LayersArgs &a, const LayerPtrs &P, int l, int it
   const uint16_t *kbase = P.kcache + cache_base + seg * 8;
   const uint16_t *vbase = P.vcache + cache_base + seg * 8;
 
-  // this KV head's q, k and v tiles of the QKV items
-  const int tq = kvh * kG * (kD / 16);
-  const int tk = (a.heads * kD + kvh * kD) / 16, tv = ((a.heads + kvn) * kD + kvh * kD) / 16;
-  if (!wait_flags(a, fA + tq, kG * (kD / 16), epoch, misc) ||
-      !wait_flags(a, fA + tk, kD / 16, epoch, misc) || !wait_flags(a, fA + tv, kD / 16, epoch, misc))
-    return false;
-
   const int L = a.pos[b] + 1;  // context including the new token
   const int active = (L + chunk - 1) / chunk;
-  const bool live = s < active && cap > 0 && L <= a.max_pos;
+  if (s >= active || cap <= 0 || L > a.max_pos) return true;  // uniform
   const int h0 = kvh * kG;
-  if (live) {
+  const unsigned tag = tag_of(ep, l);
+  {
+    // the row's q of heads h0.., new k and new v: one pair of cells per thread
     const size_t qrow = (size_t)b * a.qkv_n;
+    constexpr int kQ = kG * kD / 2, kPairs = (kG + 2) * kD / 2;
+    size_t cell;
+    if (t < kQ) cell = qrow + (size_t)h0 * kD + 2 * t;
+    else if (t < kQ + kD / 2) cell = qrow + (size_t)a.heads * kD + kvh * kD + 2 * (t - kQ);
+    else cell = qrow + (size_t)(a.heads + kvn) * kD + kvh * kD + 2 * (min(t, kPairs - 1) - kQ - kD / 2);
+    uint64_t cv[2];
+    const bool ok = spin_cells(a, a.qkvc, [&](int k) { return cell + k; }, t < kPairs ? 3ull : 0ull,
+                               tag, cv);
+    if (!waits_ok(a, ok, misc)) return false;
+    SH_MARK(l, 8);
+    if (t < kPairs) {
+      S.raw[2 * t] = cell_f32(cv[0]);
+      S.raw[2 * t + 1] = cell_f32(cv[1]);
+    }
+    __syncthreads();
+  }
+  {
     const int gq = t / kD, iq = t % kD, half = kD / 2, fi = iq % half;
     const bool q_thread = t < kG * kD;
     const int p1 = min(L, p0 + chunk), np = p1 - p0, pos = L - 1;
     const bool kv_thread = p1 == L && t < kD;
-    float qv = xld_f32(a.qkv, qrow + (h0 + min(gq, kG - 1)) * kD + iq);
-    float knv = xld_f32(a.qkv, qrow + a.heads * kD + kvh * kD + iq);
-    const float vv = xld_f32(a.qkv, qrow + (a.heads + kvn) * kD + kvh * kD + iq);
+    float qv = S.raw[min(t, kG * kD - 1)];
+    float knv = S.raw[kG * kD + iq];
+    const float vv = S.raw[(kG + 1) * kD + iq];
     const float qn = P.q_norm[iq], kn = P.k_norm[iq];
     const float cs = a.rope[(size_t)b * kD + fi], sn = a.rope[(size_t)b * kD + half + fi];
     if (!q_thread) qv = 0.0f;
@@ -529,6 +684,7 @@ __device__ bool attn_item(const LayersArgs &a, const LayerPtrs &P, int l, int it
     }
     __syncthreads();
 
+    SH_MARK(l, 9);
     float q8[kG][8];
 #pragma unroll
     for (int g = 0; g < kG; g++)
@@ -570,6 +726,7 @@ __device__ bool attn_item(const LayersArgs &a, const LayerPtrs &P, int l, int it
     }
     __syncthreads();
 
+    SH_MARK(l, 10);
     // softmax statistics (wave g for head g)
     if (wave < kG) {
       const int g = wave;
@@ -590,6 +747,7 @@ __device__ bool attn_item(const LayersArgs &a, const LayerPtrs &P, int l, int it
     }
     __syncthreads();
 
+    SH_MARK(l, 11);
     // unnormalised V sums
     float acc[kG][8];
 #pragma unroll
@@ -636,87 +794,103 @@ __device__ bool attn_item(const LayersArgs &a, const LayerPtrs &P, int l, int it
         for (int e = 0; e < 8; e++) S.red[wave][g][seg * 8 + e] = acc[g][e];
     }
     __syncthreads();
-    if (t < kG * kD) {
-      const int g = t / kD, i = t % kD;
+    SH_MARK(l, 12);
+    if (t < kG * kD / 2) {
+      const int g = t / (kD / 2), i = 2 * (t % (kD / 2));
       const size_t pp = (((size_t)b * a.heads + h0 + g) * splits + s) * kPStride;
-      xst_f32(a.part, pp + i, S.red[0][g][i] + S.red[1][g][i] + S.red[2][g][i] + S.red[3][g][i]);
-      if (i == 0) {
-        const uint64_t ml = (uint64_t)__builtin_bit_cast(uint32_t, S.stat[g][0]) |
-                            ((uint64_t)__builtin_bit_cast(uint32_t, S.stat[g][1]) << 32);
-        xst_u64(a.part, (pp + kD) * 4, ml);
-      }
+      cst2(a.partc, pp + i,
+           bits_of(S.red[0][g][i] + S.red[1][g][i] + S.red[2][g][i] + S.red[3][g][i]),
+           bits_of(S.red[0][g][i + 1] + S.red[1][g][i + 1] + S.red[2][g][i + 1] + S.red[3][g][i + 1]),
+           tag);
+    } else if (t < kG * kD / 2 + kG) {
+      const int g = t - kG * kD / 2;
+      const size_t pp = (((size_t)b * a.heads + h0 + g) * splits + s) * kPStride;
+      cst2(a.partc, pp + kD, bits_of(S.stat[g][0]), bits_of(S.stat[g][1]), tag);
     }
   }
+  SH_MARK(l, 13);
+  return true;
+}
 
-  // arrival; every split of the (b, KV head) counts, live or not
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (t == 0) {
-    unsigned *cnt = a.counters + ((size_t)l * kMaxBatch + b) * kvn + kvh;
-    const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    misc->last = (old + 1) % (unsigned)splits == 0 ? 1 : 0;
+// M: item = (b, query head): combines the partials of the active splits
+// (at most kSP),
+//   out = sum_j exp(m_j - M) acc_j / sum_j exp(m_j - M) l_j,  M = max_j m_j,
+// and writes the head's 128 outputs as fp16 pairs. Thread t holds column
+// pair t % 64 of splits t / 64, t / 64 + 4, ...; threads t < active also
+// fetch split t's (m, l).
+template <int kSP>
+__device__ bool merge_item(const LayersArgs &a, int l, int item, unsigned ep, uint8_t *smem,
+                           Misc *misc) {
+  static_assert(kSP % 4 == 0 && kSP <= kMaxSplits, "splits per merge");
+  constexpr int kPer = kSP / 4;
+  MergeLds &S = *reinterpret_cast<MergeLds *>(smem);
+  const int h = item % a.heads, b = item / a.heads;
+  const int t = threadIdx.x, q = t & 63, sg = t >> 6;
+  const int L = a.pos[b] + 1;
+  const int active = min((L + a.chunk - 1) / a.chunk, a.splits);
+  const size_t base = ((size_t)b * a.heads + h) * a.splits * kPStride;
+  const unsigned tag = tag_of(ep, l);
+  // cells k < 2 kPer: column pair q of split sg + 4 (k / 2); the last two:
+  // (m, l) of split t
+  uint64_t mask = (t < active) ? 3ull << (2 * kPer) : 0ull;
+#pragma unroll
+  for (int k = 0; k < kPer; k++)
+    if (sg + 4 * k < active) mask |= 3ull << (2 * k);
+  uint64_t cv[2 * kPer + 2];
+  const bool ok = spin_cells(a, a.partc,
+                             [&](int k) {
+                               return k < 2 * kPer
+                                          ? base + (size_t)min(sg + 4 * (k / 2), active - 1) * kPStride +
+                                                2 * q + (k & 1)
+                                          : base + (size_t)min(t, active - 1) * kPStride + kD + (k & 1);
+                             },
+                             mask, tag, cv);
+  if (!waits_ok(a, ok, misc)) return false;
+  SH_MARK(l, 14);
+  if (t < active) {
+    S.m[t] = cell_f32(cv[2 * kPer]);
+    S.l[t] = cell_f32(cv[2 * kPer + 1]);
   }
   __syncthreads();
-  if (!misc->last) return true;
-
-  // merge (active <= splits <= kMaxSplits): every thread requests its split
-  // group's 16-byte columns and waves g < kG the split statistics together;
-  // then the split weights per head (wave g) and the weighted sums
-  {
-    constexpr int kQuads = kD / 4;               // 16-byte column groups per head
-    constexpr int kGroups = kT / (kG * kQuads);  // split groups (4 for kG = 2, 8 for kG = 1)
-    constexpr int kPer = kMaxSplits / kGroups;   // splits per group at most
-    const int g = t / (kGroups * kQuads), rem = t % (kGroups * kQuads);
-    const int q = rem % kQuads, sg = rem / kQuads;
-    const size_t base = ((size_t)b * a.heads + h0 + g) * splits * kPStride;
-    const int n_my = (active - sg + kGroups - 1) / kGroups;  // splits sg, sg + kGroups, ...
-    f32x4 xv[kPer];
+  if (t < 64) {
+    const float mj = t < active ? S.m[t] : -INFINITY;
+    const float lj = t < active ? S.l[t] : 0.0f;
+    const float M = wave_max_rows(mj);
+    const float wj = t < active ? expf(mj - M) : 0.0f;
+    const float lw = wave_sum_rows(wj * lj);
+    S.w[t] = wj;
+    if (t == 0) S.lsum = lw;
+  }
+  __syncthreads();
+  float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
-    for (int u = 0; u < kPer; u++) {
-      const int j = min(sg + u * kGroups, active - 1);  // unused slots reload a valid split
-      xv[u] = __builtin_bit_cast(f32x4, xld16(a.part, (base + (size_t)j * kPStride + q * 4) * 4));
-    }
-    if (wave < kG) {
-      const size_t pw = ((size_t)b * a.heads + h0 + wave) * splits * kPStride;
-      const int j = min(lane, active - 1);
-      float mj = xld_f32(a.part, pw + (size_t)j * kPStride + kD);
-      float lj = xld_f32(a.part, pw + (size_t)j * kPStride + kD + 1);
-      if (lane >= active) {
-        mj = -INFINITY;
-        lj = 0.0f;
-      }
-      const float M = wave_max_rows(mj);
-      const float wj = lane < active ? expf(mj - M) : 0.0f;
-      const float lw = wave_sum_rows(wj * lj);
-      S.mw[wave][lane] = wj;
-      if (lane == 0) S.msum[wave] = lw;
-    }
-    __syncthreads();
-    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int u = 0; u < kPer; u++)
-      if (u < n_my) sum += S.mw[g][sg + u * kGroups] * xv[u];
-    S.macc[sg][g][q] = sum;
-    __syncthreads();
-    if (sg == 0) {
-      f32x4 v = S.macc[0][g][q];
-#pragma unroll
-      for (int k = 1; k < kGroups; k++) v += S.macc[k][g][q];
-      const float inv = 1.0f / S.msum[g];
-      const uint64_t packed = (uint64_t)f32_to_f16_bits(v[0] * inv) |
-                              ((uint64_t)f32_to_f16_bits(v[1] * inv) << 16) |
-                              ((uint64_t)f32_to_f16_bits(v[2] * inv) << 32) |
-                              ((uint64_t)f32_to_f16_bits(v[3] * inv) << 48);
-      xst_u64(a.attn, ((size_t)b * a.heads * kD + (h0 + g) * kD + q * 4) * 2, packed);
+  for (int k = 0; k < kPer; k++) {
+    const int j = sg + 4 * k;
+    if (j < active) {
+      const float wj = S.w[j];
+      s0 += wj * cell_f32(cv[2 * k]);
+      s1 += wj * cell_f32(cv[2 * k + 1]);
     }
   }
-  publish(fB + b * kvn + kvh, epoch);
+  S.acc[sg][q][0] = s0;
+  S.acc[sg][q][1] = s1;
+  __syncthreads();
+  if (t < 64) {
+    const float inv = 1.0f / S.lsum;
+    const float v0 = (S.acc[0][q][0] + S.acc[1][q][0]) + (S.acc[2][q][0] + S.acc[3][q][0]);
+    const float v1 = (S.acc[0][q][1] + S.acc[1][q][1]) + (S.acc[2][q][1] + S.acc[3][q][1]);
+    const uint32_t packed = (uint32_t)f32_to_f16_bits(v0 * inv) |
+                            ((uint32_t)f32_to_f16_bits(v1 * inv) << 16);
+    cst1(a.attnc, (size_t)(b * a.heads + h) * (kD / 2) + q, packed, tag);
+  }
+  SH_MARK(l, 15);
+  __syncthreads();  // the next item reuses the LDS
   return true;
 }
 
 // ---- the kernel ----------------------------------------------------------------
 
-template <int kG, int kLA, int kLC, int kLD, int kLE>
+template <int kG, int kLA, int kLC, int kLD, int kLE, int kSP, int kRows>
 __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   Misc *misc = reinterpret_cast<Misc *>(smem + a.lds_misc);
@@ -728,41 +902,70 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
   lds.red = reinterpret_cast<float *>(smem + xs_max);
   lds.misc = misc;
 
-  const unsigned epoch = *a.epoch;
+  const unsigned ep = *a.epoch;
   const int G = gridDim.x, w = blockIdx.x;
-  const int nA = a.qkv_n / 16, nB = B * a.kv_heads * a.splits, nC = H / 16;
-  const int nD = a.inter / 16, nE = H / 16;
+  const int nA = a.qkv_n / 16, nB = B * a.kv_heads * a.splits, nM = B * a.heads;
+  const int nC = H / 16, nD = a.inter / 16, nE = H / 16;
+  const int d0 = (w + G - nC % G) % G;  // this workgroup's first gate/up item
+  const int m0 = G - 1 - w;             // its first merge item
+  const bool hasC = w < nC;
   AttnKV kv;
   u32x4 wa[kLA][1];  // this workgroup's first QKV item's weights
   if (w < nA) load_weights<kLA, 1>(wa, a.layers[0].wqkv, H, w);
+  if (w < nB) attn_prefetch(a, a.layers[0], w, kv);
   for (int l = 0; l < a.n_layers; l++) {
     const LayerPtrs P = a.layers[l];
-    unsigned *F = a.flags + (size_t)l * a.flags_per_layer;
-    const unsigned *prevE = a.flags + (size_t)(l > 0 ? l - 1 : 0) * a.flags_per_layer + a.fE;
-    if (w < nB) attn_prefetch(a, P, w, kv);  // streams while the QKV items run
+    const bool next = l + 1 < a.n_layers;
     for (int i = w; i < nA; i += G) {
       if (i != w) load_weights<kLA, 1>(wa, P.wqkv, H, i);
-      if (!qkv_item<kLA>(a, P, i, epoch, prevE, l > 0 ? nE : 0, F + i, lds, wa)) return;
+      if (i == w) SH_TRACE(l, 0);
+      if (!qkv_item<kLA, kRows>(a, P, l, i, ep, lds, wa)) return;
+      if (i == w) { SH_TRACE(l, 1); SH_TRACE_WAIT(l, 0, misc); }
     }
     for (int i = w; i < nB; i += G) {
       if (i != w) attn_prefetch(a, P, i, kv);
-      if (!attn_item<kG>(a, P, l, i, epoch, F, F + a.fB, smem, misc, kv)) return;
+      if (i == w) SH_TRACE(l, 2);
+      if (!attn_item<kG>(a, P, l, i, ep, smem, misc, kv)) return;
+      if (i == w) { SH_TRACE(l, 3); SH_TRACE_WAIT(l, 1, misc); }
     }
-    for (int i = w; i < nC; i += G)
-      if (!o_item<kLC>(a, P, i, epoch, F + a.fB, B * a.kv_heads, F + a.fC + i, lds)) return;
-    for (int i = (w + G - nC % G) % G; i < nD; i += G)
-      if (!up_item<kLD>(a, P, i, epoch, F + a.fC, nC, F + a.fD + i, lds)) return;
-    // the next layer's first QKV weights, before the down items wait
-    if (l + 1 < a.n_layers && w < nA) load_weights<kLA, 1>(wa, a.layers[l + 1].wqkv, H, w);
-    for (int i = w; i < nE; i += G)
-      if (!down_item<kLE>(a, P, i, epoch, F + a.fD, nD, F + a.fE + i, lds)) return;
+    for (int j = m0; j < nM; j += G) {
+      if (!merge_item<kSP>(a, l, j, ep, smem, misc)) return;
+      if (j == m0) SH_TRACE(l, 15);
+    }
+    // O, gate/up and down items request their weights when they start: at
+    // batch 1 each workgroup's previous item is then a phase or more behind
+    for (int i = w; i < nC; i += G) {
+      if (i == w) SH_TRACE(l, 4);
+      if (!o_item<kLC, kRows>(a, P, l, i, ep, lds)) return;
+      if (i == w) { SH_TRACE(l, 5); SH_TRACE_WAIT(l, 2, misc); }
+    }
+    // workgroups with an O item: the next layer's K / V while the gate/up
+    // items run; the others after their gate/up item, with the next QKV weights
+    if (hasC && next && w < nB) attn_prefetch(a, a.layers[l + 1], w, kv);
+    for (int i = d0; i < nD; i += G) {
+      if (i == d0) SH_TRACE(l, 6);
+      if (!up_item<kLD, kRows>(a, P, l, i, ep, lds)) return;
+      if (i == d0) { SH_TRACE(l, 7); SH_TRACE_WAIT(l, 3, misc); }
+    }
+    if (!hasC && next) {
+      if (w < nB) attn_prefetch(a, a.layers[l + 1], w, kv);
+      if (w < nA) load_weights<kLA, 1>(wa, a.layers[l + 1].wqkv, H, w);
+    }
+    for (int i = w; i < nE; i += G) {
+      if (i == w) SH_TRACE(l, 8);
+      if (!down_item<kLE, kRows>(a, P, l, i, ep, lds)) return;
+      if (i == w) { SH_TRACE(l, 9); SH_TRACE_WAIT(l, 4, misc); }
+    }
+    if (hasC && next && w < nA) load_weights<kLA, 1>(wa, a.layers[l + 1].wqkv, H, w);
   }
 }
 
-// (kG, loads per lane of qkv / o / gate-up / down items) per supported shape
+// (kG, loads per lane of qkv / o / gate-up / down items, most splits per
+// (row, KV head)) per supported shape; each in a batch-1 variant (one row
+// per staging pass) and a variant for larger batches (four rows per pass)
 #define SH_LAYERS_SHAPES(X) \
-  X(2, 4, 8, 4, 12)  /* hidden 1024, 16 x 128 query heads, 8 KV heads, inter 3072 */ \
-  X(2, 1, 2, 1, 3)   /* hidden 256, 4 x 128 query heads, 2 KV heads, inter 768 */
+  X(2, 4, 8, 4, 12, 32)  /* hidden 1024, 16 x 128 query heads, 8 KV heads, inter 3072 */ \
+  X(2, 1, 2, 1, 3, 64)   /* hidden 256, 4 x 128 query heads, 2 KV heads, inter 768 */
 
 struct Shape {
   int g, la, lc, ld, le;
@@ -772,10 +975,16 @@ Shape shape_of(int H, int heads, int kv_heads, int inter) {
   return Shape{kv_heads > 0 ? heads / kv_heads : 0, H / 256, heads * kD / 256, H / 256, inter / 256};
 }
 
-const void *kernel_for(const Shape &s) {
-#define SH_MATCH(G, LA, LC, LD, LE)                                               \
-  if (s.g == G && s.la == LA && s.lc == LC && s.ld == LD && s.le == LE)           \
-    return reinterpret_cast<const void *>(&decode_layers_kernel<G, LA, LC, LD, LE>);
+// The kernel for a shape and batch (batch 0: the batch-1 variant), and the
+// shape's split limit.
+const void *kernel_for(const Shape &s, int batch, int *max_splits) {
+#define SH_MATCH(G, LA, LC, LD, LE, SP)                                                \
+  if (s.g == G && s.la == LA && s.lc == LC && s.ld == LD && s.le == LE) {              \
+    if (max_splits) *max_splits = SP;                                                  \
+    return batch <= 1                                                                  \
+               ? reinterpret_cast<const void *>(&decode_layers_kernel<G, LA, LC, LD, LE, SP, 1>) \
+               : reinterpret_cast<const void *>(&decode_layers_kernel<G, LA, LC, LD, LE, SP, kMaxRowsPerPass>); \
+  }
   SH_LAYERS_SHAPES(SH_MATCH)
 #undef SH_MATCH
   return nullptr;
@@ -787,10 +996,16 @@ size_t attn_lds(int g) {
 
 }  // namespace
 
-bool decode_layers_supported(int H, int heads, int kv_heads, int head_dim, int inter) {
+bool decode_layers_supported(int layers, int H, int heads, int kv_heads, int head_dim, int inter) {
+  if (layers < 1 || layers > kMaxDecodeLayers) return false;
   if (head_dim != kD || kv_heads <= 0 || heads % kv_heads != 0) return false;
   if (H % 256 || (heads * kD) % 256 || inter % 256 || H > 4096) return false;
-  return kernel_for(shape_of(H, heads, kv_heads, inter)) != nullptr;
+  return kernel_for(shape_of(H, heads, kv_heads, inter), 1, nullptr) != nullptr;
+}
+
+int decode_layers_max_splits(int H, int heads, int kv_heads, int inter) {
+  int sp = 0;
+  return kernel_for(shape_of(H, heads, kv_heads, inter), 1, &sp) ? sp : 0;
 }
 
 size_t decode_layers_lds(int B, int H, int heads, int inter, int *misc_offset) {
@@ -801,21 +1016,45 @@ size_t decode_layers_lds(int B, int H, int heads, int inter, int *misc_offset) {
   size_t end = xs_max + 3 * 2 * 64 * 4 * sizeof(float);  // + wave-reduction area
   const size_t attn = attn_lds(2);
   if (attn > end) end = attn;
+  if (sizeof(MergeLds) > end) end = sizeof(MergeLds);
   end = (end + 15) / 16 * 16;
   *misc_offset = (int)end;
   return end + sizeof(Misc);
 }
 
+size_t decode_layers_partial_cells(int heads) { return (size_t)kMaxBatch * heads * kMaxSplits * kPStride; }
+
 hipError_t decode_layers_occupancy(const LayersArgs &a, size_t lds, int *blocks_per_cu) {
-  const void *k = kernel_for(shape_of(a.H, a.heads, a.kv_heads, a.inter));
-  if (!k) return hipErrorInvalidValue;
-  hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (e != hipSuccess) return e;
-  return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, k, kT, lds);
+  const Shape sh = shape_of(a.H, a.heads, a.kv_heads, a.inter);
+  int least = 1 << 30;
+  for (int batch : {1, kMaxBatch}) {
+    const void *k = kernel_for(sh, batch, nullptr);
+    if (!k) return hipErrorInvalidValue;
+    hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    int n = 0;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, kT, lds);
+    if (e != hipSuccess) return e;
+    if (n < least) least = n;
+  }
+  *blocks_per_cu = least;
+  return hipSuccess;
 }
 
+#ifdef SH_DECODE_TRACE
+hipError_t decode_layers_trace(void *dst, size_t bytes) {
+  const size_t one = sizeof(g_decode_trace);
+  hipError_t e = hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_decode_trace), bytes < one ? bytes : one, 0,
+                                     hipMemcpyDeviceToHost);
+  if (e != hipSuccess || bytes <= one) return e;
+  bytes -= one;
+  return hipMemcpyFromSymbol(static_cast<char *>(dst) + one, HIP_SYMBOL(g_decode_trace2),
+                             bytes < one ? bytes : one, 0, hipMemcpyDeviceToHost);
+}
+#endif
+
 hipError_t launch_decode_layers(hipStream_t s, const LayersArgs &a, int grid, size_t lds) {
-  const void *k = kernel_for(shape_of(a.H, a.heads, a.kv_heads, a.inter));
+  const void *k = kernel_for(shape_of(a.H, a.heads, a.kv_heads, a.inter), a.B, nullptr);
   if (!k) return hipErrorInvalidValue;
   void *args[] = {const_cast<LayersArgs *>(&a)};
   return hipLaunchCooperativeKernel(k, dim3(grid), dim3(kT), args, (unsigned)lds, s);

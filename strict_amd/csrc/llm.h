@@ -86,10 +86,16 @@ struct LayerPtrs {
   uint16_t *kcache, *vcache;               // [max_batch][kv_heads][max_pos][128] fp16
 };
 
-// Everything the kernel exchanges between workgroups within a step lives in
-// uncached device memory (x, qkv, part, attn, act, flags, counters, err):
-// a value stored there is visible to every CU once the store has completed,
-// without the whole-L2 write-back a device-scope fence costs.
+// Everything the kernel hands between workgroups within a step travels in
+// 8-byte cells of uncached device memory (payload word, then the producing
+// step and layer's tag word; see decode_layers.hip). Cell buffers:
+//   x0c   [kMaxBatch][H]          layer output x (fp32), read by the next layer
+//   x1c   [kMaxBatch][H]          x_mid after attention (fp32)
+//   qkvc  [kMaxBatch][qkv_n]      q | k | v (fp32)
+//   partc [kMaxBatch][heads][64][132] attention partials (acc[128], max, sum)
+//   attnc [kMaxBatch][heads * 64] merged attention output, two fp16 per cell
+//   actc  [kMaxBatch][inter / 2]  SwiGLU output, two fp16 per cell
+constexpr int kMaxDecodeLayers = 63;  // tags hold the layer in 6 bits
 struct LayersArgs {
   const LayerPtrs *layers = nullptr;  // [n_layers]
   int n_layers = 0, B = 0, H = 0, heads = 0, kv_heads = 0, inter = 0, qkv_n = 0;
@@ -98,14 +104,10 @@ struct LayersArgs {
   const int *pos = nullptr;            // [B] this step's position (embed kernel)
   const float *rope = nullptr;         // [B][128]: cos | sin (embed kernel)
   const unsigned *epoch = nullptr;     // this step's number (embed kernel)
-  float *x = nullptr;                  // [2][kMaxBatch][H]: layer input / output, after attention
-  float *qkv = nullptr;                // [kMaxBatch][qkv_n]
-  float *part = nullptr;               // [kMaxBatch][heads][splits][130] attention partials
-  uint16_t *attn = nullptr;            // [kMaxBatch][heads * 128]
-  uint16_t *act = nullptr;             // [kMaxBatch][inter]
-  unsigned *flags = nullptr;           // per layer: qkv | attention | o | gate_up | down items
-  int flags_per_layer = 0, fB = 0, fC = 0, fD = 0, fE = 0;
-  unsigned *counters = nullptr;        // [n_layers][kMaxBatch][kv_heads] split arrivals
+  float *x_in = nullptr;               // [kMaxBatch][H] plain fp32: first layer's input
+                                       // (embed kernel), last layer's output
+  uint64_t *x0c = nullptr, *x1c = nullptr, *qkvc = nullptr, *partc = nullptr;
+  uint64_t *attnc = nullptr, *actc = nullptr;
   unsigned *err = nullptr;             // set when a wait timed out (sticky)
   unsigned long long spin_ticks = 0;   // wall-clock ticks a wait may take
   int lds_misc = 0;                    // byte offset of the small LDS scratch words
@@ -114,10 +116,18 @@ struct LayersArgs {
 // Model shapes the kernel is instantiated for (16-byte weight loads per lane
 // of the qkv, o, gate/up and down items) and the query heads per KV head.
 // Returns false for any other shape (the runner then keeps per-op kernels).
-bool decode_layers_supported(int H, int heads, int kv_heads, int head_dim, int inter);
+bool decode_layers_supported(int layers, int H, int heads, int kv_heads, int head_dim, int inter);
+// Most attention splits per (row, KV head) the shape's kernel merges.
+int decode_layers_max_splits(int H, int heads, int kv_heads, int inter);
+// Cells of the attention-partial buffer partc.
+size_t decode_layers_partial_cells(int heads);
 size_t decode_layers_lds(int B, int H, int heads, int inter, int *misc_offset);
 // Workgroups of the kernel resident per CU with `lds` bytes of LDS (>= 1 to use it).
 hipError_t decode_layers_occupancy(const LayersArgs &a, size_t lds, int *blocks_per_cu);
+#ifdef SH_DECODE_TRACE
+// Diagnostic builds: copies the last step's phase timeline to the host.
+hipError_t decode_layers_trace(void *dst, size_t bytes);
+#endif
 // Cooperative launch (all `grid` workgroups resident together) on stream s.
 hipError_t launch_decode_layers(hipStream_t s, const LayersArgs &a, int grid, size_t lds);
 

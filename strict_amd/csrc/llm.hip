@@ -229,12 +229,8 @@ int enqueue_step(sh_llm *m, bool logits) {
   e.inv_freq = m->inv_freq;
   e.rope = m->rope;
   e.half = d / 2;
-  float *x_final = m->x;
-  if (m->layers_kernel) {
-    e.x = m->la.x;  // layer input buffer of the decode-layers kernel
-    e.epoch = m->epoch;
-    x_final = m->la.x;
-  }
+  float *x_final = m->x;  // the decode-layers kernel reads and writes m->x too
+  if (m->layers_kernel) e.epoch = m->epoch;
   SH_HIP_TRY(launch_embed(s, e, B));
 
   if (m->layers_kernel) SH_HIP_TRY(launch_decode_layers(s, m->la, m->layers_grid, m->layers_lds));
@@ -357,7 +353,8 @@ int setup_layers_kernel(sh_llm *m) {
   const char *env = getenv("STRICT_HIP_LLM_LAYERS");
   if (env && env[0] == '0') return SH_OK;
   if (!m->qwen ||
-      !decode_layers_supported(c.hidden, c.heads, c.kv_heads, c.head_dim, c.intermediate))
+      !decode_layers_supported(c.layers, c.hidden, c.heads, c.kv_heads, c.head_dim,
+                               c.intermediate))
     return SH_OK;
   const int dev = device_of(m->ctx);
   int coop = 0, cus = 0, clock_khz = 0;
@@ -378,27 +375,24 @@ int setup_layers_kernel(sh_llm *m) {
   a.pos = m->pos;
   a.rope = m->rope;
   a.spin_ticks = (unsigned long long)clock_khz * 50;  // 50 ms per wait
+  // the kernel's merge limit must leave splits of at most kMaxSplitChunk positions
+  const int max_sp = decode_layers_max_splits(c.hidden, c.heads, c.kv_heads, c.intermediate);
+  if ((c.max_positions + kMaxSplitChunk - 1) / kMaxSplitChunk > max_sp) return SH_OK;
   int misc = 0;
   const size_t lds = decode_layers_lds(c.max_batch, c.hidden, c.heads, c.intermediate, &misc);
   int per_cu = 0;
   SH_HIP_TRY(decode_layers_occupancy(a, lds, &per_cu));
   if (per_cu < 1) return SH_OK;
-  const int nA = m->qkv_n / 16, nC = c.hidden / 16, nD = c.intermediate / 16;
-  a.fB = nA;
-  a.fC = a.fB + kMaxBatch * c.kv_heads;
-  a.fD = a.fC + nC;
-  a.fE = a.fD + nD;
-  a.flags_per_layer = a.fE + nC;
   int rc;
-  if ((rc = uc_alloc_n(m, (size_t)2 * kMaxBatch * c.hidden, &a.x)) ||
-      (rc = uc_alloc_n(m, (size_t)kMaxBatch * m->qkv_n, &a.qkv)) ||
-      (rc = uc_alloc_n(m, (size_t)kMaxBatch * c.heads * 64 * (c.head_dim + 4), &a.part)) ||
-      (rc = uc_alloc_n(m, (size_t)kMaxBatch * c.heads * c.head_dim, &a.attn)) ||
-      (rc = uc_alloc_n(m, (size_t)kMaxBatch * c.intermediate, &a.act)) ||
-      (rc = uc_alloc_n(m, (size_t)c.layers * a.flags_per_layer, &a.flags)) ||
-      (rc = uc_alloc_n(m, (size_t)c.layers * kMaxBatch * c.kv_heads, &a.counters)) ||
-      (rc = uc_alloc_n(m, 64, &a.err)) || (rc = alloc_n(m, 64, &m->epoch)))
+  const size_t MB = kMaxBatch;
+  if ((rc = uc_alloc_n(m, MB * c.hidden, &a.x0c)) || (rc = uc_alloc_n(m, MB * c.hidden, &a.x1c)) ||
+      (rc = uc_alloc_n(m, MB * m->qkv_n, &a.qkvc)) ||
+      (rc = uc_alloc_n(m, decode_layers_partial_cells(c.heads), &a.partc)) ||
+      (rc = uc_alloc_n(m, MB * c.heads * c.head_dim / 2, &a.attnc)) ||
+      (rc = uc_alloc_n(m, MB * c.intermediate / 2, &a.actc)) || (rc = uc_alloc_n(m, 64, &a.err)) ||
+      (rc = alloc_n(m, 64, &m->epoch)))
     return rc;
+  a.x_in = m->x;
   LayerPtrs *dl = nullptr;
   if ((rc = alloc_n(m, (size_t)c.layers, &dl))) return rc;
   std::vector<LayerPtrs> hl(c.layers);
@@ -608,6 +602,15 @@ SH_API int sh_llm_create(sh_ctx *ctx, const sh_llm_config *config, sh_llm **out)
   return SH_OK;
 }
 
+#ifdef SH_DECODE_TRACE
+// Diagnostic builds only (-DSH_DECODE_TRACE): the decode-layers kernel's
+// per-workgroup phase timeline of the last step, [256][32][16] wall-clock ticks.
+SH_API int sh_debug_decode_trace(void *dst, size_t bytes) {
+  SH_HIP_TRY(decode_layers_trace(dst, bytes));
+  return SH_OK;
+}
+#endif
+
 SH_API int sh_llm_destroy(sh_llm *m) {
   if (!m) return SH_OK;
   (void)hipSetDevice(device_of(m->ctx));
@@ -744,19 +747,20 @@ SH_API int sh_llm_reset(sh_llm *m, int batch) {
   m->steps_done = 0;
   if (m->layers_kernel) {
     // splits per (row, KV head): as many as give every workgroup one item at
-    // batch 1, no split longer than kMaxSplitChunk, at most 64; independent
-    // of the batch, so a row's arithmetic does not depend on its batch
+    // batch 1, no split longer than kMaxSplitChunk, at most the kernel's
+    // merge limit (setup checked that both hold together); independent of
+    // the batch, so a row's arithmetic does not depend on its batch
     LayersArgs &a = m->la;
     const sh_llm_config &c = m->cfg;
     int sp = (m->layers_grid + c.kv_heads - 1) / c.kv_heads;
     const int min_sp = (c.max_positions + kMaxSplitChunk - 1) / kMaxSplitChunk;
+    const int max_sp = decode_layers_max_splits(c.hidden, c.heads, c.kv_heads, c.intermediate);
     if (sp < min_sp) sp = min_sp;
-    if (sp > 64) sp = 64;
+    if (sp > max_sp) sp = max_sp;
     a.B = batch;
     a.splits = sp;
     a.chunk = ((c.max_positions + sp - 1) / sp + 15) / 16 * 16;
     m->layers_lds = decode_layers_lds(batch, c.hidden, c.heads, c.intermediate, &a.lds_misc);
-    SH_HIP_TRY(hipMemsetAsync(a.counters, 0, (size_t)c.layers * kMaxBatch * c.kv_heads * 4, s));
     SH_HIP_TRY(hipMemsetAsync(a.err, 0, 4, s));
   }
   return SH_OK;
