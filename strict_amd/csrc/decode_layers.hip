@@ -12,15 +12,18 @@
 //   E  down    one 16-row tile of W_down each      (x = x_mid + W_down act)
 //
 // Exchange between workgroups: every value an item hands on travels in an
-// 8-byte cell of uncached device memory, payload in the low word and the
+// 8-byte cell of device memory, payload in the low word and the
 // producing (step, layer) tag in the high word, written by one 8-byte (or
 // 16-byte, two-cell) store. A consumer loads the cells it needs until each
 // carries the tag it expects. The data is its own completion flag: a
 // producer never waits for its stores to complete, and a consumer needs one
 // memory round trip once the data has landed (a flag word would cost the
 // producer's store-completion wait, the flag poll and then the data read).
-// Relaxed 64-bit agent-scope atomic loads do the polling: the compiler
-// neither hoists them out of the spin loop nor waits after each one.
+// Every cell access is a relaxed 64-bit agent-scope atomic: the memory
+// model keeps those coherent across the XCDs' separate L2 caches (measured
+// here: ~0.35-0.45 us from a store to another XCD's poll seeing it, against
+// ~0.55-0.63 us through uncached memory), and the compiler neither hoists
+// such a load out of a spin loop nor waits after each one.
 //
 // Weights and K / V do not depend on the step's activations, so each
 // workgroup requests them for its next items right after it has finished
@@ -48,9 +51,32 @@ namespace {
 
 constexpr int kT = 256;         // threads per workgroup (4 waves)
 constexpr int kD = 128;         // head dim
-constexpr int kAttnBatch = 10;  // 16-position block steps of K / V requested ahead
 constexpr int kMaxSplits = 64;  // splits per (row, KV head) a merge item combines
 constexpr int kMaxRowsPerPass = 4;  // batch rows staged together (1 at batch 1)
+
+// Pointers the kernel reads from its argument table (LayerPtrs) are generic;
+// loads through them compile to flat instructions, which also count against
+// the LDS wait counter, so every LDS wait would wait for outstanding weight
+// and K / V requests too. The kernel casts them to the global address space.
+#define SH_GLOBAL __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ SH_GLOBAL T *gbl(T *p) {
+  return (SH_GLOBAL T *)p;
+}
+
+// One layer's pointers in the global address space.
+struct LayerG {
+  const SH_GLOBAL uint8_t *wqkv, *wo, *wup, *wdown;
+  const SH_GLOBAL float *sqkv, *so, *sup, *sdown;
+  const SH_GLOBAL float *norm1, *norm2, *q_norm, *k_norm;
+  SH_GLOBAL uint16_t *kcache, *vcache;
+};
+
+__device__ __forceinline__ LayerG layer_g(const LayerPtrs &p) {
+  return LayerG{gbl(p.wqkv),   gbl(p.wo),     gbl(p.wup),    gbl(p.wdown), gbl(p.sqkv),
+                gbl(p.so),     gbl(p.sup),    gbl(p.sdown),  gbl(p.norm1), gbl(p.norm2),
+                gbl(p.q_norm), gbl(p.k_norm), gbl(p.kcache), gbl(p.vcache)};
+}
 
 // ---- exchange cells ------------------------------------------------------------
 
@@ -105,6 +131,9 @@ __device__ __forceinline__ bool spin_cells(const LayersArgs &a, const uint64_t *
     } else if ((it & 7) == 0 && (ld_err(a.err) != 0 || wall_clock64() - t0 > a.spin_ticks)) {
       return false;
     }
+#if defined(SH_POLL_SLEEP) && SH_POLL_SLEEP > 0
+    __builtin_amdgcn_s_sleep(SH_POLL_SLEEP);
+#endif
   }
 }
 
@@ -125,57 +154,85 @@ __device__ __forceinline__ bool finish_cell(const LayersArgs &a, const uint64_t 
   return true;
 }
 
+#ifdef SH_DECODE_TRACE
+constexpr int kTraceWgs = 256, kTraceLayers = 32, kTraceSlots = 16;
+#endif
+
 // Small LDS words after the phase areas.
 struct Misc {
-  float part[4][kMaxRowsPerPass];          // per-wave partial sums of squares
+  float part[4][kMaxRowsPerPass];  // per-wave partial sums of squares
+  int vote[2][4];                  // per-wave votes of block_any (two alternating sets)
+  int par[4];                      // each wave's current vote set
 #ifdef SH_DECODE_TRACE
-  unsigned long long t_wait;            // when the last wait ended
+  unsigned long long t_wait;                          // when the last wait ended
+  unsigned long long tr[2][kTraceLayers][kTraceSlots];  // this workgroup's timeline
 #endif
 };
 
+// Workgroup barrier for LDS traffic only. __syncthreads() is a release /
+// acquire fence plus s_barrier, and the fence makes a wave wait for every
+// global store it has issued (cell stores, cache appends) before the
+// barrier; nothing in this kernel reads back through global memory what
+// another wave of its workgroup wrote, so only LDS needs to be complete.
+// The signal fences keep the compiler from moving memory accesses across.
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left alone
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// True in every thread when p holds in any thread (a barrier). Each wave
+// votes in one of two sets, alternating per call (its parity lives in its
+// own LDS word): a wave that runs ahead to the next call writes the other
+// set, and one two calls ahead has passed a barrier that every wave reaches
+// only after reading this call's votes.
+__device__ __forceinline__ bool block_any(bool p, Misc *misc) {
+  const int wave = threadIdx.x >> 6;
+  const int par = misc->par[wave];
+  const bool v = __any(p ? 1 : 0) != 0;
+  if ((threadIdx.x & 63) == 0) {
+    misc->vote[par][wave] = v ? 1 : 0;
+    misc->par[wave] = par ^ 1;
+  }
+  lds_barrier();
+  const int *vt = misc->vote[par];
+  return (vt[0] | vt[1] | vt[2] | vt[3]) != 0;
+}
+
 // Every thread's wait succeeded (block-uniform); otherwise marks the error.
 __device__ __forceinline__ bool waits_ok(const LayersArgs &a, bool ok, Misc *misc) {
-  if (__syncthreads_or(ok ? 0 : 1)) {
+  if (block_any(!ok, misc)) {
     if (threadIdx.x == 0) atomicOr(a.err, 1u);
     return false;
   }
 #ifdef SH_DECODE_TRACE
   if (threadIdx.x == 0) misc->t_wait = wall_clock64();
-#else
-  (void)misc;
 #endif
   return true;
 }
 
 #ifdef SH_DECODE_TRACE
-// Timeline of one step (diagnostic builds only): per workgroup and layer,
-// the wall clock at each phase's start (even slots 0..8: QKV, attention, O,
-// gate/up, down) and end (odd slots), when its wait ended (10..14) and when
-// the merge item ended (15).
-constexpr int kTraceWgs = 256, kTraceLayers = 32, kTraceSlots = 16;
-__device__ unsigned long long g_decode_trace[kTraceWgs][kTraceLayers][kTraceSlots];
-__device__ __forceinline__ void trace_mark(int l, int slot) {
-  if (threadIdx.x == 0 && blockIdx.x < kTraceWgs && l < kTraceLayers)
-    g_decode_trace[blockIdx.x][l][slot] = wall_clock64();
-}
-// Finer marks inside items: QKV 0..3 (staged, MFMA, reduced, stored), down
+// Timeline of one step (diagnostic builds only), kept in LDS during the step
+// and written out when the kernel ends: per workgroup and layer, tr[0] holds
+// each phase's start (even slots 0..8: QKV, attention, O, gate/up, down),
+// end (odd slots), the end of its wait (10..14) and the merge end (15); tr[1]
+// holds marks inside items: QKV 0..3 (staged, MFMA, reduced, stored), down
 // 4..7, attention 8..13 (q/k/v polled, RoPE, scores, softmax, V sums,
 // stored), merge 14..15 (polled, stored).
-__device__ unsigned long long g_decode_trace2[kTraceWgs][kTraceLayers][kTraceSlots];
-__device__ __forceinline__ void trace_mark2(int l, int slot) {
-  if (threadIdx.x == 0 && blockIdx.x < kTraceWgs && l < kTraceLayers)
-    g_decode_trace2[blockIdx.x][l][slot] = wall_clock64();
+__device__ unsigned long long g_decode_trace[2][kTraceWgs][kTraceLayers][kTraceSlots];
+__device__ __forceinline__ void trace_mark(Misc *misc, int set, int l, int slot) {
+  if (threadIdx.x == 0 && l < kTraceLayers) misc->tr[set][l][slot] = wall_clock64();
 }
-#define SH_MARK(l, slot) trace_mark2(l, slot)
-#define SH_TRACE(l, slot) trace_mark(l, slot)
-#define SH_TRACE_WAIT(l, ph, misc)                                                        \
-  do {                                                                                    \
-    if (threadIdx.x == 0 && blockIdx.x < kTraceWgs && (l) < kTraceLayers)                 \
-      g_decode_trace[blockIdx.x][l][10 + (ph)] = (misc)->t_wait;                          \
+#define SH_MARK(misc, l, slot) trace_mark(misc, 1, l, slot)
+#define SH_TRACE(misc, l, slot) trace_mark(misc, 0, l, slot)
+#define SH_TRACE_WAIT(l, ph, misc)                                                 \
+  do {                                                                             \
+    if (threadIdx.x == 0 && (l) < kTraceLayers) (misc)->tr[0][l][10 + (ph)] = (misc)->t_wait; \
   } while (0)
 #else
-#define SH_TRACE(l, slot) ((void)0)
-#define SH_MARK(l, slot) ((void)0)
+#define SH_TRACE(misc, l, slot) ((void)0)
+#define SH_MARK(misc, l, slot) ((void)0)
 #define SH_TRACE_WAIT(l, ph, misc) ((void)0)
 #endif
 
@@ -184,7 +241,7 @@ __device__ __forceinline__ void trace_mark2(int l, int slot) {
 // This wave's quarter of K for tile group g (kNT consecutive 16-row tiles of
 // an FP8 tiled matrix with K columns): kL 16-byte loads per lane and tile.
 template <int kL, int kNT>
-__device__ __forceinline__ void load_weights(u32x4 (&w)[kL][kNT], const uint8_t *W, int K, int g) {
+__device__ __forceinline__ void load_weights(u32x4 (&w)[kL][kNT], const SH_GLOBAL uint8_t *W, int K, int g) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lpr = K >> 6;
 #pragma unroll
@@ -193,7 +250,7 @@ __device__ __forceinline__ void load_weights(u32x4 (&w)[kL][kNT], const uint8_t 
     for (int j = 0; j < kNT; j++) {
       const size_t tile = (size_t)(g * kNT + j) * lpr + wave * kL + u;
       w[u][j] = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4 *>(W + tile * 1024 + (size_t)lane * 16));
+          reinterpret_cast<const SH_GLOBAL u32x4 *>(W + tile * 1024 + (size_t)lane * 16));
     }
 }
 
@@ -230,7 +287,7 @@ __device__ __forceinline__ void reduce_waves(f32x4 (&acc)[kNT], float *red) {
     for (int j = 0; j < kNT; j++)
       *reinterpret_cast<f32x4 *>(red + (((wave - 1) * kNT + j) * 64 + lane) * 4) = acc[j];
   }
-  __syncthreads();
+  lds_barrier();
   if (wave == 0) {
 #pragma unroll
     for (int j = 0; j < kNT; j++) {
@@ -250,7 +307,7 @@ __device__ __forceinline__ void reduce_waves(f32x4 (&acc)[kNT], float *red) {
 // LDS. kChunks >= K / 4 / 256.
 template <int kChunks, int kRows>
 __device__ bool stage_rms(const LayersArgs &a, const uint64_t *xc, const float *xp, unsigned tag,
-                          const float *g, int K, _Float16 *xs, Misc *misc) {
+                          const SH_GLOBAL float *g, int K, _Float16 *xs, Misc *misc) {
   typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
   constexpr int kN = kRows * kChunks * 4;
   static_assert(kN <= 64, "cells per thread");
@@ -258,7 +315,7 @@ __device__ bool stage_rms(const LayersArgs &a, const uint64_t *xc, const float *
   f32x4 gv[kChunks];
 #pragma unroll
   for (int j = 0; j < kChunks; j++)
-    gv[j] = *reinterpret_cast<const f32x4 *>(g + min(t + kT * j, c4 - 1) * 4);
+    gv[j] = *reinterpret_cast<const SH_GLOBAL f32x4 *>(g + min(t + kT * j, c4 - 1) * 4);
   for (int b0 = 0; b0 < B; b0 += kRows) {
     f32x4 v[kRows][kChunks];
     bool ok = true;
@@ -306,7 +363,7 @@ __device__ bool stage_rms(const LayersArgs &a, const uint64_t *xc, const float *
       ss = wave_sum_rows(ss);
       if (lane == 0) misc->part[wave][r] = ss;
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int r = 0; r < kRows; r++) {
       const int b = b0 + r;
@@ -323,7 +380,7 @@ __device__ bool stage_rms(const LayersArgs &a, const uint64_t *xc, const float *
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
   return true;
 }
@@ -363,7 +420,7 @@ __device__ bool stage_f16(const LayersArgs &a, const uint64_t *cells, unsigned t
           *reinterpret_cast<u32x2 *>(xs + b * (K + 8) + c * 4) = u32x2{(uint32_t)cv[k], (uint32_t)cv[k + 1]};
       }
   }
-  __syncthreads();
+  lds_barrier();
   return true;
 }
 
@@ -385,7 +442,7 @@ __device__ __forceinline__ void request_residual(const LayersArgs &a, const uint
     const int b = min(4 * (lane >> 4) + r, a.B - 1);
     rv[r] = 0.0f;
     rc[r] = 0;
-    if (xp) rv[r] = xp[(size_t)b * a.H + col];
+    if (xp) rv[r] = gbl(xp)[(size_t)b * a.H + col];
     else if (threadIdx.x < 64) rc[r] = cld(xc, (size_t)b * a.H + col);
   }
 }
@@ -409,7 +466,7 @@ __device__ __forceinline__ bool finish_residual(const LayersArgs &a, const uint6
 // A: qkv[b][16 i + c] = scale * (W_qkv RMSNorm(x)); w holds the item's
 // weights (load_weights, issued by the caller)
 template <int kL, int kRows>
-__device__ bool qkv_item(const LayersArgs &a, const LayerPtrs &P, int l, int i, unsigned ep,
+__device__ bool qkv_item(const LayersArgs &a, const LayerG &P, int l, int i, unsigned ep,
                          const Lds &s, const u32x4 (&w)[kL][1]) {
   const int lane = threadIdx.x & 63, col = lane & 15;
   const float sc = P.sqkv[i * 16 + col];
@@ -417,12 +474,12 @@ __device__ bool qkv_item(const LayersArgs &a, const LayerPtrs &P, int l, int i, 
   if (!stage_rms<(kL + 3) / 4, kRows>(a, a.x0c, l == 0 ? a.x_in : nullptr, tag_of(ep, l - 1), P.norm1,
                                a.H, s.xs, s.misc))
     return false;
-  SH_MARK(l, 0);
+  SH_MARK(s.misc, l, 0);
   f32x4 acc[1];
   mfma_weights<kL, 1>(w, s.xs, a.H + 8, a.B, acc);
-  SH_MARK(l, 1);
+  SH_MARK(s.misc, l, 1);
   reduce_waves<1>(acc, s.red);
-  SH_MARK(l, 2);
+  SH_MARK(s.misc, l, 2);
   if (threadIdx.x < 64) {
     const unsigned tag = tag_of(ep, l);
 #pragma unroll
@@ -431,13 +488,13 @@ __device__ bool qkv_item(const LayersArgs &a, const LayerPtrs &P, int l, int i, 
       if (b < a.B) cst1(a.qkvc, (size_t)b * a.qkv_n + i * 16 + col, bits_of(acc[0][r] * sc), tag);
     }
   }
-  SH_MARK(l, 3);
+  SH_MARK(s.misc, l, 3);
   return true;
 }
 
 // C: x_mid[b][16 i + c] = x[b][.] + scale * (W_o attn)
 template <int kL, int kRows>
-__device__ bool o_item(const LayersArgs &a, const LayerPtrs &P, int l, int i, unsigned ep,
+__device__ bool o_item(const LayersArgs &a, const LayerG &P, int l, int i, unsigned ep,
                        const Lds &s) {
   const int lane = threadIdx.x & 63, col = lane & 15, K = a.heads * kD;
   u32x4 w[kL][1];
@@ -466,7 +523,7 @@ __device__ bool o_item(const LayersArgs &a, const LayerPtrs &P, int l, int i, un
 // D: act[b][16 p + c] = silu(scale_g * gate) * (scale_u * up) of RMSNorm(x_mid),
 // two adjacent columns per cell
 template <int kL, int kRows>
-__device__ bool up_item(const LayersArgs &a, const LayerPtrs &P, int l, int p, unsigned ep,
+__device__ bool up_item(const LayersArgs &a, const LayerG &P, int l, int p, unsigned ep,
                         const Lds &s) {
   const int lane = threadIdx.x & 63, col = lane & 15;
   u32x4 w[kL][2];
@@ -496,7 +553,7 @@ __device__ bool up_item(const LayersArgs &a, const LayerPtrs &P, int l, int p, u
 // E: x[b][16 i + c] = x_mid[b][.] + scale * (W_down act); the last layer
 // writes the plain buffer the final norm reads
 template <int kL, int kRows>
-__device__ bool down_item(const LayersArgs &a, const LayerPtrs &P, int l, int i, unsigned ep,
+__device__ bool down_item(const LayersArgs &a, const LayerG &P, int l, int i, unsigned ep,
                           const Lds &s) {
   const int lane = threadIdx.x & 63, col = lane & 15, K = a.inter;
   u32x4 w[kL][1];
@@ -508,12 +565,12 @@ __device__ bool down_item(const LayersArgs &a, const LayerPtrs &P, int l, int i,
   request_residual(a, a.x1c, nullptr, i * 16 + col, rv, rc);
   __builtin_amdgcn_sched_barrier(0);
   if (!stage_f16<(kL + 3) / 4, kRows>(a, a.actc, tag, K, s.xs, s.misc)) return false;
-  SH_MARK(l, 4);
+  SH_MARK(s.misc, l, 4);
   f32x4 acc[1];
   mfma_weights<kL, 1>(w, s.xs, K + 8, a.B, acc);
-  SH_MARK(l, 5);
+  SH_MARK(s.misc, l, 5);
   reduce_waves<1>(acc, s.red);
-  SH_MARK(l, 6);
+  SH_MARK(s.misc, l, 6);
   if (threadIdx.x < 64) {
     finish_residual(a, a.x1c, i * 16 + col, tag, rv, rc);
     const bool last = l + 1 == a.n_layers;
@@ -522,12 +579,12 @@ __device__ bool down_item(const LayersArgs &a, const LayerPtrs &P, int l, int i,
       const int b = 4 * (lane >> 4) + r;
       const float v = rv[r] + acc[0][r] * sc;
       if (b < a.B) {
-        if (last) a.x_in[(size_t)b * a.H + i * 16 + col] = v;
+        if (last) gbl(a.x_in)[(size_t)b * a.H + i * 16 + col] = v;
         else cst1(a.x0c, (size_t)b * a.H + i * 16 + col, bits_of(v), tag);
       }
     }
   }
-  SH_MARK(l, 7);
+  SH_MARK(s.misc, l, 7);
   return true;
 }
 
@@ -535,16 +592,29 @@ __device__ bool down_item(const LayersArgs &a, const LayerPtrs &P, int l, int i,
 
 constexpr int kPStride = kD + 4;  // cells per attention partial: acc[128], m, l, pad
 
+// Attention works on blocks of kBlk positions: the scores as q (heads as
+// MFMA rows) times K^T (positions as columns), ten 16-position tiles per
+// block, tiles w, w + 4, w + 8 on wave w; the V sums as P (fp16, heads as
+// rows) times V, five 32-position steps per block, output dims
+// [32 w, 32 w + 32) on wave w. The MFMA operands hold 8 consecutive values
+// of the contracted index per lane, so this kernel keeps V transposed per
+// KV head: vcache[b][kv_head][d][vt_stride] (positions contiguous).
+constexpr int kBlk = 160;
+constexpr int kKT = 3;           // K tiles of a block per wave
+constexpr int kVS = kBlk / 32;   // V steps of a block
+
 // LDS of an attention item, from the start of the dynamic area.
 template <int kG>
 struct AttnLds {
   float raw[(kG + 2) * kD];  // this row's q (kG heads), new k and new v as produced
   float qs[kG][kD];
-  _Float16 knew[kD], vnew[kD];
+  alignas(16) _Float16 knew[kD];
+  _Float16 vnew[kD];
   float scores[kG][kMaxSplitChunk];
+  alignas(16) _Float16 p[kG][kMaxSplitChunk + kBlk];  // probabilities, zero up to whole blocks
   float red[4][kG][kD];
   float wsum[8];
-  float stat[kG][2];
+  float wmax[4][kG], wl[4][kG];
 };
 
 // LDS of a merge item.
@@ -554,58 +624,75 @@ struct MergeLds {
   float acc[4][64][2];
 };
 
-constexpr int kLPP = kD / 8;     // lanes per position (8 dims each)
-constexpr int kPPW = 64 / kLPP;  // positions per wave step
-constexpr int kPPB = 4 * kPPW;   // positions per block step
-
+// K and V^T registers of one block (the first block of an item is
+// requested ahead by attn_prefetch): k[tt][kk] holds K[position 16 (w +
+// 4 tt) + lane % 16][32 kk + 8 (lane / 16) ..], v[nt][ks] holds
+// V^T[dim 32 w + 16 nt + lane % 16][positions 32 ks + 8 (lane / 16) ..].
 struct AttnKV {
-  f16x8 k8[kAttnBatch], v8[kAttnBatch];
+  f16x8 k[kKT][4];
+  f16x8 v[2][kVS];
 };
 
-// K / V of the first kAttnBatch block steps of item `item`, clamped into the
-// cache (positions past the context are loaded and never used).
-__device__ __forceinline__ void attn_prefetch(const LayersArgs &a, const LayerPtrs &P, int item,
-                                              AttnKV &kv) {
-  const int splits = a.splits, kvn = a.kv_heads;
-  const int s = item % splits, kvh = (item / splits) % kvn, b = item / (splits * kvn);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int chunk = a.chunk, p0 = s * chunk;
-  const int cap = min(chunk, a.max_pos - p0);
-  const size_t cache_base = ((size_t)b * kvn + kvh) * (size_t)a.max_pos * kD;
-  const int seg = lane % kLPP, sub = lane / kLPP;
-  const uint16_t *kbase = P.kcache + cache_base + seg * 8;
-  const uint16_t *vbase = P.vcache + cache_base + seg * 8;
-  const int last = max(cap, 1) - 1;
+__device__ __forceinline__ void attn_load_k(const LayersArgs &a, const SH_GLOBAL uint16_t *kb, int pb,
+                                            AttnKV &kv) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, grp = lane >> 4;
 #pragma unroll
-  for (int u = 0; u < kAttnBatch; u++) {
-    const int p = min(p0 + min(u * kPPB + wave * kPPW + sub, last), a.max_pos - 1);
-    kv.k8[u] = *reinterpret_cast<const f16x8 *>(kbase + (size_t)p * kD);
-    kv.v8[u] = *reinterpret_cast<const f16x8 *>(vbase + (size_t)p * kD);
+  for (int tt = 0; tt < kKT; tt++) {
+    const int p = min(pb + 16 * (wave + 4 * tt) + r, a.max_pos - 1);
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++)
+      kv.k[tt][kk] = *reinterpret_cast<const SH_GLOBAL f16x8 *>(kb + (size_t)p * kD + 32 * kk + 8 * grp);
   }
 }
 
-// B: item = (b, KV head, split), its K / V requested by attn_prefetch.
-// Scores positions [p0, p0 + chunk) of the context for the kG query heads
-// of the KV head (Qwen3: RMSNorm of q and of the new k over the head, RoPE
-// rotate-half at this step's position; the split holding it appends the new
-// k / v to the cache) and writes the partial (unnormalised V sum, max, sum)
-// of each head as cells. Splits past the context write nothing.
+__device__ __forceinline__ void attn_load_v(const LayersArgs &a, const SH_GLOBAL uint16_t *vtb, int pb,
+                                            AttnKV &kv) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, grp = lane >> 4;
+#pragma unroll
+  for (int nt = 0; nt < 2; nt++) {
+    const SH_GLOBAL uint16_t *row = vtb + (size_t)(32 * wave + 16 * nt + r) * a.vt_stride;
+#pragma unroll
+    for (int ks = 0; ks < kVS; ks++) {
+      const int p = min(pb + 32 * ks + 8 * grp, a.vt_stride - 8);
+      kv.v[nt][ks] = *reinterpret_cast<const SH_GLOBAL f16x8 *>(row + p);
+    }
+  }
+}
+
+// Requests K / V^T of the first block of attention item `item`.
+__device__ __forceinline__ void attn_prefetch(const LayersArgs &a, const LayerG &P, int item,
+                                              AttnKV &kv) {
+  const int splits = a.splits, kvn = a.kv_heads;
+  const int s = item % splits, kvh = (item / splits) % kvn, b = item / (splits * kvn);
+  const size_t kv_row = (size_t)b * kvn + kvh;
+  const int pb = min(s * a.chunk, a.max_pos - 1);
+  attn_load_k(a, P.kcache + kv_row * a.max_pos * kD, pb, kv);
+  attn_load_v(a, P.vcache + kv_row * kD * a.vt_stride, pb, kv);
+}
+
+// B: item = (b, KV head, split), its first K / V^T block requested by
+// attn_prefetch. Scores positions [p0, p0 + chunk) of the context for the
+// kG query heads of the KV head (Qwen3: RMSNorm of q and of the new k over
+// the head, RoPE rotate-half at this step's position; the split holding it
+// appends the new k / v to the cache) and writes the partial (unnormalised
+// V sum, max, sum) of each head as cells. Splits past the context write
+// nothing.
 template <int kG>
-__device__ bool attn_item(const LayersArgs &a, const LayerPtrs &P, int l, int item, unsigned ep,
+__device__ bool attn_item(const LayersArgs &a, const LayerG &P, int l, int item, unsigned ep,
                           uint8_t *smem, Misc *misc, AttnKV &kv) {
   static_assert((kG + 2) * kD / 2 <= kT, "one pair of q / k / v cells per thread");
+  static_assert(kG <= 4, "MFMA rows 0..3 of lanes 0..15 hold the heads");
   AttnLds<kG> &S = *reinterpret_cast<AttnLds<kG> *>(smem);
   const int splits = a.splits, kvn = a.kv_heads;
   const int s = item % splits, kvh = (item / splits) % kvn, b = item / (splits * kvn);
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, r = lane & 15, grp = lane >> 4;
   const int chunk = a.chunk, p0 = s * chunk;
   const int cap = min(chunk, a.max_pos - p0);  // <= 0 for splits past the cache
-  const size_t cache_base = ((size_t)b * kvn + kvh) * (size_t)a.max_pos * kD;
-  const int seg = lane % kLPP, sub = lane / kLPP;
-  const uint16_t *kbase = P.kcache + cache_base + seg * 8;
-  const uint16_t *vbase = P.vcache + cache_base + seg * 8;
+  const size_t kv_row = (size_t)b * kvn + kvh;
+  SH_GLOBAL uint16_t *kb = P.kcache + kv_row * a.max_pos * kD;
+  SH_GLOBAL uint16_t *vtb = P.vcache + kv_row * kD * a.vt_stride;
 
-  const int L = a.pos[b] + 1;  // context including the new token
+  const int L = gbl(a.pos)[b] + 1;  // context including the new token
   const int active = (L + chunk - 1) / chunk;
   if (s >= active || cap <= 0 || L > a.max_pos) return true;  // uniform
   const int h0 = kvh * kG;
@@ -622,23 +709,24 @@ __device__ bool attn_item(const LayersArgs &a, const LayerPtrs &P, int l, int it
     const bool ok = spin_cells(a, a.qkvc, [&](int k) { return cell + k; }, t < kPairs ? 3ull : 0ull,
                                tag, cv);
     if (!waits_ok(a, ok, misc)) return false;
-    SH_MARK(l, 8);
+    SH_MARK(misc, l, 8);
     if (t < kPairs) {
       S.raw[2 * t] = cell_f32(cv[0]);
       S.raw[2 * t + 1] = cell_f32(cv[1]);
     }
-    __syncthreads();
+    lds_barrier();
   }
+  const int p1 = min(L, p0 + chunk), np = p1 - p0, pos = L - 1;
+  const bool holds_new = p1 == L;  // this split holds the new token (S.knew / S.vnew)
   {
     const int gq = t / kD, iq = t % kD, half = kD / 2, fi = iq % half;
     const bool q_thread = t < kG * kD;
-    const int p1 = min(L, p0 + chunk), np = p1 - p0, pos = L - 1;
-    const bool kv_thread = p1 == L && t < kD;
+    const bool kv_thread = holds_new && t < kD;
     float qv = S.raw[min(t, kG * kD - 1)];
     float knv = S.raw[kG * kD + iq];
     const float vv = S.raw[(kG + 1) * kD + iq];
     const float qn = P.q_norm[iq], kn = P.k_norm[iq];
-    const float cs = a.rope[(size_t)b * kD + fi], sn = a.rope[(size_t)b * kD + half + fi];
+    const float cs = gbl(a.rope)[(size_t)b * kD + fi], sn = gbl(a.rope)[(size_t)b * kD + half + fi];
     if (!q_thread) qv = 0.0f;
     if (!kv_thread) knv = 0.0f;
     // RMSNorm over each head (kD / 64 waves per head), then RoPE
@@ -649,7 +737,7 @@ __device__ bool attn_item(const LayersArgs &a, const LayerPtrs &P, int l, int it
         S.wsum[wave] = qss;
         S.wsum[4 + wave] = kss;
       }
-      __syncthreads();
+      lds_barrier();
       if (q_thread) {
         float ss = 0.0f;
 #pragma unroll
@@ -664,7 +752,7 @@ __device__ bool attn_item(const LayersArgs &a, const LayerPtrs &P, int l, int it
       }
       if (q_thread) S.red[2][gq][iq] = qv;
       if (kv_thread) S.red[3][0][iq] = knv;
-      __syncthreads();
+      lds_barrier();
       if (q_thread) {
         const float other = S.red[2][gq][iq < half ? iq + half : iq - half];
         qv = iq < half ? qv * cs - other * sn : qv * cs + other * sn;
@@ -679,136 +767,136 @@ __device__ bool attn_item(const LayersArgs &a, const LayerPtrs &P, int l, int it
       const _Float16 k16 = (_Float16)knv, v16 = (_Float16)vv;
       S.knew[iq] = k16;
       S.vnew[iq] = v16;
-      P.kcache[cache_base + (size_t)pos * kD + iq] = __builtin_bit_cast(uint16_t, k16);
-      P.vcache[cache_base + (size_t)pos * kD + iq] = __builtin_bit_cast(uint16_t, v16);
+      kb[(size_t)pos * kD + iq] = __builtin_bit_cast(uint16_t, k16);
+      vtb[(size_t)iq * a.vt_stride + pos] = __builtin_bit_cast(uint16_t, v16);
     }
-    __syncthreads();
+    lds_barrier();
+  }
+  SH_MARK(misc, l, 9);
 
-    SH_MARK(l, 9);
-    float q8[kG][8];
+  // q as the MFMA A operand: row lane % 16 = head (zero past kG), k = 32 kk + 8 (lane / 16)
+  // (read unconditionally from a clamped row, then selected: a conditional
+  // read compiles to one branch and one LDS wait per element)
+  f16x8 qa[4];
+  {
+    const float *qrow = &S.qs[min(r, kG - 1)][8 * grp];
 #pragma unroll
-    for (int g = 0; g < kG; g++)
+    for (int kk = 0; kk < 4; kk++) {
+      const f32x4 lo = *reinterpret_cast<const f32x4 *>(qrow + 32 * kk);
+      const f32x4 hi = *reinterpret_cast<const f32x4 *>(qrow + 32 * kk + 4);
 #pragma unroll
-      for (int e = 0; e < 8; e++) q8[g][e] = S.qs[g][seg * 8 + e];
-#pragma unroll
-    for (int u = 0; u < kAttnBatch; u++) {  // the new token's K / V
-      const int pi = u * kPPB + wave * kPPW + sub;
-      if (pi < np && p0 + pi == pos) {
-        kv.k8[u] = *reinterpret_cast<const f16x8 *>(&S.knew[seg * 8]);
-        kv.v8[u] = *reinterpret_cast<const f16x8 *>(&S.vnew[seg * 8]);
+      for (int e = 0; e < 4; e++) {
+        qa[kk][e] = r < kG ? (_Float16)lo[e] : (_Float16)0.0f;
+        qa[kk][e + 4] = r < kG ? (_Float16)hi[e] : (_Float16)0.0f;
       }
-    }
-
-    // scores: a position's 16 lanes are one DPP row
-    for (int base = 0; base < np; base += kAttnBatch * kPPB) {
-      if (base > 0) {
-#pragma unroll
-        for (int u = 0; u < kAttnBatch; u++) {
-          const int pi = base + u * kPPB + wave * kPPW + sub, p = p0 + pi;
-          kv.k8[u] = f16x8{};
-          if (pi < np)
-            kv.k8[u] = p == pos ? *reinterpret_cast<const f16x8 *>(&S.knew[seg * 8])
-                                : *reinterpret_cast<const f16x8 *>(kbase + (size_t)p * kD);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < kAttnBatch; u++) {
-        const int pi = base + u * kPPB + wave * kPPW + sub;
-#pragma unroll
-        for (int g = 0; g < kG; g++) {
-          float d = 0.0f;
-#pragma unroll
-          for (int e = 0; e < 8; e++) d += q8[g][e] * (float)kv.k8[u][e];
-          d = row16_sum(d);
-          if (seg == 0 && pi < np) S.scores[g][pi] = d;
-        }
-      }
-    }
-    __syncthreads();
-
-    SH_MARK(l, 10);
-    // softmax statistics (wave g for head g)
-    if (wave < kG) {
-      const int g = wave;
-      float m = -INFINITY;
-      for (int i = lane; i < np; i += 64) m = fmaxf(m, S.scores[g][i]);
-      m = wave_max_rows(m);
-      float lsum = 0.0f;
-      for (int i = lane; i < np; i += 64) {
-        const float e = expf(S.scores[g][i] - m);
-        S.scores[g][i] = e;
-        lsum += e;
-      }
-      lsum = wave_sum_rows(lsum);
-      if (lane == 0) {
-        S.stat[g][0] = m;
-        S.stat[g][1] = lsum;
-      }
-    }
-    __syncthreads();
-
-    SH_MARK(l, 11);
-    // unnormalised V sums
-    float acc[kG][8];
-#pragma unroll
-    for (int g = 0; g < kG; g++)
-#pragma unroll
-      for (int e = 0; e < 8; e++) acc[g][e] = 0.0f;
-    for (int base = 0; base < np; base += kAttnBatch * kPPB) {
-      if (base > 0) {
-#pragma unroll
-        for (int u = 0; u < kAttnBatch; u++) {
-          const int pi = base + u * kPPB + wave * kPPW + sub, p = p0 + pi;
-          kv.v8[u] = f16x8{};
-          if (pi < np)
-            kv.v8[u] = p == pos ? *reinterpret_cast<const f16x8 *>(&S.vnew[seg * 8])
-                                : *reinterpret_cast<const f16x8 *>(vbase + (size_t)p * kD);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < kAttnBatch; u++) {
-        const int pi = base + u * kPPB + wave * kPPW + sub;
-        if (pi < np) {
-#pragma unroll
-          for (int g = 0; g < kG; g++) {
-            const float wgt = S.scores[g][pi];
-#pragma unroll
-            for (int e = 0; e < 8; e++) acc[g][e] += wgt * (float)kv.v8[u][e];
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < kG; g++)
-#pragma unroll
-      for (int e = 0; e < 8; e++) {
-        float v = acc[g][e];
-#pragma unroll
-        for (int off = kLPP; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
-        acc[g][e] = v;
-      }
-    if (sub == 0) {
-#pragma unroll
-      for (int g = 0; g < kG; g++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) S.red[wave][g][seg * 8 + e] = acc[g][e];
-    }
-    __syncthreads();
-    SH_MARK(l, 12);
-    if (t < kG * kD / 2) {
-      const int g = t / (kD / 2), i = 2 * (t % (kD / 2));
-      const size_t pp = (((size_t)b * a.heads + h0 + g) * splits + s) * kPStride;
-      cst2(a.partc, pp + i,
-           bits_of(S.red[0][g][i] + S.red[1][g][i] + S.red[2][g][i] + S.red[3][g][i]),
-           bits_of(S.red[0][g][i + 1] + S.red[1][g][i + 1] + S.red[2][g][i + 1] + S.red[3][g][i + 1]),
-           tag);
-    } else if (t < kG * kD / 2 + kG) {
-      const int g = t - kG * kD / 2;
-      const size_t pp = (((size_t)b * a.heads + h0 + g) * splits + s) * kPStride;
-      cst2(a.partc, pp + kD, bits_of(S.stat[g][0]), bits_of(S.stat[g][1]), tag);
     }
   }
-  SH_MARK(l, 13);
+  const int nblk = (np + kBlk - 1) / kBlk;
+
+  // scores: lanes 0..15 of a tile's result hold heads 0..3 of its 16 positions
+  for (int bb = 0; bb < nblk; bb++) {
+    const int pb = p0 + bb * kBlk;
+    if (bb > 0) attn_load_k(a, kb, pb, kv);
+#pragma unroll
+    for (int tt = 0; tt < kKT; tt++) {
+      const int tile = wave + 4 * tt;
+      if (tile >= kBlk / 16) continue;  // uniform
+      if (holds_new && pb + 16 * tile + r == pos) {  // the new token's K (not in the requested copy)
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) kv.k[tt][kk] = *reinterpret_cast<const f16x8 *>(&S.knew[32 * kk + 8 * grp]);
+      }
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 4; kk++) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[kk], kv.k[tt][kk], acc, 0, 0, 0);
+      const int pi = bb * kBlk + 16 * tile + lane;
+      if (lane < 16 && pi < np) {
+#pragma unroll
+        for (int g = 0; g < kG; g++) S.scores[g][pi] = acc[g];
+      }
+    }
+  }
+  lds_barrier();
+  SH_MARK(misc, l, 10);
+
+  // softmax statistics per head over the np scores; P = exp(s - M) in fp16,
+  // zero up to whole blocks, and l = the sum of those fp16 values
+  float M[kG], lsum[kG];
+  {
+#pragma unroll
+    for (int g = 0; g < kG; g++) M[g] = -INFINITY;
+    for (int i = t; i < np; i += kT)
+#pragma unroll
+      for (int g = 0; g < kG; g++) M[g] = fmaxf(M[g], S.scores[g][i]);
+#pragma unroll
+    for (int g = 0; g < kG; g++) {
+      M[g] = wave_max_rows(M[g]);
+      if (lane == 0) S.wmax[wave][g] = M[g];
+    }
+    lds_barrier();
+#pragma unroll
+    for (int g = 0; g < kG; g++) {
+      M[g] = fmaxf(fmaxf(S.wmax[0][g], S.wmax[1][g]), fmaxf(S.wmax[2][g], S.wmax[3][g]));
+      lsum[g] = 0.0f;
+    }
+    for (int i = t; i < nblk * kBlk; i += kT) {
+      const int ic = min(i, np - 1);
+#pragma unroll
+      for (int g = 0; g < kG; g++) {
+        const float ev = expf(S.scores[g][ic] - M[g]);
+        const _Float16 e = i < np ? (_Float16)ev : (_Float16)0.0f;
+        S.p[g][i] = e;
+        lsum[g] += (float)e;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < kG; g++) {
+      lsum[g] = wave_sum_rows(lsum[g]);
+      if (lane == 0) S.wl[wave][g] = lsum[g];
+    }
+    lds_barrier();
+#pragma unroll
+    for (int g = 0; g < kG; g++) lsum[g] = (S.wl[0][g] + S.wl[1][g]) + (S.wl[2][g] + S.wl[3][g]);
+  }
+  SH_MARK(misc, l, 11);
+
+  // V sums: wave w owns dims [32 w, 32 w + 32); vn = the new token's V at
+  // this lane's two dims (substituted by selects, not per-element branches)
+  f32x4 oacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  const _Float16 vn[2] = {S.vnew[32 * wave + r], S.vnew[32 * wave + 16 + r]};
+  for (int bb = 0; bb < nblk; bb++) {
+    const int pb = p0 + bb * kBlk;
+    if (bb > 0) attn_load_v(a, vtb, pb, kv);
+#pragma unroll
+    for (int ks = 0; ks < kVS; ks++) {
+      const int q0 = pb + 32 * ks + 8 * grp;
+      if (holds_new && pos >= q0 && pos < q0 + 8) {  // the new token's V
+        const int e0 = pos - q0;
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+          for (int e = 0; e < 8; e++) kv.v[nt][ks][e] = e == e0 ? vn[nt] : kv.v[nt][ks][e];
+      }
+      const f16x8 pr = *reinterpret_cast<const f16x8 *>(&S.p[min(r, kG - 1)][bb * kBlk + 32 * ks + 8 * grp]);
+      const f16x8 pa = r < kG ? pr : f16x8{};
+#pragma unroll
+      for (int nt = 0; nt < 2; nt++) oacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, kv.v[nt][ks], oacc[nt], 0, 0, 0);
+    }
+  }
+  SH_MARK(misc, l, 12);
+  // lanes 0..15: oacc[nt][g] = sum_p P[g][p] V[p][32 w + 16 nt + lane]
+  if (lane < 16) {
+#pragma unroll
+    for (int g = 0; g < kG; g++) {
+      const size_t pp = (((size_t)b * a.heads + h0 + g) * splits + s) * kPStride;
+#pragma unroll
+      for (int nt = 0; nt < 2; nt++) cst1(a.partc, pp + 32 * wave + 16 * nt + lane, bits_of(oacc[nt][g]), tag);
+    }
+  }
+  if (t < kG) {
+    const size_t pp = (((size_t)b * a.heads + h0 + t) * splits + s) * kPStride;
+    cst2(a.partc, pp + kD, bits_of(M[t]), bits_of(lsum[t]), tag);
+  }
+  SH_MARK(misc, l, 13);
   return true;
 }
 
@@ -826,7 +914,7 @@ __device__ bool merge_item(const LayersArgs &a, int l, int item, unsigned ep, ui
   MergeLds &S = *reinterpret_cast<MergeLds *>(smem);
   const int h = item % a.heads, b = item / a.heads;
   const int t = threadIdx.x, q = t & 63, sg = t >> 6;
-  const int L = a.pos[b] + 1;
+  const int L = gbl(a.pos)[b] + 1;
   const int active = min((L + a.chunk - 1) / a.chunk, a.splits);
   const size_t base = ((size_t)b * a.heads + h) * a.splits * kPStride;
   const unsigned tag = tag_of(ep, l);
@@ -846,12 +934,12 @@ __device__ bool merge_item(const LayersArgs &a, int l, int item, unsigned ep, ui
                              },
                              mask, tag, cv);
   if (!waits_ok(a, ok, misc)) return false;
-  SH_MARK(l, 14);
+  SH_MARK(misc, l, 14);
   if (t < active) {
     S.m[t] = cell_f32(cv[2 * kPer]);
     S.l[t] = cell_f32(cv[2 * kPer + 1]);
   }
-  __syncthreads();
+  lds_barrier();
   if (t < 64) {
     const float mj = t < active ? S.m[t] : -INFINITY;
     const float lj = t < active ? S.l[t] : 0.0f;
@@ -861,20 +949,18 @@ __device__ bool merge_item(const LayersArgs &a, int l, int item, unsigned ep, ui
     S.w[t] = wj;
     if (t == 0) S.lsum = lw;
   }
-  __syncthreads();
+  lds_barrier();
   float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
   for (int k = 0; k < kPer; k++) {
     const int j = sg + 4 * k;
-    if (j < active) {
-      const float wj = S.w[j];
-      s0 += wj * cell_f32(cv[2 * k]);
-      s1 += wj * cell_f32(cv[2 * k + 1]);
-    }
+    const float wj = S.w[j];  // 0 past active (the cells there repeat a valid split)
+    s0 += wj * cell_f32(cv[2 * k]);
+    s1 += wj * cell_f32(cv[2 * k + 1]);
   }
   S.acc[sg][q][0] = s0;
   S.acc[sg][q][1] = s1;
-  __syncthreads();
+  lds_barrier();
   if (t < 64) {
     const float inv = 1.0f / S.lsum;
     const float v0 = (S.acc[0][q][0] + S.acc[1][q][0]) + (S.acc[2][q][0] + S.acc[3][q][0]);
@@ -883,8 +969,8 @@ __device__ bool merge_item(const LayersArgs &a, int l, int item, unsigned ep, ui
                             ((uint32_t)f32_to_f16_bits(v1 * inv) << 16);
     cst1(a.attnc, (size_t)(b * a.heads + h) * (kD / 2) + q, packed, tag);
   }
-  SH_MARK(l, 15);
-  __syncthreads();  // the next item reuses the LDS
+  SH_MARK(misc, l, 15);
+  lds_barrier();  // the next item reuses the LDS
   return true;
 }
 
@@ -902,6 +988,12 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
   lds.red = reinterpret_cast<float *>(smem + xs_max);
   lds.misc = misc;
 
+  if (threadIdx.x < 4) misc->par[threadIdx.x] = 0;
+#ifdef SH_DECODE_TRACE
+  for (int i = threadIdx.x; i < 2 * kTraceLayers * kTraceSlots; i += kT)
+    (&misc->tr[0][0][0])[i] = 0;
+#endif
+  lds_barrier();
   const unsigned ep = *a.epoch;
   const int G = gridDim.x, w = blockIdx.x;
   const int nA = a.qkv_n / 16, nB = B * a.kv_heads * a.splits, nM = B * a.heads;
@@ -911,53 +1003,61 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
   const bool hasC = w < nC;
   AttnKV kv;
   u32x4 wa[kLA][1];  // this workgroup's first QKV item's weights
-  if (w < nA) load_weights<kLA, 1>(wa, a.layers[0].wqkv, H, w);
-  if (w < nB) attn_prefetch(a, a.layers[0], w, kv);
+  if (w < nA) load_weights<kLA, 1>(wa, gbl(a.layers[0].wqkv), H, w);
+  if (w < nB) attn_prefetch(a, layer_g(a.layers[0]), w, kv);
   for (int l = 0; l < a.n_layers; l++) {
-    const LayerPtrs P = a.layers[l];
+    const LayerG P = layer_g(a.layers[l]);
     const bool next = l + 1 < a.n_layers;
     for (int i = w; i < nA; i += G) {
       if (i != w) load_weights<kLA, 1>(wa, P.wqkv, H, i);
-      if (i == w) SH_TRACE(l, 0);
+      if (i == w) SH_TRACE(misc, l, 0);
       if (!qkv_item<kLA, kRows>(a, P, l, i, ep, lds, wa)) return;
-      if (i == w) { SH_TRACE(l, 1); SH_TRACE_WAIT(l, 0, misc); }
+      if (i == w) { SH_TRACE(misc, l, 1); SH_TRACE_WAIT(l, 0, misc); }
     }
     for (int i = w; i < nB; i += G) {
       if (i != w) attn_prefetch(a, P, i, kv);
-      if (i == w) SH_TRACE(l, 2);
+      if (i == w) SH_TRACE(misc, l, 2);
       if (!attn_item<kG>(a, P, l, i, ep, smem, misc, kv)) return;
-      if (i == w) { SH_TRACE(l, 3); SH_TRACE_WAIT(l, 1, misc); }
+      if (i == w) { SH_TRACE(misc, l, 3); SH_TRACE_WAIT(l, 1, misc); }
     }
     for (int j = m0; j < nM; j += G) {
       if (!merge_item<kSP>(a, l, j, ep, smem, misc)) return;
-      if (j == m0) SH_TRACE(l, 15);
+      if (j == m0) SH_TRACE(misc, l, 15);
     }
     // O, gate/up and down items request their weights when they start: at
     // batch 1 each workgroup's previous item is then a phase or more behind
     for (int i = w; i < nC; i += G) {
-      if (i == w) SH_TRACE(l, 4);
+      if (i == w) SH_TRACE(misc, l, 4);
       if (!o_item<kLC, kRows>(a, P, l, i, ep, lds)) return;
-      if (i == w) { SH_TRACE(l, 5); SH_TRACE_WAIT(l, 2, misc); }
+      if (i == w) { SH_TRACE(misc, l, 5); SH_TRACE_WAIT(l, 2, misc); }
     }
     // workgroups with an O item: the next layer's K / V while the gate/up
     // items run; the others after their gate/up item, with the next QKV weights
-    if (hasC && next && w < nB) attn_prefetch(a, a.layers[l + 1], w, kv);
+    if (hasC && next && w < nB) attn_prefetch(a, layer_g(a.layers[l + 1]), w, kv);
     for (int i = d0; i < nD; i += G) {
-      if (i == d0) SH_TRACE(l, 6);
+      if (i == d0) SH_TRACE(misc, l, 6);
       if (!up_item<kLD, kRows>(a, P, l, i, ep, lds)) return;
-      if (i == d0) { SH_TRACE(l, 7); SH_TRACE_WAIT(l, 3, misc); }
+      if (i == d0) { SH_TRACE(misc, l, 7); SH_TRACE_WAIT(l, 3, misc); }
     }
     if (!hasC && next) {
-      if (w < nB) attn_prefetch(a, a.layers[l + 1], w, kv);
-      if (w < nA) load_weights<kLA, 1>(wa, a.layers[l + 1].wqkv, H, w);
+      if (w < nB) attn_prefetch(a, layer_g(a.layers[l + 1]), w, kv);
+      if (w < nA) load_weights<kLA, 1>(wa, gbl(a.layers[l + 1].wqkv), H, w);
     }
     for (int i = w; i < nE; i += G) {
-      if (i == w) SH_TRACE(l, 8);
+      if (i == w) SH_TRACE(misc, l, 8);
       if (!down_item<kLE, kRows>(a, P, l, i, ep, lds)) return;
-      if (i == w) { SH_TRACE(l, 9); SH_TRACE_WAIT(l, 4, misc); }
+      if (i == w) { SH_TRACE(misc, l, 9); SH_TRACE_WAIT(l, 4, misc); }
     }
-    if (hasC && next && w < nA) load_weights<kLA, 1>(wa, a.layers[l + 1].wqkv, H, w);
+    if (hasC && next && w < nA) load_weights<kLA, 1>(wa, gbl(a.layers[l + 1].wqkv), H, w);
   }
+#ifdef SH_DECODE_TRACE
+  lds_barrier();
+  if (w < kTraceWgs)
+    for (int i = threadIdx.x; i < 2 * kTraceLayers * kTraceSlots; i += kT) {
+      const int set = i / (kTraceLayers * kTraceSlots), rem = i % (kTraceLayers * kTraceSlots);
+      g_decode_trace[set][w][rem / kTraceSlots][rem % kTraceSlots] = (&misc->tr[0][0][0])[i];
+    }
+#endif
 }
 
 // (kG, loads per lane of qkv / o / gate-up / down items, most splits per
@@ -1043,13 +1143,8 @@ hipError_t decode_layers_occupancy(const LayersArgs &a, size_t lds, int *blocks_
 
 #ifdef SH_DECODE_TRACE
 hipError_t decode_layers_trace(void *dst, size_t bytes) {
-  const size_t one = sizeof(g_decode_trace);
-  hipError_t e = hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_decode_trace), bytes < one ? bytes : one, 0,
-                                     hipMemcpyDeviceToHost);
-  if (e != hipSuccess || bytes <= one) return e;
-  bytes -= one;
-  return hipMemcpyFromSymbol(static_cast<char *>(dst) + one, HIP_SYMBOL(g_decode_trace2),
-                             bytes < one ? bytes : one, 0, hipMemcpyDeviceToHost);
+  if (bytes > sizeof(g_decode_trace)) bytes = sizeof(g_decode_trace);
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_decode_trace), bytes, 0, hipMemcpyDeviceToHost);
 }
 #endif
 

@@ -83,11 +83,12 @@ struct LayerPtrs {
   const uint8_t *wqkv, *wo, *wup, *wdown;  // FP8 tiled (gate/up tiles interleaved)
   const float *sqkv, *so, *sup, *sdown;    // per-row scales
   const float *norm1, *norm2, *q_norm, *k_norm;
-  uint16_t *kcache, *vcache;               // [max_batch][kv_heads][max_pos][128] fp16
+  uint16_t *kcache;  // [max_batch][kv_heads][max_pos][128] fp16
+  uint16_t *vcache;  // transposed: [max_batch][kv_heads][128][vt_stride] fp16
 };
 
 // Everything the kernel hands between workgroups within a step travels in
-// 8-byte cells of uncached device memory (payload word, then the producing
+// 8-byte cells of device memory (payload word, then the producing
 // step and layer's tag word; see decode_layers.hip). Cell buffers:
 //   x0c   [kMaxBatch][H]          layer output x (fp32), read by the next layer
 //   x1c   [kMaxBatch][H]          x_mid after attention (fp32)
@@ -100,6 +101,7 @@ struct LayersArgs {
   const LayerPtrs *layers = nullptr;  // [n_layers]
   int n_layers = 0, B = 0, H = 0, heads = 0, kv_heads = 0, inter = 0, qkv_n = 0;
   int max_pos = 0, splits = 1, chunk = 16;
+  int vt_stride = 0;                   // positions per V^T cache row: max_pos rounded up to 16
   float eps = 1e-6f, scale = 1.0f;     // RMSNorm epsilon, attention 1 / sqrt(d)
   const int *pos = nullptr;            // [B] this step's position (embed kernel)
   const float *rope = nullptr;         // [B][128]: cos | sin (embed kernel)

@@ -11,7 +11,6 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
-#include <mutex>
 #include <string>
 #include <vector>
 
@@ -83,7 +82,6 @@ struct sh_llm {
   int layers_grid = 0;
   size_t layers_lds = 0;
   unsigned *epoch = nullptr;
-  std::vector<void *> uc_blocks;  // uncached blocks taken from the process pool
 };
 
 namespace {
@@ -99,64 +97,6 @@ int llm_alloc(sh_llm *m, size_t bytes, void **p) {
   if (rc != SH_OK) return rc;
   SH_HIP_TRY(hipMemsetAsync(*p, 0, bytes, stream_of(m->ctx)));
   return SH_OK;
-}
-
-// Uncached device memory backs the decode-layers kernel's exchange buffers.
-// It is never freed (freeing uncached memory that kernels have read has
-// corrupted later allocations on this platform): a destroyed model returns
-// its blocks to this per-process pool, and the next model on the same device
-// takes them from it.
-struct UcBlock {
-  int device;
-  void *p;
-  size_t bytes;
-  bool used;
-};
-std::mutex g_uc_mu;
-std::vector<UcBlock> g_uc_pool;
-
-int uc_alloc(sh_llm *m, size_t bytes, void **p) {
-  *p = nullptr;
-  bytes = (bytes + 255) / 256 * 256;
-  const int dev = device_of(m->ctx);
-  {
-    std::lock_guard<std::mutex> lock(g_uc_mu);
-    UcBlock *best = nullptr;
-    for (UcBlock &b : g_uc_pool)
-      if (!b.used && b.device == dev && b.bytes >= bytes && (!best || b.bytes < best->bytes)) best = &b;
-    if (best) {
-      best->used = true;
-      *p = best->p;
-      bytes = best->bytes;
-    }
-  }
-  if (!*p) {
-    SH_HIP_TRY(hipExtMallocWithFlags(p, bytes, hipDeviceMallocUncached));
-    std::lock_guard<std::mutex> lock(g_uc_mu);
-    g_uc_pool.push_back(UcBlock{dev, *p, bytes, true});
-  }
-  m->uc_blocks.push_back(*p);
-  const int rc = sh_register_external(m->ctx, *p, bytes);  // readable with sh_download
-  if (rc != SH_OK) return rc;
-  SH_HIP_TRY(hipMemsetAsync(*p, 0, bytes, stream_of(m->ctx)));
-  return SH_OK;
-}
-
-template <class T>
-int uc_alloc_n(sh_llm *m, size_t n, T **p) {
-  void *v = nullptr;
-  int rc = uc_alloc(m, n * sizeof(T), &v);
-  *p = static_cast<T *>(v);
-  return rc;
-}
-
-void uc_release(sh_llm *m) {
-  for (void *p : m->uc_blocks) (void)sh_unregister_external(m->ctx, p);
-  std::lock_guard<std::mutex> lock(g_uc_mu);
-  for (void *p : m->uc_blocks)
-    for (UcBlock &b : g_uc_pool)
-      if (b.p == p) b.used = false;
-  m->uc_blocks.clear();
 }
 
 template <class T>
@@ -370,6 +310,7 @@ int setup_layers_kernel(sh_llm *m) {
   a.inter = c.intermediate;
   a.qkv_n = m->qkv_n;
   a.max_pos = c.max_positions;
+  a.vt_stride = (c.max_positions + 15) / 16 * 16;
   a.eps = c.norm_eps;
   a.scale = 1.0f / std::sqrt((float)c.head_dim);
   a.pos = m->pos;
@@ -385,11 +326,13 @@ int setup_layers_kernel(sh_llm *m) {
   if (per_cu < 1) return SH_OK;
   int rc;
   const size_t MB = kMaxBatch;
-  if ((rc = uc_alloc_n(m, MB * c.hidden, &a.x0c)) || (rc = uc_alloc_n(m, MB * c.hidden, &a.x1c)) ||
-      (rc = uc_alloc_n(m, MB * m->qkv_n, &a.qkvc)) ||
-      (rc = uc_alloc_n(m, decode_layers_partial_cells(c.heads), &a.partc)) ||
-      (rc = uc_alloc_n(m, MB * c.heads * c.head_dim / 2, &a.attnc)) ||
-      (rc = uc_alloc_n(m, MB * c.intermediate / 2, &a.actc)) || (rc = uc_alloc_n(m, 64, &a.err)) ||
+  // ordinary device memory: every access to these is an agent-scope atomic,
+  // which the memory model keeps coherent across the XCDs' separate L2s
+  if ((rc = alloc_n(m, MB * c.hidden, &a.x0c)) || (rc = alloc_n(m, MB * c.hidden, &a.x1c)) ||
+      (rc = alloc_n(m, MB * m->qkv_n, &a.qkvc)) ||
+      (rc = alloc_n(m, decode_layers_partial_cells(c.heads), &a.partc)) ||
+      (rc = alloc_n(m, MB * c.heads * c.head_dim / 2, &a.attnc)) ||
+      (rc = alloc_n(m, MB * c.intermediate / 2, &a.actc)) || (rc = alloc_n(m, 64, &a.err)) ||
       (rc = alloc_n(m, 64, &m->epoch)))
     return rc;
   a.x_in = m->x;
@@ -528,7 +471,9 @@ SH_API int sh_llm_create(sh_ctx *ctx, const sh_llm_config *config, sh_llm **out)
   }
   m->vocab_pad = (c.vocab + 15) / 16 * 16;
   const int B = c.max_batch, H = c.hidden, d = c.head_dim;
-  m->kv_layer_elems = (size_t)B * c.kv_heads * c.max_positions * d;
+  // positions rounded up to 16: the decode-layers kernel keeps V transposed
+  // with rows of that many positions
+  m->kv_layer_elems = (size_t)B * c.kv_heads * ((c.max_positions + 15) / 16 * 16) * d;
   const int max_splits = attention_splits(1, c.kv_heads, c.max_positions);
 
   auto cleanup = [&](int status) {
@@ -537,7 +482,6 @@ SH_API int sh_llm_create(sh_ctx *ctx, const sh_llm_config *config, sh_llm **out)
       (void)sh_unregister_external(ctx, p);
       (void)hipFree(p);
     }
-    uc_release(m);
     delete m;
     return status;
   };
@@ -620,7 +564,6 @@ SH_API int sh_llm_destroy(sh_llm *m) {
     (void)sh_unregister_external(m->ctx, p);
     (void)hipFree(p);
   }
-  uc_release(m);
   delete m;
   return SH_OK;
 }
