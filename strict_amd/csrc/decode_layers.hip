@@ -262,19 +262,45 @@ __device__ __forceinline__ void mfma_weights(const u32x4 (&w)[kL][kNT], const _F
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int arow = lane & 15, acol = 8 * (lane >> 4);
   const int row = arow < B ? arow : 0;  // rows past B read row 0 and are never stored
+  // independent accumulator chains (MFMA k-step s on chain s % kCh), so
+  // consecutive MFMAs do not wait for each other's results
+  constexpr int kCh = kNT == 1 ? 4 : 2;
+  f32x4 part[kCh][kNT];
 #pragma unroll
-  for (int j = 0; j < kNT; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < kCh; c++)
 #pragma unroll
-  for (int u = 0; u < kL; u++) {
-    const int kbase = (wave * kL + u) * 64;
+    for (int j = 0; j < kNT; j++) part[c][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // activation fragments are read kG4 k-steps at a time, all before their
+  // MFMAs, so the LDS latency is paid once per group rather than per step
+  constexpr int kG4 = kL < 4 ? kL : 4;
+  static_assert(kL % kG4 == 0, "k-step groups");
+  const _Float16 *xrow = xs + row * stride + wave * kL * 64 + acol;
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-      const f16x8 af = *reinterpret_cast<const f16x8 *>(xs + row * stride + kbase + 32 * h + acol);
+  for (int u0 = 0; u0 < kL; u0 += kG4) {
+    f16x8 af[kG4][2];
 #pragma unroll
-      for (int j = 0; j < kNT; j++)
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            af, e4m3x8_to_f16(w[u][j][2 * h], w[u][j][2 * h + 1]), acc[j], 0, 0, 0);
+    for (int v = 0; v < kG4; v++)
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+        af[v][h] = *reinterpret_cast<const f16x8 *>(xrow + (u0 + v) * 64 + 32 * h);
+#pragma unroll
+    for (int v = 0; v < kG4; v++) {
+      const int u = u0 + v;
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int j = 0; j < kNT; j++)
+          part[(2 * u + h) % kCh][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              af[v][h], e4m3x8_to_f16(w[u][j][2 * h], w[u][j][2 * h + 1]), part[(2 * u + h) % kCh][j],
+              0, 0, 0);
     }
+  }
+#pragma unroll
+  for (int j = 0; j < kNT; j++) {
+    f32x4 sum = part[0][j];
+#pragma unroll
+    for (int c = 1; c < kCh; c++) sum += part[c][j];
+    acc[j] = sum;
   }
 }
 
@@ -697,6 +723,10 @@ __device__ bool attn_item(const LayersArgs &a, const LayerG &P, int l, int item,
   if (s >= active || cap <= 0 || L > a.max_pos) return true;  // uniform
   const int h0 = kvh * kG;
   const unsigned tag = tag_of(ep, l);
+  // norm gains and this step's RoPE factors, requested before the wait
+  const int iq = t % kD, half = kD / 2, fi = iq % half;
+  const float qn = P.q_norm[iq], kn = P.k_norm[iq];
+  const float cs = gbl(a.rope)[(size_t)b * kD + fi], sn = gbl(a.rope)[(size_t)b * kD + half + fi];
   {
     // the row's q of heads h0.., new k and new v: one pair of cells per thread
     const size_t qrow = (size_t)b * a.qkv_n;
@@ -719,14 +749,12 @@ __device__ bool attn_item(const LayersArgs &a, const LayerG &P, int l, int item,
   const int p1 = min(L, p0 + chunk), np = p1 - p0, pos = L - 1;
   const bool holds_new = p1 == L;  // this split holds the new token (S.knew / S.vnew)
   {
-    const int gq = t / kD, iq = t % kD, half = kD / 2, fi = iq % half;
+    const int gq = t / kD;
     const bool q_thread = t < kG * kD;
     const bool kv_thread = holds_new && t < kD;
     float qv = S.raw[min(t, kG * kD - 1)];
     float knv = S.raw[kG * kD + iq];
     const float vv = S.raw[(kG + 1) * kD + iq];
-    const float qn = P.q_norm[iq], kn = P.k_norm[iq];
-    const float cs = gbl(a.rope)[(size_t)b * kD + fi], sn = gbl(a.rope)[(size_t)b * kD + half + fi];
     if (!q_thread) qv = 0.0f;
     if (!kv_thread) knv = 0.0f;
     // RMSNorm over each head (kD / 64 waves per head), then RoPE
@@ -793,7 +821,11 @@ __device__ bool attn_item(const LayersArgs &a, const LayerG &P, int l, int item,
   }
   const int nblk = (np + kBlk - 1) / kBlk;
 
-  // scores: lanes 0..15 of a tile's result hold heads 0..3 of its 16 positions
+  // scores: lanes 0..15 of a tile's result hold heads 0..3 of its 16
+  // positions; each lane keeps the max of the scores it stores
+  float M[kG], lsum[kG];
+#pragma unroll
+  for (int g = 0; g < kG; g++) M[g] = -INFINITY;
   for (int bb = 0; bb < nblk; bb++) {
     const int pb = p0 + bb * kBlk;
     if (bb > 0) attn_load_k(a, kb, pb, kv);
@@ -811,28 +843,24 @@ __device__ bool attn_item(const LayersArgs &a, const LayerG &P, int l, int item,
       const int pi = bb * kBlk + 16 * tile + lane;
       if (lane < 16 && pi < np) {
 #pragma unroll
-        for (int g = 0; g < kG; g++) S.scores[g][pi] = acc[g];
+        for (int g = 0; g < kG; g++) {
+          S.scores[g][pi] = acc[g];
+          M[g] = fmaxf(M[g], acc[g]);
+        }
       }
     }
+  }
+#pragma unroll
+  for (int g = 0; g < kG; g++) {
+    M[g] = wave_max_rows(M[g]);
+    if (lane == 0) S.wmax[wave][g] = M[g];
   }
   lds_barrier();
   SH_MARK(misc, l, 10);
 
   // softmax statistics per head over the np scores; P = exp(s - M) in fp16,
   // zero up to whole blocks, and l = the sum of those fp16 values
-  float M[kG], lsum[kG];
   {
-#pragma unroll
-    for (int g = 0; g < kG; g++) M[g] = -INFINITY;
-    for (int i = t; i < np; i += kT)
-#pragma unroll
-      for (int g = 0; g < kG; g++) M[g] = fmaxf(M[g], S.scores[g][i]);
-#pragma unroll
-    for (int g = 0; g < kG; g++) {
-      M[g] = wave_max_rows(M[g]);
-      if (lane == 0) S.wmax[wave][g] = M[g];
-    }
-    lds_barrier();
 #pragma unroll
     for (int g = 0; g < kG; g++) {
       M[g] = fmaxf(fmaxf(S.wmax[0][g], S.wmax[1][g]), fmaxf(S.wmax[2][g], S.wmax[3][g]));
