@@ -1,7 +1,11 @@
-"""Summaries of rocprofv3 CSV output for the libstrict_hip kernels.
+"""Summaries of rocprofv3 output for the libstrict_hip kernels.
 
-    python -m strict_amd.profile_summary trace <run_kernel_trace.csv> [--last N]
-    python -m strict_amd.profile_summary counters <run_counter_collection.csv> [--last N]
+    python -m strict_amd.profile_summary trace <run_kernel_trace.csv | run_results.db> [--last N]
+    python -m strict_amd.profile_summary counters <run_counter_collection.csv | run_results.db> [--last N]
+
+Either rocprofv3's CSV files or its default rocpd SQLite database
+(``run_results.db``) are read; the database survives a profiler that
+crashes while writing its CSV files at exit.
 
 ``trace``: per-kernel dispatch count, average and total duration of the last N
 dispatches (all by default), plus their span from first start to last end;
@@ -22,8 +26,56 @@ def _rows(path):
         return list(csv.DictReader(f))
 
 
+def _demangle(names: dict) -> dict:
+    """Demangled kernel names through c++filt when it is installed."""
+    import shutil
+    import subprocess
+
+    if not names or not shutil.which("c++filt"):
+        return names
+    keys = list(names)
+    res = subprocess.run(["c++filt"], input="\n".join(names[k] for k in keys), text=True,
+                         capture_output=True)
+    out = res.stdout.splitlines()
+    return dict(zip(keys, out)) if res.returncode == 0 and len(out) == len(keys) else names
+
+
+def _db_dispatches(path):
+    """Kernel dispatches of a rocpd database as CSV-like rows."""
+    import sqlite3
+
+    con = sqlite3.connect(path)
+    names = _demangle({k: v.removesuffix(".kd") for k, v in
+                       con.execute("select id, kernel_name from rocpd_info_kernel_symbol")})
+    rows = []
+    for kid, ev, start, end, did in con.execute(
+            "select kernel_id, event_id, start, end, dispatch_id from rocpd_kernel_dispatch"):
+        rows.append({"Kernel_Name": names.get(kid, str(kid)),
+                     "Start_Timestamp": start, "End_Timestamp": end, "Dispatch_Id": did,
+                     "_event": ev})
+    return con, rows
+
+
+def _db_counter_rows(path):
+    """(dispatch row, counter name, value summed over instances) of a rocpd database."""
+    con, disp = _db_dispatches(path)
+    by_event = {r["_event"]: r for r in disp}
+    pmc = dict(con.execute("select id, name from rocpd_info_pmc"))
+    sums = collections.defaultdict(float)
+    for ev, pid, val in con.execute("select event_id, pmc_id, value from rocpd_pmc_event"):
+        sums[(ev, pmc.get(pid, str(pid)))] += float(val)
+    out = []
+    for (ev, name), val in sums.items():
+        if ev in by_event:
+            r = dict(by_event[ev])
+            r["Counter_Name"] = name
+            r["Counter_Value"] = val
+            out.append(r)
+    return out
+
+
 def trace(path: str, last: int | None) -> str:
-    rows = _rows(path)
+    rows = _db_dispatches(path)[1] if path.endswith(".db") else _rows(path)
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
     if last:
         rows = rows[-last:]
@@ -40,7 +92,7 @@ def trace(path: str, last: int | None) -> str:
 
 
 def counters(path: str, last: int | None) -> str:
-    rows = _rows(path)
+    rows = _db_counter_rows(path) if path.endswith(".db") else _rows(path)
     key = "Dispatch_Id" if "Dispatch_Id" in rows[0] else "Correlation_Id"
     rows.sort(key=lambda r: int(r[key]))
     if last:
