@@ -7,9 +7,18 @@
 //  - one 256-thread workgroup per 256 x 256 tile of C; its 4 waves own
 //    128 x 128 quadrants, each a 4 x 4 grid of v_mfma_f32_32x32x16_bf16
 //    accumulators (256 fp32 per lane, held in AGPRs at one wave per SIMD);
-//  - K advances in 64-wide slabs staged in LDS, double buffered (2 x 64 KiB):
-//    the next slab's global loads are issued before the MFMAs of the current
-//    one and written to the other buffer after them, one barrier per slab;
+//  - K advances in 64-wide slabs staged in LDS, double buffered (2 x 64 KiB),
+//    software-pipelined: within a slab the fragments of k-step s + 1 are read
+//    while the MFMAs of step s run; the next slab goes out to the other buffer
+//    during steps 2 (A rows) and 3 (B columns), and each half's global loads
+//    for the slab after that are issued as soon as its staging registers are
+//    written out, so they have four k-steps to arrive; one barrier per slab,
+//    before the last four MFMAs, whose shadow covers the next slab's first
+//    fragment reads; scheduling barriers fix the instruction order (one
+//    MFMA, then the memory operations that go with it);
+//  - operands are read with buffer loads: one 32-bit lane offset per operand,
+//    the row and slab steps in the scalar offset (the tile's A rows and all of
+//    B's rows must span < 2 GiB);
 //  - A rows and B columns are stored K-contiguous in LDS (128 B per row), the
 //    16-byte chunk index XOR-swizzled by (row / 2) % 8 so that the 16-lane
 //    phases of ds_read_b128 / ds_write_b128 touch 16 distinct bank groups;
@@ -52,13 +61,10 @@ void gemm_bf16_mfma_kernel(const uint16_t *__restrict__ A, const uint16_t *__res
                            int tiles_m, int tiles_n, int grouped) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
-  // ---- tile of this workgroup ----
   const int ntiles = tiles_m * tiles_n;
   int tile = blockIdx.x;
   int tm, tn;
   if (grouped) {
-    // workgroup b runs on XCD b % 8; give XCD x the tiles x*T/8 .. (x+1)*T/8-1,
-    // laid out as 4 x 8 tile blocks
     tile = (blockIdx.x & 7) * (ntiles >> 3) + (blockIdx.x >> 3);
     const int g = tile >> 5, li = tile & 31;
     const int groups_n = tiles_n >> 3;
@@ -72,47 +78,61 @@ void gemm_bf16_mfma_kernel(const uint16_t *__restrict__ A, const uint16_t *__res
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // ---- global load roles ----
-  // A: rows t/8 + 32i (i < 8), 16-byte chunk t%8 of the 64-wide slab
+  // A: rows t/8 + 32i (i < 8), 16-byte chunk t%8 of the 64-wide slab;
+  // B: an 8 x 8 block, k rows 8*(t%8) .. +7, n columns 8*(t/8) .. +7
   const int a_row = t >> 3, a_chunk = t & 7;
-  const uint16_t *a_src = A + (size_t)(tm * kBM + a_row) * lda + a_chunk * 8;
-  // B: 8 x 8 block, k rows 8*(t%8) .. +7, n columns 8*(t/8) .. +7
   const int b_kc = t & 7, b_nc = t >> 3;
-  const uint16_t *b_src = B + (size_t)(8 * b_kc) * ldb + tn * kBN + 8 * b_nc;
 
+  const __amdgpu_buffer_rsrc_t a_rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(A + (size_t)tm * kBM * lda), (short)0, (255 * lda + K) * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t b_rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(B + tn * kBN), (short)0, ((K - 1) * ldb + kBN) * 2, 0x00020000);
+  const int a_voff = (a_row * lda + a_chunk * 8) * 2, b_voff = (8 * b_kc * ldb + 8 * b_nc) * 2;
   u32x4 ra[8], rb[8];
-  auto load_slab = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-      ra[i] = *reinterpret_cast<const u32x4 *>(a_src + (size_t)(32 * i) * lda + kt * kBK);
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-      rb[i] = *reinterpret_cast<const u32x4 *>(b_src + (size_t)(kt * kBK + i) * ldb);
+  auto load_a = [&](int kt, int i) {
+    ra[i] = __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_voff, (32 * i * lda + kt * kBK) * 2, 0);
   };
-  auto store_slab = [&](int buf) {
-    uint8_t *la = lds + buf * 2 * kLdsTile;
-    uint8_t *lb = la + kLdsTile;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const int r = a_row + 32 * i;
-      *reinterpret_cast<u32x4 *>(la + r * kLdsRow + swz(r, a_chunk) * 16) = ra[i];
-    }
-    // transpose the 8x8 bf16 block: column j of rb -> 8 k values of n = 8*b_nc + j.
-    // Odd column groups write their rows in the opposite parity order, so the
-    // two 8-lane halves of each 16-lane store phase hit different bank groups.
+  auto load_b = [&](int kt, int i) {
+    rb[i] = __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff, (kt * kBK + i) * ldb * 2, 0);
+  };
+  auto store_a = [&](uint8_t *buf, int i) {
+    const int r = a_row + 32 * i;
+    *reinterpret_cast<u32x4 *>(buf + r * kLdsRow + swz(r, a_chunk) * 16) = ra[i];
+  };
+  // B's 8 x 8 block transposed: every output column needs all eight staged
+  // rows, so the whole block is permuted before any of its registers is
+  // reloaded
+  u32x4 bt[8];
+  auto transpose_b = [&]() {
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       const int jj = j ^ (b_nc & 1);
       const uint32_t sel = (jj & 1) ? 0x07060302u : 0x05040100u;
-      u32x4 o;
-      o.x = __builtin_amdgcn_perm(rb[1][jj >> 1], rb[0][jj >> 1], sel);
-      o.y = __builtin_amdgcn_perm(rb[3][jj >> 1], rb[2][jj >> 1], sel);
-      o.z = __builtin_amdgcn_perm(rb[5][jj >> 1], rb[4][jj >> 1], sel);
-      o.w = __builtin_amdgcn_perm(rb[7][jj >> 1], rb[6][jj >> 1], sel);
-      const int n = 8 * b_nc + jj;
-      *reinterpret_cast<u32x4 *>(lb + n * kLdsRow + swz(n, b_kc) * 16) = o;
+      bt[j].x = __builtin_amdgcn_perm(rb[1][jj >> 1], rb[0][jj >> 1], sel);
+      bt[j].y = __builtin_amdgcn_perm(rb[3][jj >> 1], rb[2][jj >> 1], sel);
+      bt[j].z = __builtin_amdgcn_perm(rb[5][jj >> 1], rb[4][jj >> 1], sel);
+      bt[j].w = __builtin_amdgcn_perm(rb[7][jj >> 1], rb[6][jj >> 1], sel);
     }
   };
+  auto store_b = [&](uint8_t *buf, int j) {
+    const int n = 8 * b_nc + (j ^ (b_nc & 1));
+    *reinterpret_cast<u32x4 *>(buf + kLdsTile + n * kLdsRow + swz(n, b_kc) * 16) = bt[j];
+  };
+
+  // Fragment q of k-step s: q < 4 is A rows wm*128 + 32 q + (lane % 32), q >= 4
+  // B columns wn*128 + 32 (q - 4) + (lane % 32); 8 k values each, k chunk
+  // 2 s + lane / 32. The row swizzle (row / 2) % 8 only depends on lane % 32.
+  const int frag_row = lane & 31, frag_half = lane >> 5, fsw = (frag_row >> 1) & 7;
+  const int a_off = (wm * 128 + frag_row) * kLdsRow, b_off = kLdsTile + (wn * 128 + frag_row) * kLdsRow;
+  bf16x8 f[2][8];
+  auto read_frag = [&](bf16x8 (&fr)[8], const uint8_t *buf, int s, int q) {
+    const int chunk = ((2 * s + frag_half) ^ fsw) * 16;
+    const int off = q < 4 ? a_off + q * 32 * kLdsRow : b_off + (q - 4) * 32 * kLdsRow;
+    fr[q] = *reinterpret_cast<const bf16x8 *>(buf + off + chunk);
+  };
+  // fragments are read A0, B0, B1, B2, B3, A1, A2, A3: the order the MFMAs
+  // (row-major over the 4 x 4 accumulators) first need them
+  constexpr int kReadOrder[8] = {0, 4, 5, 6, 7, 1, 2, 3};
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -121,43 +141,84 @@ void gemm_bf16_mfma_kernel(const uint16_t *__restrict__ A, const uint16_t *__res
     for (int j = 0; j < 4; j++)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+  auto mfma = [&](const bf16x8 (&fr)[8], int k) {
+    const int i = k >> 2, j = k & 3;
+    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr[4 + j], fr[i], acc[i][j], 0, 0, 0);
+  };
 
   const int ktiles = K / kBK;
-  load_slab(0);
-  store_slab(0);
+  // prologue: slab 0 into buffer 0, slab 1 requested, step 0 fragments read
+#pragma unroll
+  for (int i = 0; i < 8; i++) load_a(0, i);
+#pragma unroll
+  for (int i = 0; i < 8; i++) load_b(0, i);
+#pragma unroll
+  for (int i = 0; i < 8; i++) store_a(lds, i);
+  transpose_b();
+#pragma unroll
+  for (int j = 0; j < 8; j++) store_b(lds, j);
+  const int k1 = min(1, ktiles - 1);
+#pragma unroll
+  for (int i = 0; i < 8; i++) load_a(k1, i);
+#pragma unroll
+  for (int i = 0; i < 8; i++) load_b(k1, i);
   __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 8; q++) read_frag(f[0], lds, 0, kReadOrder[q]);
 
-  const int frag_row = lane & 31, frag_half = lane >> 5;
   for (int kt = 0; kt < ktiles; kt++) {
-    const int buf = kt & 1;
-    if (kt + 1 < ktiles) load_slab(kt + 1);
-    const uint8_t *la = lds + buf * 2 * kLdsTile;
-    const uint8_t *lb = la + kLdsTile;
+    const uint8_t *cur = lds + (kt & 1) * 2 * kLdsTile;
+    uint8_t *nxt = lds + ((kt & 1) ^ 1) * 2 * kLdsTile;
+    // slab after the next one (re-reads the last slab at the end; those
+    // values are never used)
+    const int k2 = min(kt + 2, ktiles - 1);
+    // steps 0 and 1: MFMAs of step s, reads of step s + 1
 #pragma unroll
-    for (int s = 0; s < kBK / 16; s++) {
-      const int chunk = 2 * s + frag_half;
-      bf16x8 fa[4], fb[4];
+    for (int s = 0; s < 2; s++) {
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int m = wm * 128 + i * 32 + frag_row;
-        fa[i] = *reinterpret_cast<const bf16x8 *>(la + m * kLdsRow + swz(m, chunk) * 16);
+      for (int k = 0; k < 16; k++) {
+        mfma(f[s & 1], k);
+        if (k < 8) read_frag(f[(s + 1) & 1], cur, s + 1, kReadOrder[k]);
+        __builtin_amdgcn_sched_barrier(0);
       }
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int n = wn * 128 + j * 32 + frag_row;
-        fb[j] = *reinterpret_cast<const bf16x8 *>(lb + n * kLdsRow + swz(n, chunk) * 16);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < ktiles) store_slab(buf ^ 1);
-    __syncthreads();
+    // step 2: reads of step 3, then the A half of the next slab out to LDS
+    // and the A half of the slab after it requested
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      mfma(f[0], k);
+      if (k < 8) {
+        read_frag(f[1], cur, 3, kReadOrder[k]);
+      } else {
+        store_a(nxt, k - 8);
+        load_a(k2, k - 8);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // step 3: the B half likewise, then the barrier, then the next slab's
+    // step 0 fragments under the last four MFMAs
+    transpose_b();
+#pragma unroll
+    for (int k = 0; k < 12; k++) {
+      mfma(f[1], k);
+      if (k < 8) {
+        store_b(nxt, k);
+        load_b(k2, k);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes done
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 12; k < 16; k++) {
+      mfma(f[1], k);
+      read_frag(f[0], nxt, 0, kReadOrder[2 * (k - 12)]);
+      read_frag(f[0], nxt, 0, kReadOrder[2 * (k - 12) + 1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 
-  // ---- epilogue: lane holds C row m, columns n0 + 8q + 4*half + 0..3 ----
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int m = tm * kBM + wm * 128 + i * 32 + frag_row;
@@ -238,7 +299,8 @@ bool gemm_bf16_uses_mfma(int M, int N, int K, int lda, int ldb, int ldc, const v
                          const void *B, const void *C) {
   return M % kBM == 0 && N % kBN == 0 && K % kBK == 0 && K > 0 && lda % 8 == 0 &&
          ldb % 8 == 0 && ldc % 4 == 0 && aligned16(A) && aligned16(B) &&
-         (reinterpret_cast<uintptr_t>(C) & 7) == 0;
+         (reinterpret_cast<uintptr_t>(C) & 7) == 0 && (int64_t)kBM * lda * 2 < (1ll << 31) &&
+         (int64_t)K * ldb * 2 < (1ll << 31);
 }
 
 hipError_t launch_gemm_bf16(hipStream_t s, const uint16_t *A, const uint16_t *B, uint16_t *C,

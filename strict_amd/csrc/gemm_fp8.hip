@@ -13,7 +13,14 @@
 //    accumulators (E8M0 block scales fixed at 1: the fp32 row / column scales
 //    are applied once in the epilogue);
 //  - K advances in 128-byte slabs staged in LDS, double buffered (2 x 64 KiB),
-//    next slab loaded during the current one's MFMAs, one barrier per slab;
+//    software-pipelined like the bf16 kernel: the second 64-deep k-step's
+//    fragments are read under the first step's MFMAs; the next slab goes out
+//    to the other buffer during the slab (A rows in step 0, Bt rows in step 1)
+//    and each half's loads for the slab after it are issued as soon as its
+//    staging registers are free; one barrier per slab, before the last four
+//    MFMAs, whose shadow covers the next slab's first fragment reads;
+//    scheduling barriers fix the order; buffer loads with 32-bit lane offsets
+//    (the tile's rows of A and of Bt must each span < 2 GiB);
 //  - both operands are K-contiguous, so A rows and Bt rows are staged alike
 //    (no transpose), the 16-byte chunk index XOR-swizzled by (row / 2) % 8 so
 //    16-lane LDS phases hit 16 distinct bank groups;
@@ -75,30 +82,43 @@ void gemm_fp8_mfma_kernel(const uint8_t *__restrict__ A, const float *__restrict
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // global load roles: rows t/8 + 32i (i < 8), 16-byte chunk t%8 of the slab
+  // rows t/8 + 32i (i < 8), 16-byte chunk t%8 of the slab
   const int g_row = t >> 3, g_chunk = t & 7;
-  const uint8_t *a_src = A + (size_t)(tm * kBM + g_row) * lda + g_chunk * 16;
-  const uint8_t *b_src = Bt + (size_t)(tn * kBN + g_row) * ldb + g_chunk * 16;
-
+  const __amdgpu_buffer_rsrc_t a_rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(A + (size_t)tm * kBM * lda), (short)0, 255 * lda + K, 0x00020000);
+  const __amdgpu_buffer_rsrc_t b_rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(Bt + (size_t)tn * kBN * ldb), (short)0, 255 * ldb + K, 0x00020000);
+  const int a_voff = g_row * lda + g_chunk * 16, b_voff = g_row * ldb + g_chunk * 16;
   u32x4 ra[8], rb[8];
-  auto load_slab = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-      ra[i] = *reinterpret_cast<const u32x4 *>(a_src + (size_t)(32 * i) * lda + kt * kBK);
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-      rb[i] = *reinterpret_cast<const u32x4 *>(b_src + (size_t)(32 * i) * ldb + kt * kBK);
+  auto load_a = [&](int kt, int i) {
+    ra[i] = __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_voff, 32 * i * lda + kt * kBK, 0);
   };
-  auto store_slab = [&](int buf) {
-    uint8_t *la = lds + buf * 2 * kLdsTile;
-    uint8_t *lb = la + kLdsTile;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const int r = g_row + 32 * i;
-      *reinterpret_cast<u32x4 *>(la + r * kLdsRow + swz(r, g_chunk) * 16) = ra[i];
-      *reinterpret_cast<u32x4 *>(lb + r * kLdsRow + swz(r, g_chunk) * 16) = rb[i];
-    }
+  auto load_b = [&](int kt, int i) {
+    rb[i] = __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff, 32 * i * ldb + kt * kBK, 0);
   };
+  auto store_a = [&](uint8_t *buf, int i) {
+    const int r = g_row + 32 * i;
+    *reinterpret_cast<u32x4 *>(buf + r * kLdsRow + swz(r, g_chunk) * 16) = ra[i];
+  };
+  auto store_b = [&](uint8_t *buf, int i) {
+    const int r = g_row + 32 * i;
+    *reinterpret_cast<u32x4 *>(buf + kLdsTile + r * kLdsRow + swz(r, g_chunk) * 16) = rb[i];
+  };
+
+  // Fragment q of k-step s (q < 4: A rows wm*128 + 32 q + lane % 32; q >= 4:
+  // Bt rows wn*128 + 32 (q - 4) + lane % 32): 32 bytes, chunks c0 and c0 + 1
+  // with c0 = 4 s + 2 (lane / 32), read as two halves h.
+  const int frag_row = lane & 31, frag_half = lane >> 5, fsw = (frag_row >> 1) & 7;
+  const int a_off = (wm * 128 + frag_row) * kLdsRow, b_off = kLdsTile + (wn * 128 + frag_row) * kLdsRow;
+  u32x4 f[2][8][2];
+  auto read_half = [&](u32x4 (&fr)[8][2], const uint8_t *buf, int s, int q, int h) {
+    const int chunk = ((4 * s + 2 * frag_half + h) ^ fsw) * 16;
+    const int off = q < 4 ? a_off + q * 32 * kLdsRow : b_off + (q - 4) * 32 * kLdsRow;
+    fr[q][h] = *reinterpret_cast<const u32x4 *>(buf + off + chunk);
+  };
+  // halves in the order the MFMAs (row-major over the 4 x 4 accumulators)
+  // first need them: A0, B0, B1, B2, B3, A1, A2, A3
+  constexpr int kReadOrder[8] = {0, 4, 5, 6, 7, 1, 2, 3};
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -107,48 +127,77 @@ void gemm_fp8_mfma_kernel(const uint8_t *__restrict__ A, const float *__restrict
     for (int j = 0; j < 4; j++)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+  auto mfma = [&](const u32x4 (&fr)[8][2], int k) {
+    const int i = k >> 2, j = k & 3;
+    const u32x4 al = fr[i][0], ah = fr[i][1], bl = fr[4 + j][0], bh = fr[4 + j][1];
+    const i32x8 fa = i32x8{(int)al.x, (int)al.y, (int)al.z, (int)al.w, (int)ah.x, (int)ah.y, (int)ah.z, (int)ah.w};
+    const i32x8 fb = i32x8{(int)bl.x, (int)bl.y, (int)bl.z, (int)bl.w, (int)bh.x, (int)bh.y, (int)bh.z, (int)bh.w};
+    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb, fa, acc[i][j], 0, 0, 0, kScaleOne, 0,
+                                                                 kScaleOne);
+  };
 
   const int ktiles = K / kBK;
-  load_slab(0);
-  store_slab(0);
+#pragma unroll
+  for (int i = 0; i < 8; i++) load_a(0, i);
+#pragma unroll
+  for (int i = 0; i < 8; i++) load_b(0, i);
+#pragma unroll
+  for (int i = 0; i < 8; i++) store_a(lds, i);
+#pragma unroll
+  for (int i = 0; i < 8; i++) store_b(lds, i);
+  const int k1 = min(1, ktiles - 1);
+#pragma unroll
+  for (int i = 0; i < 8; i++) load_a(k1, i);
+#pragma unroll
+  for (int i = 0; i < 8; i++) load_b(k1, i);
   __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 16; q++) read_half(f[0], lds, 0, kReadOrder[q >> 1], q & 1);
 
-  const int frag_row = lane & 31, frag_half = lane >> 5;
   for (int kt = 0; kt < ktiles; kt++) {
-    const int buf = kt & 1;
-    if (kt + 1 < ktiles) load_slab(kt + 1);
-    const uint8_t *la = lds + buf * 2 * kLdsTile;
-    const uint8_t *lb = la + kLdsTile;
+    const uint8_t *cur = lds + (kt & 1) * 2 * kLdsTile;
+    uint8_t *nxt = lds + ((kt & 1) ^ 1) * 2 * kLdsTile;
+    const int k2 = min(kt + 2, ktiles - 1);  // re-reads the last slab at the end, unused
+    // step 0: MFMAs, step 1's fragments, then A rows of the next slab out
+    // and the A rows of the slab after it requested
 #pragma unroll
-    for (int s = 0; s < kBK / 64; s++) {
-      const int c0 = 4 * s + 2 * frag_half;  // the lane's two 16-byte chunks
-      i32x8 fa[4], fb[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int m = wm * 128 + i * 32 + frag_row;
-        const u32x4 lo = *reinterpret_cast<const u32x4 *>(la + m * kLdsRow + swz(m, c0) * 16);
-        const u32x4 hi = *reinterpret_cast<const u32x4 *>(la + m * kLdsRow + swz(m, c0 + 1) * 16);
-        fa[i] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    for (int k = 0; k < 16; k++) {
+      mfma(f[0], k);
+      if (k < 8) {
+        read_half(f[1], cur, 1, kReadOrder[k], 0);
+        read_half(f[1], cur, 1, kReadOrder[k], 1);
+      } else {
+        store_a(nxt, k - 8);
+        load_a(k2, k - 8);
       }
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int n = wn * 128 + j * 32 + frag_row;
-        const u32x4 lo = *reinterpret_cast<const u32x4 *>(lb + n * kLdsRow + swz(n, c0) * 16);
-        const u32x4 hi = *reinterpret_cast<const u32x4 *>(lb + n * kLdsRow + swz(n, c0 + 1) * 16);
-        fb[j] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-      }
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-              fb[j], fa[i], acc[i][j], 0, 0, 0, kScaleOne, 0, kScaleOne);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (kt + 1 < ktiles) store_slab(buf ^ 1);
-    __syncthreads();
+    // step 1: the Bt rows likewise, the barrier, then the next slab's step 0
+    // fragments under the last four MFMAs
+#pragma unroll
+    for (int k = 0; k < 12; k++) {
+      mfma(f[1], k);
+      if (k < 8) {
+        store_b(nxt, k);
+        load_b(k2, k);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes done
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 12; k < 16; k++) {
+      mfma(f[1], k);
+#pragma unroll
+      for (int h = 0; h < 4; h++) {
+        const int q = 4 * (k - 12) + h;
+        read_half(f[0], nxt, 0, kReadOrder[q >> 1], q & 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 
-  // ---- epilogue: lane holds C row m, columns n0 + 8q + 4*half + 0..3 ----
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int m = tm * kBM + wm * 128 + i * 32 + frag_row;
@@ -231,7 +280,7 @@ bool gemm_fp8_uses_mfma(int M, int N, int K, int lda, int ldb, int ldc, const vo
                         const void *Bt, const void *C, const void *sb) {
   return M % kBM == 0 && N % kBN == 0 && K % kBK == 0 && K > 0 && lda % 16 == 0 &&
          ldb % 16 == 0 && ldc % 4 == 0 && aligned(A, 16) && aligned(Bt, 16) && aligned(C, 8) &&
-         aligned(sb, 16);
+         aligned(sb, 16) && (int64_t)kBM * lda < (1ll << 31) && (int64_t)kBN * ldb < (1ll << 31);
 }
 
 hipError_t launch_gemm_fp8(hipStream_t s, const uint8_t *A, const float *sa, const uint8_t *Bt,
