@@ -64,6 +64,19 @@ __device__ __forceinline__ SH_GLOBAL T *gbl(T *p) {
   return (SH_GLOBAL T *)p;
 }
 
+// Tables that the host or an earlier kernel of the step writes and this
+// kernel only reads (the layer pointer table, the rows' positions, the
+// step's epoch) are read through the constant address space: uniform reads
+// of it become scalar loads, which complete on their own counter. Read as
+// global memory they were vector loads, queued behind every weight and K / V
+// request outstanding, and each layer's first use of a layer pointer waited
+// for all of them.
+#define SH_CONST __attribute__((address_space(4)))
+template <class T>
+__device__ __forceinline__ const SH_CONST T *cnst(const T *p) {
+  return (const SH_CONST T *)p;
+}
+
 // One layer's pointers in the global address space.
 struct LayerG {
   const SH_GLOBAL uint8_t *wqkv, *wo, *wup, *wdown;
@@ -73,6 +86,14 @@ struct LayerG {
 };
 
 __device__ __forceinline__ LayerG layer_g(const LayerPtrs &p) {
+  return LayerG{gbl(p.wqkv),   gbl(p.wo),     gbl(p.wup),    gbl(p.wdown), gbl(p.sqkv),
+                gbl(p.so),     gbl(p.sup),    gbl(p.sdown),  gbl(p.norm1), gbl(p.norm2),
+                gbl(p.q_norm), gbl(p.k_norm), gbl(p.kcache), gbl(p.vcache)};
+}
+
+// Layer l's pointers, read from the table with scalar loads.
+__device__ __forceinline__ LayerG layer_g(const LayersArgs &a, int l) {
+  const SH_CONST LayerPtrs &p = cnst(a.layers)[l];
   return LayerG{gbl(p.wqkv),   gbl(p.wo),     gbl(p.wup),    gbl(p.wdown), gbl(p.sqkv),
                 gbl(p.so),     gbl(p.sup),    gbl(p.sdown),  gbl(p.norm1), gbl(p.norm2),
                 gbl(p.q_norm), gbl(p.k_norm), gbl(p.kcache), gbl(p.vcache)};
@@ -457,8 +478,11 @@ struct Lds {
 };
 
 // Requests x[b][col] of the four batch rows b = 4 (lane / 16) + r this
-// lane's accumulator holds (lanes of wave 0): plain values of the first
-// layer's input, or cells (checked by finish_residual).
+// lane's accumulator holds (used in wave 0): the cells (checked by
+// finish_residual), and for the first layer's O item the plain input xp.
+// Every thread loads its cells, without a branch: a load under a branch
+// made the compiler wait for all outstanding requests (the item's weights)
+// before the poll that follows.
 __device__ __forceinline__ void request_residual(const LayersArgs &a, const uint64_t *xc,
                                                  const float *xp, int col, float (&rv)[4],
                                                  uint64_t (&rc)[4]) {
@@ -466,10 +490,15 @@ __device__ __forceinline__ void request_residual(const LayersArgs &a, const uint
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     const int b = min(4 * (lane >> 4) + r, a.B - 1);
+    rc[r] = cld(xc, (size_t)b * a.H + col);
     rv[r] = 0.0f;
-    rc[r] = 0;
-    if (xp) rv[r] = gbl(xp)[(size_t)b * a.H + col];
-    else if (threadIdx.x < 64) rc[r] = cld(xc, (size_t)b * a.H + col);
+  }
+  if (xp) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int b = min(4 * (lane >> 4) + r, a.B - 1);
+      rv[r] = gbl(xp)[(size_t)b * a.H + col];
+    }
   }
 }
 
@@ -718,7 +747,7 @@ __device__ bool attn_item(const LayersArgs &a, const LayerG &P, int l, int item,
   SH_GLOBAL uint16_t *kb = P.kcache + kv_row * a.max_pos * kD;
   SH_GLOBAL uint16_t *vtb = P.vcache + kv_row * kD * a.vt_stride;
 
-  const int L = gbl(a.pos)[b] + 1;  // context including the new token
+  const int L = cnst(a.pos)[b] + 1;  // context including the new token
   const int active = (L + chunk - 1) / chunk;
   if (s >= active || cap <= 0 || L > a.max_pos) return true;  // uniform
   const int h0 = kvh * kG;
@@ -942,7 +971,7 @@ __device__ bool merge_item(const LayersArgs &a, int l, int item, unsigned ep, ui
   MergeLds &S = *reinterpret_cast<MergeLds *>(smem);
   const int h = item % a.heads, b = item / a.heads;
   const int t = threadIdx.x, q = t & 63, sg = t >> 6;
-  const int L = gbl(a.pos)[b] + 1;
+  const int L = cnst(a.pos)[b] + 1;
   const int active = min((L + a.chunk - 1) / a.chunk, a.splits);
   const size_t base = ((size_t)b * a.heads + h) * a.splits * kPStride;
   const unsigned tag = tag_of(ep, l);
@@ -1022,7 +1051,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
     (&misc->tr[0][0][0])[i] = 0;
 #endif
   lds_barrier();
-  const unsigned ep = *a.epoch;
+  const unsigned ep = *cnst(a.epoch);
   const int G = gridDim.x, w = blockIdx.x;
   const int nA = a.qkv_n / 16, nB = B * a.kv_heads * a.splits, nM = B * a.heads;
   const int nC = H / 16, nD = a.inter / 16, nE = H / 16;
@@ -1031,10 +1060,10 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
   const bool hasC = w < nC;
   AttnKV kv;
   u32x4 wa[kLA][1];  // this workgroup's first QKV item's weights
-  if (w < nA) load_weights<kLA, 1>(wa, gbl(a.layers[0].wqkv), H, w);
-  if (w < nB) attn_prefetch(a, layer_g(a.layers[0]), w, kv);
+  if (w < nA) load_weights<kLA, 1>(wa, layer_g(a, 0).wqkv, H, w);
+  if (w < nB) attn_prefetch(a, layer_g(a, 0), w, kv);
   for (int l = 0; l < a.n_layers; l++) {
-    const LayerG P = layer_g(a.layers[l]);
+    const LayerG P = layer_g(a, l);
     const bool next = l + 1 < a.n_layers;
     for (int i = w; i < nA; i += G) {
       if (i != w) load_weights<kLA, 1>(wa, P.wqkv, H, i);
@@ -1061,22 +1090,22 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
     }
     // workgroups with an O item: the next layer's K / V while the gate/up
     // items run; the others after their gate/up item, with the next QKV weights
-    if (hasC && next && w < nB) attn_prefetch(a, layer_g(a.layers[l + 1]), w, kv);
+    if (hasC && next && w < nB) attn_prefetch(a, layer_g(a, l + 1), w, kv);
     for (int i = d0; i < nD; i += G) {
       if (i == d0) SH_TRACE(misc, l, 6);
       if (!up_item<kLD, kRows>(a, P, l, i, ep, lds)) return;
       if (i == d0) { SH_TRACE(misc, l, 7); SH_TRACE_WAIT(l, 3, misc); }
     }
     if (!hasC && next) {
-      if (w < nB) attn_prefetch(a, layer_g(a.layers[l + 1]), w, kv);
-      if (w < nA) load_weights<kLA, 1>(wa, gbl(a.layers[l + 1].wqkv), H, w);
+      if (w < nB) attn_prefetch(a, layer_g(a, l + 1), w, kv);
+      if (w < nA) load_weights<kLA, 1>(wa, layer_g(a, l + 1).wqkv, H, w);
     }
     for (int i = w; i < nE; i += G) {
       if (i == w) SH_TRACE(misc, l, 8);
       if (!down_item<kLE, kRows>(a, P, l, i, ep, lds)) return;
       if (i == w) { SH_TRACE(misc, l, 9); SH_TRACE_WAIT(l, 4, misc); }
     }
-    if (hasC && next && w < nA) load_weights<kLA, 1>(wa, gbl(a.layers[l + 1].wqkv), H, w);
+    if (hasC && next && w < nA) load_weights<kLA, 1>(wa, layer_g(a, l + 1).wqkv, H, w);
   }
 #ifdef SH_DECODE_TRACE
   lds_barrier();
