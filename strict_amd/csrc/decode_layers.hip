@@ -353,7 +353,7 @@ __device__ __forceinline__ void reduce_waves(f32x4 (&acc)[kNT], float *red) {
 // the per-row sums of squares are combined across the four waves through
 // LDS. kChunks >= K / 4 / 256.
 template <int kChunks, int kRows>
-__device__ bool stage_rms(const LayersArgs &a, const uint64_t *xc, const float *xp, unsigned tag,
+__device__ __forceinline__ bool stage_rms(const LayersArgs &a, const uint64_t *xc, const float *xp, unsigned tag,
                           const SH_GLOBAL float *g, int K, _Float16 *xs, Misc *misc) {
   typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
   constexpr int kN = kRows * kChunks * 4;
@@ -436,7 +436,7 @@ __device__ bool stage_rms(const LayersArgs &a, const uint64_t *xc, const float *
 // tagged `tag`) -> xs (row stride K + 8), kRows rows per pass. kChunks >=
 // K / 4 / 256 two-cell chunks per thread and row.
 template <int kChunks, int kRows>
-__device__ bool stage_f16(const LayersArgs &a, const uint64_t *cells, unsigned tag, int K,
+__device__ __forceinline__ bool stage_f16(const LayersArgs &a, const uint64_t *cells, unsigned tag, int K,
                           _Float16 *xs, Misc *misc) {
   constexpr int kN = kRows * kChunks * 2;
   static_assert(kN <= 64, "cells per thread");
@@ -518,10 +518,18 @@ __device__ __forceinline__ bool finish_residual(const LayersArgs &a, const uint6
   return ok;
 }
 
+// Marks loaded cells as used. A load whose result no path consumes leaves
+// its destination registers pending at the join, and the compiler then
+// waits for every outstanding request (the next layer's K / V) before the
+// registers' next write.
+__device__ __forceinline__ void consume_cells(const uint64_t (&c)[4]) {
+  asm volatile("" ::"v"(c[0]), "v"(c[1]), "v"(c[2]), "v"(c[3]));
+}
+
 // A: qkv[b][16 i + c] = scale * (W_qkv RMSNorm(x)); w holds the item's
 // weights (load_weights, issued by the caller)
 template <int kL, int kRows>
-__device__ bool qkv_item(const LayersArgs &a, const LayerG &P, int l, int i, unsigned ep,
+__device__ __forceinline__ bool qkv_item(const LayersArgs &a, const LayerG &P, int l, int i, unsigned ep,
                          const Lds &s, const u32x4 (&w)[kL][1]) {
   const int lane = threadIdx.x & 63, col = lane & 15;
   const float sc = P.sqkv[i * 16 + col];
@@ -549,7 +557,7 @@ __device__ bool qkv_item(const LayersArgs &a, const LayerG &P, int l, int i, uns
 
 // C: x_mid[b][16 i + c] = x[b][.] + scale * (W_o attn)
 template <int kL, int kRows>
-__device__ bool o_item(const LayersArgs &a, const LayerG &P, int l, int i, unsigned ep,
+__device__ __forceinline__ bool o_item(const LayersArgs &a, const LayerG &P, int l, int i, unsigned ep,
                        const Lds &s) {
   const int lane = threadIdx.x & 63, col = lane & 15, K = a.heads * kD;
   u32x4 w[kL][1];
@@ -565,6 +573,7 @@ __device__ bool o_item(const LayersArgs &a, const LayerG &P, int l, int i, unsig
   reduce_waves<1>(acc, s.red);
   if (threadIdx.x < 64) {
     if (l > 0) finish_residual(a, a.x0c, i * 16 + col, tag_of(ep, l - 1), rv, rc);
+    else consume_cells(rc);  // unused at the first layer, but the loads must retire here
     const unsigned tag = tag_of(ep, l);
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -578,7 +587,7 @@ __device__ bool o_item(const LayersArgs &a, const LayerG &P, int l, int i, unsig
 // D: act[b][16 p + c] = silu(scale_g * gate) * (scale_u * up) of RMSNorm(x_mid),
 // two adjacent columns per cell
 template <int kL, int kRows>
-__device__ bool up_item(const LayersArgs &a, const LayerG &P, int l, int p, unsigned ep,
+__device__ __forceinline__ bool up_item(const LayersArgs &a, const LayerG &P, int l, int p, unsigned ep,
                         const Lds &s) {
   const int lane = threadIdx.x & 63, col = lane & 15;
   u32x4 w[kL][2];
@@ -608,7 +617,7 @@ __device__ bool up_item(const LayersArgs &a, const LayerG &P, int l, int p, unsi
 // E: x[b][16 i + c] = x_mid[b][.] + scale * (W_down act); the last layer
 // writes the plain buffer the final norm reads
 template <int kL, int kRows>
-__device__ bool down_item(const LayersArgs &a, const LayerG &P, int l, int i, unsigned ep,
+__device__ __forceinline__ bool down_item(const LayersArgs &a, const LayerG &P, int l, int i, unsigned ep,
                           const Lds &s) {
   const int lane = threadIdx.x & 63, col = lane & 15, K = a.inter;
   u32x4 w[kL][1];
@@ -733,7 +742,7 @@ __device__ __forceinline__ void attn_prefetch(const LayersArgs &a, const LayerG 
 // V sum, max, sum) of each head as cells. Splits past the context write
 // nothing.
 template <int kG>
-__device__ bool attn_item(const LayersArgs &a, const LayerG &P, int l, int item, unsigned ep,
+__device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, int l, int item, unsigned ep,
                           uint8_t *smem, Misc *misc, AttnKV &kv) {
   static_assert((kG + 2) * kD / 2 <= kT, "one pair of q / k / v cells per thread");
   static_assert(kG <= 4, "MFMA rows 0..3 of lanes 0..15 hold the heads");
@@ -964,7 +973,7 @@ __device__ bool attn_item(const LayersArgs &a, const LayerG &P, int l, int item,
 // pair t % 64 of splits t / 64, t / 64 + 4, ...; threads t < active also
 // fetch split t's (m, l).
 template <int kSP>
-__device__ bool merge_item(const LayersArgs &a, int l, int item, unsigned ep, uint8_t *smem,
+__device__ __forceinline__ bool merge_item(const LayersArgs &a, int l, int item, unsigned ep, uint8_t *smem,
                            Misc *misc) {
   static_assert(kSP % 4 == 0 && kSP <= kMaxSplits, "splits per merge");
   constexpr int kPer = kSP / 4;
@@ -1033,7 +1042,24 @@ __device__ bool merge_item(const LayersArgs &a, int l, int item, unsigned ep, ui
 
 // ---- the kernel ----------------------------------------------------------------
 
-template <int kG, int kLA, int kLC, int kLD, int kLE, int kSP, int kRows>
+// Runs f(i) for this workgroup's items i = first, first + G, .. < n. With
+// kOne the host has checked that every phase has at most G items, so there
+// is at most one: no loop, whose preheader would make the compiler wait for
+// every outstanding request (it flushes the load counter ahead of a loop
+// that uses values loaded before it), including the weights and K / V
+// requested ahead. False when an item failed.
+template <bool kOne, class F>
+__device__ __forceinline__ bool for_items(int first, int n, int G, F &&f) {
+  if constexpr (kOne) {
+    return first < n ? f(first) : true;
+  } else {
+    for (int i = first; i < n; i += G)
+      if (!f(i)) return false;
+    return true;
+  }
+}
+
+template <int kG, int kLA, int kLC, int kLD, int kLE, int kSP, int kRows, bool kOne>
 __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   Misc *misc = reinterpret_cast<Misc *>(smem + a.lds_misc);
@@ -1065,46 +1091,58 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
   for (int l = 0; l < a.n_layers; l++) {
     const LayerG P = layer_g(a, l);
     const bool next = l + 1 < a.n_layers;
-    for (int i = w; i < nA; i += G) {
-      if (i != w) load_weights<kLA, 1>(wa, P.wqkv, H, i);
-      if (i == w) SH_TRACE(misc, l, 0);
-      if (!qkv_item<kLA, kRows>(a, P, l, i, ep, lds, wa)) return;
-      if (i == w) { SH_TRACE(misc, l, 1); SH_TRACE_WAIT(l, 0, misc); }
-    }
-    for (int i = w; i < nB; i += G) {
-      if (i != w) attn_prefetch(a, P, i, kv);
-      if (i == w) SH_TRACE(misc, l, 2);
-      if (!attn_item<kG>(a, P, l, i, ep, smem, misc, kv)) return;
-      if (i == w) { SH_TRACE(misc, l, 3); SH_TRACE_WAIT(l, 1, misc); }
-    }
-    for (int j = m0; j < nM; j += G) {
-      if (!merge_item<kSP>(a, l, j, ep, smem, misc)) return;
-      if (j == m0) SH_TRACE(misc, l, 15);
-    }
+    if (!for_items<kOne>(w, nA, G, [&](int i) {
+          if (i != w) load_weights<kLA, 1>(wa, P.wqkv, H, i);
+          if (i == w) SH_TRACE(misc, l, 0);
+          if (!qkv_item<kLA, kRows>(a, P, l, i, ep, lds, wa)) return false;
+          if (i == w) { SH_TRACE(misc, l, 1); SH_TRACE_WAIT(l, 0, misc); }
+          return true;
+        }))
+      return;
+    if (!for_items<kOne>(w, nB, G, [&](int i) {
+          if (i != w) attn_prefetch(a, P, i, kv);
+          if (i == w) SH_TRACE(misc, l, 2);
+          if (!attn_item<kG>(a, P, l, i, ep, smem, misc, kv)) return false;
+          if (i == w) { SH_TRACE(misc, l, 3); SH_TRACE_WAIT(l, 1, misc); }
+          return true;
+        }))
+      return;
+    if (!for_items<kOne>(m0, nM, G, [&](int j) {
+          if (!merge_item<kSP>(a, l, j, ep, smem, misc)) return false;
+          if (j == m0) SH_TRACE(misc, l, 15);
+          return true;
+        }))
+      return;
     // O, gate/up and down items request their weights when they start: at
     // batch 1 each workgroup's previous item is then a phase or more behind
-    for (int i = w; i < nC; i += G) {
-      if (i == w) SH_TRACE(misc, l, 4);
-      if (!o_item<kLC, kRows>(a, P, l, i, ep, lds)) return;
-      if (i == w) { SH_TRACE(misc, l, 5); SH_TRACE_WAIT(l, 2, misc); }
-    }
+    if (!for_items<kOne>(w, nC, G, [&](int i) {
+          if (i == w) SH_TRACE(misc, l, 4);
+          if (!o_item<kLC, kRows>(a, P, l, i, ep, lds)) return false;
+          if (i == w) { SH_TRACE(misc, l, 5); SH_TRACE_WAIT(l, 2, misc); }
+          return true;
+        }))
+      return;
     // workgroups with an O item: the next layer's K / V while the gate/up
     // items run; the others after their gate/up item, with the next QKV weights
     if (hasC && next && w < nB) attn_prefetch(a, layer_g(a, l + 1), w, kv);
-    for (int i = d0; i < nD; i += G) {
-      if (i == d0) SH_TRACE(misc, l, 6);
-      if (!up_item<kLD, kRows>(a, P, l, i, ep, lds)) return;
-      if (i == d0) { SH_TRACE(misc, l, 7); SH_TRACE_WAIT(l, 3, misc); }
-    }
+    if (!for_items<kOne>(d0, nD, G, [&](int i) {
+          if (i == d0) SH_TRACE(misc, l, 6);
+          if (!up_item<kLD, kRows>(a, P, l, i, ep, lds)) return false;
+          if (i == d0) { SH_TRACE(misc, l, 7); SH_TRACE_WAIT(l, 3, misc); }
+          return true;
+        }))
+      return;
     if (!hasC && next) {
       if (w < nB) attn_prefetch(a, layer_g(a, l + 1), w, kv);
       if (w < nA) load_weights<kLA, 1>(wa, layer_g(a, l + 1).wqkv, H, w);
     }
-    for (int i = w; i < nE; i += G) {
-      if (i == w) SH_TRACE(misc, l, 8);
-      if (!down_item<kLE, kRows>(a, P, l, i, ep, lds)) return;
-      if (i == w) { SH_TRACE(misc, l, 9); SH_TRACE_WAIT(l, 4, misc); }
-    }
+    if (!for_items<kOne>(w, nE, G, [&](int i) {
+          if (i == w) SH_TRACE(misc, l, 8);
+          if (!down_item<kLE, kRows>(a, P, l, i, ep, lds)) return false;
+          if (i == w) { SH_TRACE(misc, l, 9); SH_TRACE_WAIT(l, 4, misc); }
+          return true;
+        }))
+      return;
     if (hasC && next && w < nA) load_weights<kLA, 1>(wa, layer_g(a, l + 1).wqkv, H, w);
   }
 #ifdef SH_DECODE_TRACE
@@ -1132,19 +1170,30 @@ Shape shape_of(int H, int heads, int kv_heads, int inter) {
   return Shape{kv_heads > 0 ? heads / kv_heads : 0, H / 256, heads * kD / 256, H / 256, inter / 256};
 }
 
-// The kernel for a shape and batch (batch 0: the batch-1 variant), and the
-// shape's split limit.
-const void *kernel_for(const Shape &s, int batch, int *max_splits) {
-#define SH_MATCH(G, LA, LC, LD, LE, SP)                                                \
-  if (s.g == G && s.la == LA && s.lc == LC && s.ld == LD && s.le == LE) {              \
-    if (max_splits) *max_splits = SP;                                                  \
-    return batch <= 1                                                                  \
-               ? reinterpret_cast<const void *>(&decode_layers_kernel<G, LA, LC, LD, LE, SP, 1>) \
-               : reinterpret_cast<const void *>(&decode_layers_kernel<G, LA, LC, LD, LE, SP, kMaxRowsPerPass>); \
+// The kernel for a shape and batch (batch 0: the batch-1 variant; `one`: at
+// most one item per workgroup in every phase), and the shape's split limit.
+const void *kernel_for(const Shape &s, int batch, bool one, int *max_splits) {
+#define SH_MATCH(G, LA, LC, LD, LE, SP)                                                            \
+  if (s.g == G && s.la == LA && s.lc == LC && s.ld == LD && s.le == LE) {                          \
+    if (max_splits) *max_splits = SP;                                                              \
+    if (batch > 1)                                                                                 \
+      return reinterpret_cast<const void *>(                                                       \
+          &decode_layers_kernel<G, LA, LC, LD, LE, SP, kMaxRowsPerPass, false>);                   \
+    return one ? reinterpret_cast<const void *>(&decode_layers_kernel<G, LA, LC, LD, LE, SP, 1, true>) \
+               : reinterpret_cast<const void *>(&decode_layers_kernel<G, LA, LC, LD, LE, SP, 1, false>); \
   }
   SH_LAYERS_SHAPES(SH_MATCH)
 #undef SH_MATCH
   return nullptr;
+}
+
+// Every phase of a launch with `grid` workgroups has at most one item per
+// workgroup.
+bool one_item_each(const LayersArgs &a, int grid) {
+  const int n[] = {a.qkv_n / 16, a.B * a.kv_heads * a.splits, a.B * a.heads, a.H / 16, a.inter / 16};
+  for (int k : n)
+    if (k > grid) return false;
+  return true;
 }
 
 size_t attn_lds(int g) {
@@ -1157,12 +1206,12 @@ bool decode_layers_supported(int layers, int H, int heads, int kv_heads, int hea
   if (layers < 1 || layers > kMaxDecodeLayers) return false;
   if (head_dim != kD || kv_heads <= 0 || heads % kv_heads != 0) return false;
   if (H % 256 || (heads * kD) % 256 || inter % 256 || H > 4096) return false;
-  return kernel_for(shape_of(H, heads, kv_heads, inter), 1, nullptr) != nullptr;
+  return kernel_for(shape_of(H, heads, kv_heads, inter), 1, false, nullptr) != nullptr;
 }
 
 int decode_layers_max_splits(int H, int heads, int kv_heads, int inter) {
   int sp = 0;
-  return kernel_for(shape_of(H, heads, kv_heads, inter), 1, &sp) ? sp : 0;
+  return kernel_for(shape_of(H, heads, kv_heads, inter), 1, false, &sp) ? sp : 0;
 }
 
 size_t decode_layers_lds(int B, int H, int heads, int inter, int *misc_offset) {
@@ -1184,8 +1233,8 @@ size_t decode_layers_partial_cells(int heads) { return (size_t)kMaxBatch * heads
 hipError_t decode_layers_occupancy(const LayersArgs &a, size_t lds, int *blocks_per_cu) {
   const Shape sh = shape_of(a.H, a.heads, a.kv_heads, a.inter);
   int least = 1 << 30;
-  for (int batch : {1, kMaxBatch}) {
-    const void *k = kernel_for(sh, batch, nullptr);
+  for (int v = 0; v < 3; v++) {
+    const void *k = kernel_for(sh, v == 2 ? kMaxBatch : 1, v == 0, nullptr);
     if (!k) return hipErrorInvalidValue;
     hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
@@ -1206,7 +1255,7 @@ hipError_t decode_layers_trace(void *dst, size_t bytes) {
 #endif
 
 hipError_t launch_decode_layers(hipStream_t s, const LayersArgs &a, int grid, size_t lds) {
-  const void *k = kernel_for(shape_of(a.H, a.heads, a.kv_heads, a.inter), a.B, nullptr);
+  const void *k = kernel_for(shape_of(a.H, a.heads, a.kv_heads, a.inter), a.B, one_item_each(a, grid), nullptr);
   if (!k) return hipErrorInvalidValue;
   void *args[] = {const_cast<LayersArgs *>(&a)};
   return hipLaunchCooperativeKernel(k, dim3(grid), dim3(kT), args, (unsigned)lds, s);
