@@ -670,14 +670,11 @@ constexpr int kVS = kBlk / 32;   // V steps of a block
 // LDS of an attention item, from the start of the dynamic area.
 template <int kG>
 struct AttnLds {
-  float raw[(kG + 2) * kD];  // this row's q (kG heads), new k and new v as produced
-  float qs[kG][kD];
+  float qs[kG][kD];  // this row's normed, rotated, scaled q of the KV head's query heads
   alignas(16) _Float16 knew[kD];
   _Float16 vnew[kD];
   float scores[kG][kMaxSplitChunk];
   alignas(16) _Float16 p[kG][kMaxSplitChunk + kBlk];  // probabilities, zero up to whole blocks
-  float red[4][kG][kD];
-  float wsum[8];
   float wmax[4][kG], wl[4][kG];
 };
 
@@ -761,83 +758,65 @@ __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, 
   if (s >= active || cap <= 0 || L > a.max_pos) return true;  // uniform
   const int h0 = kvh * kG;
   const unsigned tag = tag_of(ep, l);
-  // norm gains and this step's RoPE factors, requested before the wait
-  const int iq = t % kD, half = kD / 2, fi = iq % half;
-  const float qn = P.q_norm[iq], kn = P.k_norm[iq];
-  const float cs = gbl(a.rope)[(size_t)b * kD + fi], sn = gbl(a.rope)[(size_t)b * kD + half + fi];
+  // Each wave holds one head as a pair of cells per lane: waves 0 and 1 the
+  // query heads h0 and h0 + 1, wave 2 the new k, wave 3 the new v; lane j
+  // values e0 = 2 j and 2 j + 1. The RMSNorm of a head is a wave sum, and
+  // RoPE's rotate-half partner of index e (e +- 64) sits in lane j +- 32.
+  // This step's norm gains and RoPE factors are requested before the wait.
+  static_assert(kG == 2 && (kG + 2) * kD / 2 == kT, "one head per wave");
+  const int e0 = 2 * lane, fe = e0 & (kD / 2 - 1);
+  const SH_GLOBAL float *gain = wave == 2 ? P.k_norm : P.q_norm;
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  const f32x2 g = *reinterpret_cast<const SH_GLOBAL f32x2 *>(gain + e0);
+  const f32x2 cs = *reinterpret_cast<const SH_GLOBAL f32x2 *>(gbl(a.rope) + (size_t)b * kD + fe);
+  const f32x2 sn = *reinterpret_cast<const SH_GLOBAL f32x2 *>(gbl(a.rope) + (size_t)b * kD + kD / 2 + fe);
+  float v0, v1;
   {
-    // the row's q of heads h0.., new k and new v: one pair of cells per thread
     const size_t qrow = (size_t)b * a.qkv_n;
-    constexpr int kQ = kG * kD / 2, kPairs = (kG + 2) * kD / 2;
     size_t cell;
-    if (t < kQ) cell = qrow + (size_t)h0 * kD + 2 * t;
-    else if (t < kQ + kD / 2) cell = qrow + (size_t)a.heads * kD + kvh * kD + 2 * (t - kQ);
-    else cell = qrow + (size_t)(a.heads + kvn) * kD + kvh * kD + 2 * (min(t, kPairs - 1) - kQ - kD / 2);
+    if (wave < 2) cell = qrow + (size_t)(h0 + wave) * kD + e0;
+    else if (wave == 2) cell = qrow + (size_t)a.heads * kD + kvh * kD + e0;
+    else cell = qrow + (size_t)(a.heads + kvn) * kD + kvh * kD + e0;
     uint64_t cv[2];
-    const bool ok = spin_cells(a, a.qkvc, [&](int k) { return cell + k; }, t < kPairs ? 3ull : 0ull,
-                               tag, cv);
+    const bool ok = spin_cells(a, a.qkvc, [&](int k) { return cell + k; }, 3ull, tag, cv);
     if (!waits_ok(a, ok, misc)) return false;
     SH_MARK(misc, l, 8);
-    if (t < kPairs) {
-      S.raw[2 * t] = cell_f32(cv[0]);
-      S.raw[2 * t + 1] = cell_f32(cv[1]);
-    }
-    lds_barrier();
+    v0 = cell_f32(cv[0]);
+    v1 = cell_f32(cv[1]);
   }
   const int p1 = min(L, p0 + chunk), np = p1 - p0, pos = L - 1;
   const bool holds_new = p1 == L;  // this split holds the new token (S.knew / S.vnew)
-  {
-    const int gq = t / kD;
-    const bool q_thread = t < kG * kD;
-    const bool kv_thread = holds_new && t < kD;
-    float qv = S.raw[min(t, kG * kD - 1)];
-    float knv = S.raw[kG * kD + iq];
-    const float vv = S.raw[(kG + 1) * kD + iq];
-    if (!q_thread) qv = 0.0f;
-    if (!kv_thread) knv = 0.0f;
-    // RMSNorm over each head (kD / 64 waves per head), then RoPE
-    {
-      constexpr int kWavesPerHead = kD / 64;
-      const float qss = wave_sum_rows(qv * qv), kss = wave_sum_rows(knv * knv);
-      if (lane == 0) {
-        S.wsum[wave] = qss;
-        S.wsum[4 + wave] = kss;
-      }
-      lds_barrier();
-      if (q_thread) {
-        float ss = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kWavesPerHead; w++) ss += S.wsum[gq * kWavesPerHead + w];
-        qv = qv * (1.0f / sqrtf(ss / kD + a.eps)) * qn;
-      }
-      if (kv_thread) {
-        float ss = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kWavesPerHead; w++) ss += S.wsum[4 + w];
-        knv = knv * (1.0f / sqrtf(ss / kD + a.eps)) * kn;
-      }
-      if (q_thread) S.red[2][gq][iq] = qv;
-      if (kv_thread) S.red[3][0][iq] = knv;
-      lds_barrier();
-      if (q_thread) {
-        const float other = S.red[2][gq][iq < half ? iq + half : iq - half];
-        qv = iq < half ? qv * cs - other * sn : qv * cs + other * sn;
-      }
-      if (kv_thread) {
-        const float other = S.red[3][0][iq < half ? iq + half : iq - half];
-        knv = iq < half ? knv * cs - other * sn : knv * cs + other * sn;
-      }
+  if (wave < 3) {  // q heads and k: RMSNorm over the head, then RoPE
+    const float ss = wave_sum_rows(v0 * v0 + v1 * v1);
+    const float inv = 1.0f / sqrtf(ss / kD + a.eps);
+    v0 = v0 * inv * g.x;
+    v1 = v1 * inv * g.y;
+    const float o0 = __shfl_xor(v0, 32, 64), o1 = __shfl_xor(v1, 32, 64);
+    if (lane < 32) {
+      v0 = v0 * cs.x - o0 * sn.x;
+      v1 = v1 * cs.y - o1 * sn.y;
+    } else {
+      v0 = v0 * cs.x + o0 * sn.x;
+      v1 = v1 * cs.y + o1 * sn.y;
     }
-    if (q_thread) S.qs[gq][iq] = qv * a.scale;
-    if (kv_thread) {
-      const _Float16 k16 = (_Float16)knv, v16 = (_Float16)vv;
-      S.knew[iq] = k16;
-      S.vnew[iq] = v16;
-      kb[(size_t)pos * kD + iq] = __builtin_bit_cast(uint16_t, k16);
-      vtb[(size_t)iq * a.vt_stride + pos] = __builtin_bit_cast(uint16_t, v16);
-    }
-    lds_barrier();
   }
+  if (wave < 2) {
+    *reinterpret_cast<f32x2 *>(&S.qs[wave][e0]) = f32x2{v0 * a.scale, v1 * a.scale};
+  } else if (holds_new) {
+    const _Float16 h0v = (_Float16)v0, h1v = (_Float16)v1;
+    const uint16_t u0 = __builtin_bit_cast(uint16_t, h0v), u1 = __builtin_bit_cast(uint16_t, h1v);
+    if (wave == 2) {
+      S.knew[e0] = h0v;
+      S.knew[e0 + 1] = h1v;
+      *reinterpret_cast<SH_GLOBAL uint32_t *>(kb + (size_t)pos * kD + e0) = (uint32_t)u0 | ((uint32_t)u1 << 16);
+    } else {
+      S.vnew[e0] = h0v;
+      S.vnew[e0 + 1] = h1v;
+      vtb[(size_t)e0 * a.vt_stride + pos] = u0;
+      vtb[(size_t)(e0 + 1) * a.vt_stride + pos] = u1;
+    }
+  }
+  lds_barrier();
   SH_MARK(misc, l, 9);
 
   // q as the MFMA A operand: row lane % 16 = head (zero past kG), k = 32 kk + 8 (lane / 16)
