@@ -76,16 +76,16 @@ __global__ __launch_bounds__(kBlock) void brightness_byte_kernel(const uint8_t *
 // ---------------------------------------------------------------------------
 // Blur, RGBA streaming kernel.
 //
-// One wave owns a column strip of kStripPx output pixels and kRows output rows.
+// One wave owns a column strip of kStripPx output pixels and kR output rows.
 // Lane l holds the 16-byte chunk of pixels [x0 - 4 + 4l, x0 + 4l) of each
 // input row; lanes 1..62 produce output, lanes 0 and 63 only supply the two
 // halo pixels their neighbours need (exchanged with lane shuffles, no LDS).
-// The wave walks down its strip: every input row is loaded once (16-byte
-// loads, the next group of 5 rows in flight while the current one is summed),
-// split into 16-bit lanes (R|B and G|A words), summed horizontally over 5
-// pixels, and pushed into a 5-row register ring whose running column sum is
-// the 25-tap box sum. Ring slots are static because rows are processed in
-// unrolled groups of 5.
+// The wave walks down its strip one input row per step: the row is split
+// into 16-bit lanes (R|B and G|A words) and added to the 5-row column sums,
+// the row leaving the window is subtracted, and the 5-pixel horizontal sum
+// of the column sums is the 25-tap box sum of the output row two rows up.
+// Raw rows sit in a 10-slot register ring (the window, the current row and
+// the next four in flight); the loop is unrolled so the slots are static.
 // ---------------------------------------------------------------------------
 
 constexpr int kStripPx = 248;  // 62 output lanes x 4 pixels
@@ -132,26 +132,77 @@ struct StreamArgs {
   uint32_t d_lo, d_hi;  // brightness deltas per 16-bit lane (R|B, G|A)
 };
 
-// Horizontal 5-pixel sums of the 4 pixels of this lane, as 16-bit lanes:
-// h[2k] = R|B, h[2k+1] = G|A of pixel k. `v` is this lane's 4 pixels; the two
-// pixels on either side come from the neighbouring lanes. At the image's left
-// and right edges the missing neighbours are replaced by the edge pixel
-// (config: clamp) or by zero (reference: out-of-bounds taps add nothing).
+// Bytes of one output pixel from its 25-tap sums (lo word R|B, hi word G|A,
+// each lane < 6400; in config mode the lanes already carry the +12 rounding
+// bias). floor(s / 25) = (s * 671089) >> 24 exactly for s < 6400: 671089 /
+// 2^24 exceeds 1/25 by < 2.2e-8, the product fits 32 bits and the quotient is
+// its top byte, which v_perm gathers.
+template <int kMode>
+__device__ __forceinline__ uint32_t finish_pixel(uint32_t vl, uint32_t vh, uint32_t count) {
+  if (kMode == SH_BLUR_CONFIG || count == 25) {
+    const uint32_t r = __umul24(vl & 0xffffu, 671089u);
+    const uint32_t b = __umul24(vl >> 16, 671089u);
+    const uint32_t g = __umul24(vh & 0xffffu, 671089u);
+    const uint32_t a = __umul24(vh >> 16, 671089u);
+    const uint32_t rg = __builtin_amdgcn_perm(g, r, 0x0c0c0703u);
+    const uint32_t ba = __builtin_amdgcn_perm(a, b, 0x07030c0cu);
+    return rg | ba;
+  }
+  const uint32_t c0 = (vl & 0xffffu) / count, c2 = (vl >> 16) / count;
+  const uint32_t c1 = (vh & 0xffffu) / count, c3 = (vh >> 16) / count;
+  return c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
+}
+
+// One input row for this lane (a cached load: the band above and below read
+// the same halo rows). The row index is wave-uniform (scalar), so the
+// row address is scalar and each lane adds its column offset. Lanes whose
+// chunk lies outside the image load a valid chunk nobody uses (the edge fix-up
+// in hsum supplies the clamped or zero taps instead).
+template <int kMode>
+__device__ __forceinline__ u32x4 load_row(const StreamArgs &a, int y, int lx) {
+  if (kMode == SH_BLUR_CONFIG) {
+    const int cy = min(max(y, 0), a.height - 1);
+    return *reinterpret_cast<const u32x4 *>(a.in + (size_t)cy * (size_t)a.width + lx);
+  } else {
+    if (y < 0 || y >= a.height) return u32x4{0, 0, 0, 0};
+    return *reinterpret_cast<const u32x4 *>(a.in + (size_t)y * (size_t)a.width + lx);
+  }
+}
+
+// Input rows y0 - 2 .. y0 + kR + 1 are loaded once per wave (kR + 4 loads
+// for kR output rows; the halo rows are shared with the neighbouring bands
+// through L2), each 5 steps before its use.
+// This lane's 4 pixels of one input row as 16-bit lanes, brightened (kFuse);
+// reference mode: rows outside the image contribute nothing.
 template <int kMode, int kFuse>
-__device__ __forceinline__ void hsum(const u32x4 v, int y, int height, uint32_t h[8],
-                                     bool left_edge, bool right_edge, uint32_t d_lo,
-                                     uint32_t d_hi) {
-  if (kMode == SH_BLUR_REFERENCE && (y < 0 || y >= height)) {  // row outside: no taps
+__device__ __forceinline__ void expand_row(const u32x4 v, int y, int height, uint32_t e[8],
+                                           uint32_t d_lo, uint32_t d_hi) {
+  if (kMode == SH_BLUR_REFERENCE && (y < 0 || y >= height)) {
 #pragma unroll
-    for (int k = 0; k < 8; k++) h[k] = 0;
+    for (int k = 0; k < 8; k++) e[k] = 0;
     return;
   }
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    e[2 * k] = brighten_lanes<kFuse>(__builtin_amdgcn_perm(0u, w[k], 0x0c020c00u), d_lo);
+    e[2 * k + 1] = brighten_lanes<kFuse>(__builtin_amdgcn_perm(0u, w[k], 0x0c030c01u), d_hi);
+  }
+}
+
+// 5-pixel horizontal sums of the column sums vs (layout of expand_row: vs[2k]
+// R|B, vs[2k+1] G|A of pixel k). The two columns on either side come from the
+// neighbouring lanes; at the image's left and right edges the missing columns
+// are replaced by the edge column (config: clamp) or by zero (reference:
+// out-of-bounds taps add nothing).
+template <int kMode>
+__device__ __forceinline__ void hsum_cols(const uint32_t vs[8], uint32_t h[8], bool left_edge,
+                                          bool right_edge) {
   uint32_t lo[8], hi[8];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    lo[k + 2] = brighten_lanes<kFuse>(__builtin_amdgcn_perm(0u, w[k], 0x0c020c00u), d_lo);
-    hi[k + 2] = brighten_lanes<kFuse>(__builtin_amdgcn_perm(0u, w[k], 0x0c030c01u), d_hi);
+    lo[k + 2] = vs[2 * k];
+    hi[k + 2] = vs[2 * k + 1];
   }
   lo[0] = from_left(lo[4]);
   lo[1] = from_left(lo[5]);
@@ -192,49 +243,9 @@ __device__ __forceinline__ void hsum(const u32x4 v, int y, int height, uint32_t 
   }
 }
 
-// Bytes of one output pixel from its 25-tap sums (lo word R|B, hi word G|A,
-// each lane < 6400; in config mode the lanes already carry the +12 rounding
-// bias). floor(s / 25) = (s * 671089) >> 24 exactly for s < 6400: 671089 /
-// 2^24 exceeds 1/25 by < 2.2e-8, the product fits 32 bits and the quotient is
-// its top byte, which v_perm gathers.
-template <int kMode>
-__device__ __forceinline__ uint32_t finish_pixel(uint32_t vl, uint32_t vh, uint32_t count) {
-  if (kMode == SH_BLUR_CONFIG || count == 25) {
-    const uint32_t r = __umul24(vl & 0xffffu, 671089u);
-    const uint32_t b = __umul24(vl >> 16, 671089u);
-    const uint32_t g = __umul24(vh & 0xffffu, 671089u);
-    const uint32_t a = __umul24(vh >> 16, 671089u);
-    const uint32_t rg = __builtin_amdgcn_perm(g, r, 0x0c0c0703u);
-    const uint32_t ba = __builtin_amdgcn_perm(a, b, 0x07030c0cu);
-    return rg | ba;
-  }
-  const uint32_t c0 = (vl & 0xffffu) / count, c2 = (vl >> 16) / count;
-  const uint32_t c1 = (vh & 0xffffu) / count, c3 = (vh >> 16) / count;
-  return c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
-}
-
-// One input row for this lane (a cached load: the band above and below read
-// the same halo rows). The row index is wave-uniform (scalar), so the
-// row address is scalar and each lane adds its column offset. Lanes whose
-// chunk lies outside the image load a valid chunk nobody uses (the edge fix-up
-// in hsum supplies the clamped or zero taps instead).
-template <int kMode>
-__device__ __forceinline__ u32x4 load_row(const StreamArgs &a, int y, int lx) {
-  if (kMode == SH_BLUR_CONFIG) {
-    const int cy = min(max(y, 0), a.height - 1);
-    return *reinterpret_cast<const u32x4 *>(a.in + (size_t)cy * (size_t)a.width + lx);
-  } else {
-    if (y < 0 || y >= a.height) return u32x4{0, 0, 0, 0};
-    return *reinterpret_cast<const u32x4 *>(a.in + (size_t)y * (size_t)a.width + lx);
-  }
-}
-
-template <int kMode, int kFuse, int kGroups>
-__global__ __launch_bounds__(kBlock) void blur_rgba_stream_kernel(const StreamArgs a) {
-  constexpr int kRows = 5 * kGroups;
-  // Blocks are dealt round-robin to the 8 XCDs; renumber them so each XCD
-  // walks a contiguous range of waves (neighbouring bands share halo rows in
-  // that XCD's L2).
+template <int kMode, int kFuse, int kR>
+__global__ __launch_bounds__(kBlock) void blur_rgba_rows_kernel(const StreamArgs a) {
+  constexpr int kQ = 10;  // raw row ring
   int b = blockIdx.x;
   if (a.xcd_blocks) b = (b & 7) * a.xcd_blocks + (b >> 3);
   const int lane = threadIdx.x & 63;
@@ -242,82 +253,64 @@ __global__ __launch_bounds__(kBlock) void blur_rgba_stream_kernel(const StreamAr
   if (wi >= a.total_waves) return;
   const int sx = wi % a.strips_x, band = wi / a.strips_x;
   const int x0 = sx * kStripPx;
-  const int cx = x0 - 4 + 4 * lane;  // first pixel of this lane's chunk
+  const int cx = x0 - 4 + 4 * lane;
   const int lx = min(max(cx, 0), a.width - 4);
-  const bool left_edge = cx == 0;              // pixels -2, -1 are outside
-  const bool right_edge = cx + 4 == a.width;   // pixels W, W+1 are outside
-  const int y0 = band * kRows;
+  const bool left_edge = cx == 0;
+  const bool right_edge = cx + 4 == a.width;
+  const int y0 = band * kR;
   const bool writer = lane >= 1 && lane <= 62 && cx < a.width;
-  const int out_rows = min(kRows, a.height - y0);
+  const int out_rows = min(kR, a.height - y0);
 
-  int cxk[4];  // reference mode: in-bounds taps per row for each pixel
+  int cxk[4];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
     const int x = cx + k;
     cxk[k] = min(x + 2, a.width - 1) - max(x - 2, 0) + 1;
   }
-
-  // vs starts at the config mode's +12 rounding bias in every lane.
+  // the config mode's +12 rounding bias, added to the 25-tap sums
   const uint32_t bias = kMode == SH_BLUR_CONFIG ? 0x000c000cu : 0u;
-  uint32_t ring[5][8];
   uint32_t vs[8];
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    vs[i] = bias;
-    ring[4][i] = 0;
-  }
-  {  // prologue: input rows y0-2 .. y0+1 into slots 0..3
-    u32x4 p[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) p[r] = load_row<kMode>(a, y0 - 2 + r, lx);
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      hsum<kMode, kFuse>(p[r], y0 - 2 + r, a.height, ring[r], left_edge, right_edge, a.d_lo,
-                         a.d_hi);
-#pragma unroll
-      for (int i = 0; i < 8; i++) vs[i] += ring[r][i];
-    }
-  }
+  for (int k = 0; k < 8; k++) vs[k] = 0;
 
-  u32x4 cur[5], nxt[5];
+  // step i handles input row y0 - 2 + i (i < kR + 4); ring slot i % kQ
+  u32x4 raw[kQ];
 #pragma unroll
-  for (int r = 0; r < 5; r++) cur[r] = load_row<kMode>(a, y0 + 2 + r, lx);
-
-#pragma unroll 1
-  for (int g = 0; g < kGroups; g++) {
-    if (5 * g >= out_rows) break;
-    if (g + 1 < kGroups) {
+  for (int i = 0; i < 5; i++) raw[i] = load_row<kMode>(a, y0 - 2 + i, lx);
 #pragma unroll
-      for (int r = 0; r < 5; r++) nxt[r] = load_row<kMode>(a, y0 + 7 + 5 * g + r, lx);
+  for (int i = 0; i < kR + 4; i++) {
+    if (i >= 5) {  // the row leaving the window
+      uint32_t e[8];
+      expand_row<kMode, kFuse>(raw[(i - 5) % kQ], y0 - 7 + i, a.height, e, a.d_lo, a.d_hi);
+#pragma unroll
+      for (int k = 0; k < 8; k++) vs[k] -= e[k];
     }
+    if (i + 5 < kR + 4) raw[(i + 5) % kQ] = load_row<kMode>(a, y0 + 3 + i, lx);
+    {
+      uint32_t e[8];
+      expand_row<kMode, kFuse>(raw[i % kQ], y0 - 2 + i, a.height, e, a.d_lo, a.d_hi);
 #pragma unroll
-    for (int i = 0; i < 5; i++) {
-      const int slot = (4 + i) % 5;  // input row 4 + 5g + i of the strip
+      for (int k = 0; k < 8; k++) vs[k] += e[k];
+    }
+    if (i >= 4) {
+      const int row = i - 4, y = y0 + row;
       uint32_t h[8];
-      hsum<kMode, kFuse>(cur[i], y0 + 2 + 5 * g + i, a.height, h, left_edge, right_edge, a.d_lo,
-                         a.d_hi);
+      hsum_cols<kMode>(vs, h, left_edge, right_edge);
 #pragma unroll
-      for (int k = 0; k < 8; k++) {
-        vs[k] = (vs[k] - ring[slot][k]) + h[k];  // lanes never borrow: ring is part of vs
-        ring[slot][k] = h[k];
-      }
-      const int row = 5 * g + i;
-      const int y = y0 + row;
+      for (int k = 0; k < 8; k++) h[k] += bias;
       if (writer && row < out_rows) {
         const uint32_t ry = kMode == SH_BLUR_CONFIG
                                 ? 5u
                                 : (uint32_t)(min(y + 2, a.height - 1) - max(y - 2, 0) + 1);
         u32x4 o;
-        o.x = finish_pixel<kMode>(vs[0], vs[1], ry * cxk[0]);
-        o.y = finish_pixel<kMode>(vs[2], vs[3], ry * cxk[1]);
-        o.z = finish_pixel<kMode>(vs[4], vs[5], ry * cxk[2]);
-        o.w = finish_pixel<kMode>(vs[6], vs[7], ry * cxk[3]);
+        o.x = finish_pixel<kMode>(h[0], h[1], ry * cxk[0]);
+        o.y = finish_pixel<kMode>(h[2], h[3], ry * cxk[1]);
+        o.z = finish_pixel<kMode>(h[4], h[5], ry * cxk[2]);
+        o.w = finish_pixel<kMode>(h[6], h[7], ry * cxk[3]);
         __builtin_nontemporal_store(
             o, reinterpret_cast<u32x4 *>(a.out + (size_t)y * (size_t)a.width + cx));
       }
     }
-#pragma unroll
-    for (int r = 0; r < 5; r++) cur[r] = nxt[r];
   }
 }
 
@@ -374,30 +367,30 @@ Brightness make_brightness(bool enabled, int channels, int delta, int all_channe
   return br;
 }
 
-// Output rows per wave = 5 * groups: 2 (10 rows) by default; the
-// STRICT_HIP_BLUR_GROUPS environment variable (1, 2 or 4) overrides it for
-// tuning sweeps.
-int blur_groups() {
-  static const int groups = [] {
-    const char *e = getenv("STRICT_HIP_BLUR_GROUPS");
-    const int g = e ? atoi(e) : 2;
-    return (g == 1 || g == 4) ? g : 2;
+// Output rows per wave: 8 by default (measured fastest on 4096 x 4096: 31.0
+// us against 31.9 / 32.9 us for 16 / 32 rows); the STRICT_HIP_BLUR_ROWS
+// environment variable (8, 16 or 32) overrides it for tuning sweeps.
+int blur_rows() {
+  static const int rows = [] {
+    const char *e = getenv("STRICT_HIP_BLUR_ROWS");
+    const int r = e ? atoi(e) : 8;
+    return (r == 16 || r == 32) ? r : 8;
   }();
-  return groups;
+  return rows;
 }
 
-template <int kMode, int kGroups>
-void launch_stream_fuse(hipStream_t s, const StreamArgs &a, int fuse) {
+template <int kMode, int kR>
+void launch_rows_fuse(hipStream_t s, const StreamArgs &a, int fuse) {
   const int blocks = a.xcd_blocks * 8;
   if (fuse == 1)
-    blur_rgba_stream_kernel<kMode, 1, kGroups><<<blocks, kBlock, 0, s>>>(a);
+    blur_rgba_rows_kernel<kMode, 1, kR><<<blocks, kBlock, 0, s>>>(a);
   else if (fuse == 2)
-    blur_rgba_stream_kernel<kMode, 2, kGroups><<<blocks, kBlock, 0, s>>>(a);
+    blur_rgba_rows_kernel<kMode, 2, kR><<<blocks, kBlock, 0, s>>>(a);
   else
-    blur_rgba_stream_kernel<kMode, 0, kGroups><<<blocks, kBlock, 0, s>>>(a);
+    blur_rgba_rows_kernel<kMode, 0, kR><<<blocks, kBlock, 0, s>>>(a);
 }
 
-template <int kGroups>
+template <int kRowsPerWave>
 void launch_blur_stream(hipStream_t s, const uint32_t *in, uint32_t *out, int width, int height,
                         int mode, bool fuse, int delta, int all_channels) {
   StreamArgs a;
@@ -406,7 +399,7 @@ void launch_blur_stream(hipStream_t s, const uint32_t *in, uint32_t *out, int wi
   a.width = width;
   a.height = height;
   a.strips_x = (width + kStripPx - 1) / kStripPx;
-  const int bands = (height + 5 * kGroups - 1) / (5 * kGroups);
+  const int bands = (height + kRowsPerWave - 1) / kRowsPerWave;
   a.total_waves = a.strips_x * bands;
   // padded to a multiple of 8 workgroups (the extra waves exit at once) so
   // that every XCD gets an equal contiguous range of bands
@@ -421,9 +414,9 @@ void launch_blur_stream(hipStream_t s, const uint32_t *in, uint32_t *out, int wi
     a.d_hi = d | (all_channels ? d << 16 : 0u);             // G, and A only if asked
   }
   if (mode == SH_BLUR_CONFIG)
-    launch_stream_fuse<SH_BLUR_CONFIG, kGroups>(s, a, f);
+    launch_rows_fuse<SH_BLUR_CONFIG, kRowsPerWave>(s, a, f);
   else
-    launch_stream_fuse<SH_BLUR_REFERENCE, kGroups>(s, a, f);
+    launch_rows_fuse<SH_BLUR_REFERENCE, kRowsPerWave>(s, a, f);
 }
 
 }  // namespace
@@ -449,15 +442,15 @@ hipError_t launch_blur5_u8(hipStream_t s, const uint8_t *in, uint8_t *out, int w
   if (channels == 4 && width % 4 == 0 && aligned16(in) && aligned16(out)) {
     const uint32_t *in32 = reinterpret_cast<const uint32_t *>(in);
     uint32_t *out32 = reinterpret_cast<uint32_t *>(out);
-    switch (blur_groups()) {
-      case 1:
-        launch_blur_stream<1>(s, in32, out32, width, height, mode, fuse, delta, all_channels);
+    switch (blur_rows()) {
+      case 16:
+        launch_blur_stream<16>(s, in32, out32, width, height, mode, fuse, delta, all_channels);
         break;
-      case 4:
-        launch_blur_stream<4>(s, in32, out32, width, height, mode, fuse, delta, all_channels);
+      case 32:
+        launch_blur_stream<32>(s, in32, out32, width, height, mode, fuse, delta, all_channels);
         break;
       default:
-        launch_blur_stream<2>(s, in32, out32, width, height, mode, fuse, delta, all_channels);
+        launch_blur_stream<8>(s, in32, out32, width, height, mode, fuse, delta, all_channels);
         break;
     }
   } else {
