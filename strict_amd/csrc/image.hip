@@ -77,18 +77,20 @@ __global__ __launch_bounds__(kBlock) void brightness_byte_kernel(const uint8_t *
 // Blur, RGBA streaming kernel.
 //
 // One wave owns a column strip of kStripPx output pixels and kR output rows.
-// Lane l holds the 16-byte chunk of pixels [x0 - 4 + 4l, x0 + 4l) of each
-// input row; lanes 1..62 produce output, lanes 0 and 63 only supply the two
-// halo pixels their neighbours need (exchanged with lane shuffles, no LDS).
+// Lane l holds the 16-byte chunk of pixels [x0 + 4l, x0 + 4l + 4) of each
+// input row (each wave row is 1 KiB, aligned); lanes 0 and 63 also load the
+// two pixels left and right of the strip (8 bytes each). Neighbouring columns
+// cross lanes by DPP lane moves, no LDS.
 // The wave walks down its strip one input row per step: the row is split
-// into 16-bit lanes (R|B and G|A words) and added to the 5-row column sums,
-// the row leaving the window is subtracted, and the 5-pixel horizontal sum
-// of the column sums is the 25-tap box sum of the output row two rows up.
-// Raw rows sit in a 10-slot register ring (the window, the current row and
-// the next four in flight); the loop is unrolled so the slots are static.
+// into 16-bit lanes (R|B and G|A words) and added to the 5-row column sums
+// (the halo pixels' sums alongside), the row leaving the window is
+// subtracted, and the 5-pixel horizontal sum of the column sums is the
+// 25-tap box sum of the output row two rows up. Raw rows sit in a 10-slot
+// register ring (the window, the current row and the next four in flight);
+// the loop is unrolled so the slots are static.
 // ---------------------------------------------------------------------------
 
-constexpr int kStripPx = 248;  // 62 output lanes x 4 pixels
+constexpr int kStripPx = 256;  // 64 lanes x 4 pixels
 
 // SWAR brightness on packed RGBA words (direct kernel and byte paths).
 struct Brightness {
@@ -169,9 +171,6 @@ __device__ __forceinline__ u32x4 load_row(const StreamArgs &a, int y, int lx) {
   }
 }
 
-// Input rows y0 - 2 .. y0 + kR + 1 are loaded once per wave (kR + 4 loads
-// for kR output rows; the halo rows are shared with the neighbouring bands
-// through L2), each 5 steps before its use.
 // This lane's 4 pixels of one input row as 16-bit lanes, brightened (kFuse);
 // reference mode: rows outside the image contribute nothing.
 template <int kMode, int kFuse>
@@ -190,62 +189,12 @@ __device__ __forceinline__ void expand_row(const u32x4 v, int y, int height, uin
   }
 }
 
-// 5-pixel horizontal sums of the column sums vs (layout of expand_row: vs[2k]
-// R|B, vs[2k+1] G|A of pixel k). The two columns on either side come from the
-// neighbouring lanes; at the image's left and right edges the missing columns
-// are replaced by the edge column (config: clamp) or by zero (reference:
-// out-of-bounds taps add nothing).
-template <int kMode>
-__device__ __forceinline__ void hsum_cols(const uint32_t vs[8], uint32_t h[8], bool left_edge,
-                                          bool right_edge) {
-  uint32_t lo[8], hi[8];
-#pragma unroll
-  for (int k = 0; k < 4; k++) {
-    lo[k + 2] = vs[2 * k];
-    hi[k + 2] = vs[2 * k + 1];
-  }
-  lo[0] = from_left(lo[4]);
-  lo[1] = from_left(lo[5]);
-  hi[0] = from_left(hi[4]);
-  hi[1] = from_left(hi[5]);
-  lo[6] = from_right(lo[2]);
-  lo[7] = from_right(lo[3]);
-  hi[6] = from_right(hi[2]);
-  hi[7] = from_right(hi[3]);
-  if (kMode == SH_BLUR_CONFIG) {
-    lo[0] = left_edge ? lo[2] : lo[0];
-    lo[1] = left_edge ? lo[2] : lo[1];
-    hi[0] = left_edge ? hi[2] : hi[0];
-    hi[1] = left_edge ? hi[2] : hi[1];
-    lo[6] = right_edge ? lo[5] : lo[6];
-    lo[7] = right_edge ? lo[5] : lo[7];
-    hi[6] = right_edge ? hi[5] : hi[6];
-    hi[7] = right_edge ? hi[5] : hi[7];
-  } else {
-    lo[0] = left_edge ? 0u : lo[0];
-    lo[1] = left_edge ? 0u : lo[1];
-    hi[0] = left_edge ? 0u : hi[0];
-    hi[1] = left_edge ? 0u : hi[1];
-    lo[6] = right_edge ? 0u : lo[6];
-    lo[7] = right_edge ? 0u : lo[7];
-    hi[6] = right_edge ? 0u : hi[6];
-    hi[7] = right_edge ? 0u : hi[7];
-  }
-#pragma unroll
-  for (int part = 0; part < 2; part++) {
-    const uint32_t *a = part ? hi : lo;
-    const uint32_t u34 = a[3] + a[4];
-    const uint32_t s = a[2] + u34, t = u34 + a[5];
-    h[0 + part] = s + a[0] + a[1];
-    h[2 + part] = s + a[1] + a[5];
-    h[4 + part] = t + a[2] + a[6];
-    h[6 + part] = t + a[6] + a[7];
-  }
-}
-
+// Input rows y0 - 2 .. y0 + kR + 1 are loaded once per wave (kR + 4 loads
+// for kR output rows; the halo rows are shared with the neighbouring bands
+// through L2), each 5 steps before its use.
 template <int kMode, int kFuse, int kR>
 __global__ __launch_bounds__(kBlock) void blur_rgba_rows_kernel(const StreamArgs a) {
-  constexpr int kQ = 10;  // raw row ring
+  constexpr int kQ = 10;
   int b = blockIdx.x;
   if (a.xcd_blocks) b = (b & 7) * a.xcd_blocks + (b >> 3);
   const int lane = threadIdx.x & 63;
@@ -253,12 +202,15 @@ __global__ __launch_bounds__(kBlock) void blur_rgba_rows_kernel(const StreamArgs
   if (wi >= a.total_waves) return;
   const int sx = wi % a.strips_x, band = wi / a.strips_x;
   const int x0 = sx * kStripPx;
-  const int cx = x0 - 4 + 4 * lane;
-  const int lx = min(max(cx, 0), a.width - 4);
+  const int cx = x0 + 4 * lane;
+  const int lx = min(cx, a.width - 4);
   const bool left_edge = cx == 0;
   const bool right_edge = cx + 4 == a.width;
+  const bool halo_lane = lane == 0 || lane == 63;
+  // halo pixels: lane 0 the two left of the strip, lane 63 the two right of it
+  const int hx = lane == 0 ? max(x0 - 2, 0) : min(x0 + kStripPx, a.width - 2);
   const int y0 = band * kR;
-  const bool writer = lane >= 1 && lane <= 62 && cx < a.width;
+  const bool writer = cx < a.width;
   const int out_rows = min(kR, a.height - y0);
 
   int cxk[4];
@@ -267,37 +219,124 @@ __global__ __launch_bounds__(kBlock) void blur_rgba_rows_kernel(const StreamArgs
     const int x = cx + k;
     cxk[k] = min(x + 2, a.width - 1) - max(x - 2, 0) + 1;
   }
-  // the config mode's +12 rounding bias, added to the 25-tap sums
   const uint32_t bias = kMode == SH_BLUR_CONFIG ? 0x000c000cu : 0u;
-  uint32_t vs[8];
+  uint32_t vs[8], hs[4];
 #pragma unroll
   for (int k = 0; k < 8; k++) vs[k] = 0;
-
-  // step i handles input row y0 - 2 + i (i < kR + 4); ring slot i % kQ
-  u32x4 raw[kQ];
 #pragma unroll
-  for (int i = 0; i < 5; i++) raw[i] = load_row<kMode>(a, y0 - 2 + i, lx);
+  for (int k = 0; k < 4; k++) hs[k] = 0;
+
+  auto load_halo = [&](int y) -> u32x2 {
+    u32x2 v = {0u, 0u};
+    int cy = y;
+    if (kMode == SH_BLUR_CONFIG) cy = min(max(y, 0), a.height - 1);
+    else if (y < 0 || y >= a.height) return v;
+    if (halo_lane) v = *reinterpret_cast<const u32x2 *>(a.in + (size_t)cy * (size_t)a.width + hx);
+    return v;
+  };
+  auto expand_halo = [&](const u32x2 v, int y, uint32_t e[4]) {
+    if (kMode == SH_BLUR_REFERENCE && (y < 0 || y >= a.height)) {
+#pragma unroll
+      for (int k = 0; k < 4; k++) e[k] = 0;
+      return;
+    }
+    const uint32_t w[2] = {v.x, v.y};
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      e[2 * k] = brighten_lanes<kFuse>(__builtin_amdgcn_perm(0u, w[k], 0x0c020c00u), a.d_lo);
+      e[2 * k + 1] = brighten_lanes<kFuse>(__builtin_amdgcn_perm(0u, w[k], 0x0c030c01u), a.d_hi);
+    }
+  };
+
+  u32x4 raw[kQ];
+  u32x2 hraw[kQ];
+#pragma unroll
+  for (int i = 0; i < 5; i++) {
+    raw[i] = load_row<kMode>(a, y0 - 2 + i, lx);
+    hraw[i] = load_halo(y0 - 2 + i);
+  }
 #pragma unroll
   for (int i = 0; i < kR + 4; i++) {
-    if (i >= 5) {  // the row leaving the window
-      uint32_t e[8];
+    if (i >= 5) {
+      uint32_t e[8], eh[4];
       expand_row<kMode, kFuse>(raw[(i - 5) % kQ], y0 - 7 + i, a.height, e, a.d_lo, a.d_hi);
+      expand_halo(hraw[(i - 5) % kQ], y0 - 7 + i, eh);
 #pragma unroll
       for (int k = 0; k < 8; k++) vs[k] -= e[k];
+#pragma unroll
+      for (int k = 0; k < 4; k++) hs[k] -= eh[k];
     }
-    if (i + 5 < kR + 4) raw[(i + 5) % kQ] = load_row<kMode>(a, y0 + 3 + i, lx);
+    if (i + 5 < kR + 4) {
+      raw[(i + 5) % kQ] = load_row<kMode>(a, y0 + 3 + i, lx);
+      hraw[(i + 5) % kQ] = load_halo(y0 + 3 + i);
+    }
     {
-      uint32_t e[8];
+      uint32_t e[8], eh[4];
       expand_row<kMode, kFuse>(raw[i % kQ], y0 - 2 + i, a.height, e, a.d_lo, a.d_hi);
+      expand_halo(hraw[i % kQ], y0 - 2 + i, eh);
 #pragma unroll
       for (int k = 0; k < 8; k++) vs[k] += e[k];
+#pragma unroll
+      for (int k = 0; k < 4; k++) hs[k] += eh[k];
     }
     if (i >= 4) {
       const int row = i - 4, y = y0 + row;
-      uint32_t h[8];
-      hsum_cols<kMode>(vs, h, left_edge, right_edge);
+      // columns cx-2, cx-1 and cx+4, cx+5: neighbours' sums, the halo sums
+      // at the strip's ends, the edge rule at the image's
+      uint32_t lo[8], hi[8];
 #pragma unroll
-      for (int k = 0; k < 8; k++) h[k] += bias;
+      for (int k = 0; k < 4; k++) {
+        lo[k + 2] = vs[2 * k];
+        hi[k + 2] = vs[2 * k + 1];
+      }
+      // (the lane moves run in every lane first: a move under a branch would
+      // read an inactive neighbour)
+      lo[0] = from_left(lo[4]);
+      lo[1] = from_left(lo[5]);
+      hi[0] = from_left(hi[4]);
+      hi[1] = from_left(hi[5]);
+      lo[6] = from_right(lo[2]);
+      lo[7] = from_right(lo[3]);
+      hi[6] = from_right(hi[2]);
+      hi[7] = from_right(hi[3]);
+      lo[0] = lane == 0 ? hs[0] : lo[0];
+      lo[1] = lane == 0 ? hs[2] : lo[1];
+      hi[0] = lane == 0 ? hs[1] : hi[0];
+      hi[1] = lane == 0 ? hs[3] : hi[1];
+      lo[6] = lane == 63 ? hs[0] : lo[6];
+      lo[7] = lane == 63 ? hs[2] : lo[7];
+      hi[6] = lane == 63 ? hs[1] : hi[6];
+      hi[7] = lane == 63 ? hs[3] : hi[7];
+      if (kMode == SH_BLUR_CONFIG) {
+        lo[0] = left_edge ? lo[2] : lo[0];
+        lo[1] = left_edge ? lo[2] : lo[1];
+        hi[0] = left_edge ? hi[2] : hi[0];
+        hi[1] = left_edge ? hi[2] : hi[1];
+        lo[6] = right_edge ? lo[5] : lo[6];
+        lo[7] = right_edge ? lo[5] : lo[7];
+        hi[6] = right_edge ? hi[5] : hi[6];
+        hi[7] = right_edge ? hi[5] : hi[7];
+      } else {
+        lo[0] = left_edge ? 0u : lo[0];
+        lo[1] = left_edge ? 0u : lo[1];
+        hi[0] = left_edge ? 0u : hi[0];
+        hi[1] = left_edge ? 0u : hi[1];
+        lo[6] = right_edge ? 0u : lo[6];
+        lo[7] = right_edge ? 0u : lo[7];
+        hi[6] = right_edge ? 0u : hi[6];
+        hi[7] = right_edge ? 0u : hi[7];
+      }
+      uint32_t h[8];
+#pragma unroll
+      for (int part = 0; part < 2; part++) {
+        const uint32_t *q = part ? hi : lo;
+        const uint32_t u34 = q[3] + q[4];
+        const uint32_t s = q[2] + u34, t = u34 + q[5];
+        h[0 + part] = s + q[0] + q[1] + bias;
+        h[2 + part] = s + q[1] + q[5] + bias;
+        h[4 + part] = t + q[2] + q[6] + bias;
+        h[6 + part] = t + q[6] + q[7] + bias;
+      }
       if (writer && row < out_rows) {
         const uint32_t ry = kMode == SH_BLUR_CONFIG
                                 ? 5u
@@ -367,14 +406,15 @@ Brightness make_brightness(bool enabled, int channels, int delta, int all_channe
   return br;
 }
 
-// Output rows per wave: 8 by default (measured fastest on 4096 x 4096: 31.0
-// us against 31.9 / 32.9 us for 16 / 32 rows); the STRICT_HIP_BLUR_ROWS
-// environment variable (8, 16 or 32) overrides it for tuning sweeps.
+// Output rows per wave: 16 by default, which on 4096 x 4096 makes 16 x 256 =
+// 4096 waves, one round at 4 waves per SIMD (measured 29.1 us against 31.3 us
+// with 8 rows, two rounds); the STRICT_HIP_BLUR_ROWS environment variable
+// (8, 16 or 32) overrides it for tuning sweeps.
 int blur_rows() {
   static const int rows = [] {
     const char *e = getenv("STRICT_HIP_BLUR_ROWS");
-    const int r = e ? atoi(e) : 8;
-    return (r == 16 || r == 32) ? r : 8;
+    const int r = e ? atoi(e) : 16;
+    return (r == 8 || r == 32) ? r : 16;
   }();
   return rows;
 }
@@ -443,14 +483,14 @@ hipError_t launch_blur5_u8(hipStream_t s, const uint8_t *in, uint8_t *out, int w
     const uint32_t *in32 = reinterpret_cast<const uint32_t *>(in);
     uint32_t *out32 = reinterpret_cast<uint32_t *>(out);
     switch (blur_rows()) {
-      case 16:
-        launch_blur_stream<16>(s, in32, out32, width, height, mode, fuse, delta, all_channels);
+      case 8:
+        launch_blur_stream<8>(s, in32, out32, width, height, mode, fuse, delta, all_channels);
         break;
       case 32:
         launch_blur_stream<32>(s, in32, out32, width, height, mode, fuse, delta, all_channels);
         break;
       default:
-        launch_blur_stream<8>(s, in32, out32, width, height, mode, fuse, delta, all_channels);
+        launch_blur_stream<16>(s, in32, out32, width, height, mode, fuse, delta, all_channels);
         break;
     }
   } else {

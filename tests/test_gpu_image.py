@@ -75,7 +75,7 @@ def test_blur_config_4096_rgba(ctx, mode):
 
 BLUR_SHAPES = [(1, 1, 4), (4, 1, 4), (2, 3, 3), (5, 5, 4), (10, 10, 3), (20, 20, 3),
                (8, 37, 4), (260, 33, 4), (512, 64, 4), (300, 2, 4), (17, 9, 4), (33, 6, 1),
-               (1028, 70, 4), (64, 1, 2)]
+               (1028, 70, 4), (64, 1, 2), (264, 17, 4), (768, 18, 4)]
 
 
 @pytest.mark.parametrize("w,h,c", BLUR_SHAPES)
