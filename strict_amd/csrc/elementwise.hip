@@ -21,6 +21,14 @@ constexpr int kBlock = 256;
 constexpr int kUnroll = 4;
 constexpr size_t kPerBlock = (size_t)kBlock * kUnroll;  // f32x4 units per block
 
+// Whether this block's kPerBlock vectors all lie below n (block-uniform).
+// Full blocks take a path without per-vector bounds checks: a load under a
+// divergent check leaves its register pending at the join, and the compiler
+// then waited for each load before issuing the next.
+__device__ __forceinline__ bool full_block(size_t n) {
+  return ((size_t)blockIdx.x + 1) * kPerBlock <= n;
+}
+
 struct AddOp { __device__ float operator()(float a, float b) const { return a + b; } };
 struct SubOp { __device__ float operator()(float a, float b) const { return a - b; } };
 struct MulOp { __device__ float operator()(float a, float b) const { return a * b; } };
@@ -64,15 +72,23 @@ __global__ __launch_bounds__(kBlock) void unary_kernel(const float *__restrict__
   f32x4 *y4 = reinterpret_cast<f32x4 *>(y);
   const size_t base = (size_t)blockIdx.x * kPerBlock + threadIdx.x;
   f32x4 v[kUnroll];
+  if (full_block(n4)) {
 #pragma unroll
-  for (int u = 0; u < kUnroll; u++) {
-    size_t i = base + (size_t)u * kBlock;
-    if (i < n4) v[u] = __builtin_nontemporal_load(x4 + i);
-  }
+    for (int u = 0; u < kUnroll; u++) v[u] = __builtin_nontemporal_load(x4 + base + (size_t)u * kBlock);
 #pragma unroll
-  for (int u = 0; u < kUnroll; u++) {
-    size_t i = base + (size_t)u * kBlock;
-    if (i < n4) __builtin_nontemporal_store(apply(op, v[u]), y4 + i);
+    for (int u = 0; u < kUnroll; u++)
+      __builtin_nontemporal_store(apply(op, v[u]), y4 + base + (size_t)u * kBlock);
+  } else {
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+      size_t i = base + (size_t)u * kBlock;
+      if (i < n4) v[u] = __builtin_nontemporal_load(x4 + i);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+      size_t i = base + (size_t)u * kBlock;
+      if (i < n4) __builtin_nontemporal_store(apply(op, v[u]), y4 + i);
+    }
   }
   // scalar tail (n % 4 elements) in block 0
   if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
@@ -91,18 +107,29 @@ __global__ __launch_bounds__(kBlock) void binary_kernel(const float *__restrict_
   f32x4 *o4 = reinterpret_cast<f32x4 *>(out);
   const size_t base = (size_t)blockIdx.x * kPerBlock + threadIdx.x;
   f32x4 va[kUnroll], vb[kUnroll];
+  if (full_block(n4)) {
 #pragma unroll
-  for (int u = 0; u < kUnroll; u++) {
-    size_t i = base + (size_t)u * kBlock;
-    if (i < n4) {
-      va[u] = __builtin_nontemporal_load(a4 + i);
-      vb[u] = __builtin_nontemporal_load(b4 + i);
+    for (int u = 0; u < kUnroll; u++) {
+      va[u] = __builtin_nontemporal_load(a4 + base + (size_t)u * kBlock);
+      vb[u] = __builtin_nontemporal_load(b4 + base + (size_t)u * kBlock);
     }
-  }
 #pragma unroll
-  for (int u = 0; u < kUnroll; u++) {
-    size_t i = base + (size_t)u * kBlock;
-    if (i < n4) __builtin_nontemporal_store(apply2(op, va[u], vb[u]), o4 + i);
+    for (int u = 0; u < kUnroll; u++)
+      __builtin_nontemporal_store(apply2(op, va[u], vb[u]), o4 + base + (size_t)u * kBlock);
+  } else {
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+      size_t i = base + (size_t)u * kBlock;
+      if (i < n4) {
+        va[u] = __builtin_nontemporal_load(a4 + i);
+        vb[u] = __builtin_nontemporal_load(b4 + i);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+      size_t i = base + (size_t)u * kBlock;
+      if (i < n4) __builtin_nontemporal_store(apply2(op, va[u], vb[u]), o4 + i);
+    }
   }
   if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
     size_t i = n4 * 4 + threadIdx.x;
@@ -146,15 +173,22 @@ __global__ __launch_bounds__(kBlock) void copy_vec_kernel(const u32x4 *__restric
                                                            size_t bytes) {
   const size_t base = (size_t)blockIdx.x * kPerBlock + threadIdx.x;
   u32x4 v[kUnroll];
+  if (full_block(n16)) {
 #pragma unroll
-  for (int u = 0; u < kUnroll; u++) {
-    size_t i = base + (size_t)u * kBlock;
-    if (i < n16) v[u] = __builtin_nontemporal_load(src + i);
-  }
+    for (int u = 0; u < kUnroll; u++) v[u] = __builtin_nontemporal_load(src + base + (size_t)u * kBlock);
 #pragma unroll
-  for (int u = 0; u < kUnroll; u++) {
-    size_t i = base + (size_t)u * kBlock;
-    if (i < n16) __builtin_nontemporal_store(v[u], dst + i);
+    for (int u = 0; u < kUnroll; u++) __builtin_nontemporal_store(v[u], dst + base + (size_t)u * kBlock);
+  } else {
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+      size_t i = base + (size_t)u * kBlock;
+      if (i < n16) v[u] = __builtin_nontemporal_load(src + i);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+      size_t i = base + (size_t)u * kBlock;
+      if (i < n16) __builtin_nontemporal_store(v[u], dst + i);
+    }
   }
   if (blockIdx.x == 0 && threadIdx.x < (bytes & 15)) {
     size_t i = n16 * 16 + threadIdx.x;

@@ -43,15 +43,25 @@ __global__ __launch_bounds__(kBlock) void brightness_vec_kernel(const uint8_t *i
   u32x4 *out4 = reinterpret_cast<u32x4 *>(out);
   const size_t base = (size_t)blockIdx.x * kBlock * kBrUnroll + threadIdx.x;
   u32x4 v[kBrUnroll];
+  // full blocks without per-vector bounds checks (a load under a divergent
+  // check can make the compiler wait for it before the next one)
+  if (((size_t)blockIdx.x + 1) * kBlock * kBrUnroll <= n16) {
 #pragma unroll
-  for (int u = 0; u < kBrUnroll; u++) {
-    size_t i = base + (size_t)u * kBlock;
-    if (i < n16) v[u] = __builtin_nontemporal_load(in4 + i);
-  }
+    for (int u = 0; u < kBrUnroll; u++) v[u] = __builtin_nontemporal_load(in4 + base + (size_t)u * kBlock);
 #pragma unroll
-  for (int u = 0; u < kBrUnroll; u++) {
-    size_t i = base + (size_t)u * kBlock;
-    if (i < n16) __builtin_nontemporal_store(brighten16(v[u], mag, negative != 0, mask), out4 + i);
+    for (int u = 0; u < kBrUnroll; u++)
+      __builtin_nontemporal_store(brighten16(v[u], mag, negative != 0, mask), out4 + base + (size_t)u * kBlock);
+  } else {
+#pragma unroll
+    for (int u = 0; u < kBrUnroll; u++) {
+      size_t i = base + (size_t)u * kBlock;
+      if (i < n16) v[u] = __builtin_nontemporal_load(in4 + i);
+    }
+#pragma unroll
+    for (int u = 0; u < kBrUnroll; u++) {
+      size_t i = base + (size_t)u * kBlock;
+      if (i < n16) __builtin_nontemporal_store(brighten16(v[u], mag, negative != 0, mask), out4 + i);
+    }
   }
   // byte tail; the 16-byte units start on pixel boundaries when channels == 4,
   // and for channels < 4 every byte is adjusted, so the mask byte index is i % 4.
