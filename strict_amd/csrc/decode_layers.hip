@@ -6,7 +6,7 @@
 // Work per layer, as items spread over the workgroups:
 //   A  QKV     one 16-row tile of W_qkv each      (RMSNorm of x in every item)
 //   B  attn    one (row, KV head, split) each      (q/k norm, RoPE, cache append)
-//   M  merge   one (row, query head) each          (combines the split partials)
+//   M  merge   one (row, query head, dim quarter) (combines the split partials)
 //   C  O       one 16-row tile of W_o each         (x_mid = x + W_o attn)
 //   D  gate/up one gate tile + up tile pair each   (RMSNorm of x_mid, SwiGLU)
 //   E  down    one 16-row tile of W_down each      (x = x_mid + W_down act)
@@ -84,12 +84,6 @@ struct LayerG {
   const SH_GLOBAL float *norm1, *norm2, *q_norm, *k_norm;
   SH_GLOBAL uint16_t *kcache, *vcache;
 };
-
-__device__ __forceinline__ LayerG layer_g(const LayerPtrs &p) {
-  return LayerG{gbl(p.wqkv),   gbl(p.wo),     gbl(p.wup),    gbl(p.wdown), gbl(p.sqkv),
-                gbl(p.so),     gbl(p.sup),    gbl(p.sdown),  gbl(p.norm1), gbl(p.norm2),
-                gbl(p.q_norm), gbl(p.k_norm), gbl(p.kcache), gbl(p.vcache)};
-}
 
 // Layer l's pointers, read from the table with scalar loads.
 __device__ __forceinline__ LayerG layer_g(const LayersArgs &a, int l) {
@@ -679,10 +673,15 @@ struct AttnLds {
 };
 
 // LDS of a merge item.
+// Merge items per (row, query head). Measured at batch 1: 4 parts +1.6 %
+// tokens/s over 1 part (each item polls a quarter of the partials); 8 parts
+// -3.7 % against 4.
+constexpr int kMergeParts = 4;
+
 struct MergeLds {
   float m[kMaxSplits], l[kMaxSplits], w[kMaxSplits];
   float lsum;
-  float acc[4][64][2];
+  float acc[kT][2];  // [split group][column pair]
 };
 
 // K and V^T registers of one block (the first block of an item is
@@ -952,29 +951,36 @@ __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, 
 // pair t % 64 of splits t / 64, t / 64 + 4, ...; threads t < active also
 // fetch split t's (m, l).
 template <int kSP>
-__device__ __forceinline__ bool merge_item(const LayersArgs &a, int l, int item, unsigned ep, uint8_t *smem,
-                           Misc *misc) {
-  static_assert(kSP % 4 == 0 && kSP <= kMaxSplits, "splits per merge");
-  constexpr int kPer = kSP / 4;
+__device__ __forceinline__ bool merge_item(const LayersArgs &a, int l, int item, unsigned ep,
+                                           uint8_t *smem, Misc *misc) {
+  // item = (row, head, part): dims [32 part, 32 part + 32) of one head, so a
+  // head's merge is spread over kMergeParts workgroups (each polls a quarter
+  // of the head's partials)
+  constexpr int kPairs = kD / kMergeParts / 2;  // column pairs per item
+  constexpr int kGroups = kT / kPairs;           // split groups
+  static_assert(kSP % kGroups == 0 && kSP <= kMaxSplits && kSP <= 64, "splits per merge");
+  constexpr int kPer = kSP / kGroups;  // splits per thread
   MergeLds &S = *reinterpret_cast<MergeLds *>(smem);
-  const int h = item % a.heads, b = item / a.heads;
-  const int t = threadIdx.x, q = t & 63, sg = t >> 6;
+  const int part = item % kMergeParts, hb = item / kMergeParts;
+  const int h = hb % a.heads, b = hb / a.heads;
+  const int t = threadIdx.x, q = t % kPairs, sg = t / kPairs;
   const int L = cnst(a.pos)[b] + 1;
   const int active = min((L + a.chunk - 1) / a.chunk, a.splits);
   const size_t base = ((size_t)b * a.heads + h) * a.splits * kPStride;
+  const int col = kD / kMergeParts * part + 2 * q;  // this thread's column pair
   const unsigned tag = tag_of(ep, l);
-  // cells k < 2 kPer: column pair q of split sg + 4 (k / 2); the last two:
+  // cells k < 2 kPer: column pair q of split sg + kGroups (k / 2); the last two:
   // (m, l) of split t
   uint64_t mask = (t < active) ? 3ull << (2 * kPer) : 0ull;
 #pragma unroll
   for (int k = 0; k < kPer; k++)
-    if (sg + 4 * k < active) mask |= 3ull << (2 * k);
+    if (sg + kGroups * k < active) mask |= 3ull << (2 * k);
   uint64_t cv[2 * kPer + 2];
   const bool ok = spin_cells(a, a.partc,
                              [&](int k) {
                                return k < 2 * kPer
-                                          ? base + (size_t)min(sg + 4 * (k / 2), active - 1) * kPStride +
-                                                2 * q + (k & 1)
+                                          ? base + (size_t)min(sg + kGroups * (k / 2), active - 1) * kPStride +
+                                                col + (k & 1)
                                           : base + (size_t)min(t, active - 1) * kPStride + kD + (k & 1);
                              },
                              mask, tag, cv);
@@ -998,21 +1004,25 @@ __device__ __forceinline__ bool merge_item(const LayersArgs &a, int l, int item,
   float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
   for (int k = 0; k < kPer; k++) {
-    const int j = sg + 4 * k;
+    const int j = sg + kGroups * k;
     const float wj = S.w[j];  // 0 past active (the cells there repeat a valid split)
     s0 += wj * cell_f32(cv[2 * k]);
     s1 += wj * cell_f32(cv[2 * k + 1]);
   }
-  S.acc[sg][q][0] = s0;
-  S.acc[sg][q][1] = s1;
+  S.acc[t][0] = s0;  // t = sg * kPairs + q
+  S.acc[t][1] = s1;
   lds_barrier();
-  if (t < 64) {
+  if (t < kPairs) {
     const float inv = 1.0f / S.lsum;
-    const float v0 = (S.acc[0][q][0] + S.acc[1][q][0]) + (S.acc[2][q][0] + S.acc[3][q][0]);
-    const float v1 = (S.acc[0][q][1] + S.acc[1][q][1]) + (S.acc[2][q][1] + S.acc[3][q][1]);
+    float v0 = 0.0f, v1 = 0.0f;
+#pragma unroll
+    for (int g = 0; g < kGroups; g++) {
+      v0 += S.acc[g * kPairs + q][0];
+      v1 += S.acc[g * kPairs + q][1];
+    }
     const uint32_t packed = (uint32_t)f32_to_f16_bits(v0 * inv) |
                             ((uint32_t)f32_to_f16_bits(v1 * inv) << 16);
-    cst1(a.attnc, (size_t)(b * a.heads + h) * (kD / 2) + q, packed, tag);
+    cst1(a.attnc, (size_t)(b * a.heads + h) * (kD / 2) + col / 2, packed, tag);
   }
   SH_MARK(misc, l, 15);
   lds_barrier();  // the next item reuses the LDS
@@ -1058,7 +1068,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
   lds_barrier();
   const unsigned ep = *cnst(a.epoch);
   const int G = gridDim.x, w = blockIdx.x;
-  const int nA = a.qkv_n / 16, nB = B * a.kv_heads * a.splits, nM = B * a.heads;
+  const int nA = a.qkv_n / 16, nB = B * a.kv_heads * a.splits, nM = B * a.heads * kMergeParts;
   const int nC = H / 16, nD = a.inter / 16, nE = H / 16;
   const int d0 = (w + G - nC % G) % G;  // this workgroup's first gate/up item
   const int m0 = G - 1 - w;             // its first merge item
@@ -1169,7 +1179,8 @@ const void *kernel_for(const Shape &s, int batch, bool one, int *max_splits) {
 // Every phase of a launch with `grid` workgroups has at most one item per
 // workgroup.
 bool one_item_each(const LayersArgs &a, int grid) {
-  const int n[] = {a.qkv_n / 16, a.B * a.kv_heads * a.splits, a.B * a.heads, a.H / 16, a.inter / 16};
+  const int n[] = {a.qkv_n / 16, a.B * a.kv_heads * a.splits, a.B * a.heads * kMergeParts, a.H / 16,
+                   a.inter / 16};
   for (int k : n)
     if (k > grid) return false;
   return true;
