@@ -327,7 +327,7 @@ def gemv_kernel(ctx, rng, steps):
 
 def decode_run(ctx, cfg, batch, prompt_len, steps, warmup, seed=42):
     """Prefill `prompt_len` random tokens per sequence, then time `steps`
-    greedy decode steps (graph replays). Returns (ms_per_step, context_avg)."""
+    greedy decode steps, enqueued back to back. Returns (ms_per_step, context_avg)."""
     from strict_amd import llm
 
     m = llm.Model(ctx, cfg)
@@ -485,8 +485,8 @@ def main() -> int:
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                     "traffic": read_traffic("qwen3_decode_step"),
-                    "kernel": "decode step: HIP-graph replay of embed, decode_layers_kernel (all 28 "
-                              "layers in one persistent launch), final RMSNorm, LM-head GEMV"}
+                    "kernel": "decode step: embed, decode_layers_kernel (all 28 layers in one "
+                              "persistent cooperative launch), final RMSNorm, LM-head GEMV"}
         log(f"headline: {value:.1f} tokens/s, {achieved:.1f} GB/s algorithmic")
         if not args.no_extra:
             for b, st in ((4, 32), (16, 16)):

@@ -4,8 +4,10 @@
 //                       norm+up GEMV (SwiGLU / GELU), down GEMV + residual]
 //         -> final norm + LM head GEMV with argmax
 // on the context's stream. Every per-step quantity (tokens, positions, argmax
-// keys) lives in device memory, so a step is captured once per batch size as
-// a HIP graph and replayed.
+// keys) lives in device memory, so a step of the per-op path is captured once
+// per batch size as a HIP graph and replayed. With the decode-layers kernel
+// (a cooperative launch, which stream capture does not take) a step is four
+// eager launches: embed, the layers kernel, final norm, LM head.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
