@@ -10,6 +10,8 @@
 //   C  O       one 16-row tile of W_o each         (x_mid = x + W_o attn)
 //   D  gate/up one gate tile + up tile pair each   (RMSNorm of x_mid, SwiGLU)
 //   E  down    one 16-row tile of W_down each      (x = x_mid + W_down act)
+// and, on steps with logits, after the last layer:
+//   H  head    16-row tiles of the LM head          (final RMSNorm, logits, argmax)
 //
 // Exchange between workgroups: every value an item hands on travels in an
 // 8-byte cell of device memory, payload in the low word and the
@@ -637,8 +639,10 @@ __device__ __forceinline__ bool down_item(const LayersArgs &a, const LayerG &P, 
       const int b = 4 * (lane >> 4) + r;
       const float v = rv[r] + acc[0][r] * sc;
       if (b < a.B) {
+        // the last layer also writes the plain buffer the separate final
+        // norm reads (steps whose LM head runs outside this kernel)
         if (last) gbl(a.x_in)[(size_t)b * a.H + i * 16 + col] = v;
-        else cst1(a.x0c, (size_t)b * a.H + i * 16 + col, bits_of(v), tag);
+        cst1(a.x0c, (size_t)b * a.H + i * 16 + col, bits_of(v), tag);
       }
     }
   }
@@ -1031,6 +1035,85 @@ __device__ __forceinline__ bool merge_item(const LayersArgs &a, int l, int item,
 
 // ---- the kernel ----------------------------------------------------------------
 
+// H (steps with logits): logits[b][n] = head_scale[n] * (W_head
+// RMSNorm(x; final_g))[b][n] for the 16-row tiles j = w, w + G, .. of this
+// workgroup, each wave taking every fourth of them over the whole K (kLH
+// 16-byte loads per lane and tile), the next tile's weights requested while
+// the current one is multiplied; the running argmax keys go to keys[b]
+// (read first, atomicMax only when larger).
+template <int kLA, int kRows>
+__device__ __forceinline__ bool head_phase(const LayersArgs &a, unsigned ep, const Lds &s) {
+  constexpr int kLH = 4 * kLA;  // K / 64
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, G = gridDim.x, w = blockIdx.x;
+  const int nT = a.head_tiles, H = a.H, B = a.B;
+  const SH_GLOBAL uint8_t *W = gbl(a.head_w);
+  const int first = w + G * wave, step = 4 * G;
+  u32x4 wb[2][kLH];
+  float sc[2];
+  auto load_tile = [&](u32x4 (&dst)[kLH], float &scale, int j) {
+    const int jj = min(j, nT - 1);  // past the end: the last tile again, never used
+#pragma unroll
+    for (int u = 0; u < kLH; u++)
+      dst[u] = __builtin_nontemporal_load(reinterpret_cast<const SH_GLOBAL u32x4 *>(
+          W + ((size_t)jj * kLH + u) * 1024 + (size_t)lane * 16));
+    scale = gbl(a.head_scale)[jj * 16 + (lane & 15)];
+  };
+  if (first < nT) load_tile(wb[0], sc[0], first);
+  __builtin_amdgcn_sched_barrier(0);
+  if (!stage_rms<(kLA + 3) / 4, kRows>(a, a.x0c, nullptr, tag_of(ep, a.n_layers - 1), gbl(a.final_g),
+                                       H, s.xs, s.misc))
+    return false;
+  const int arow = lane & 15, acol = 8 * (lane >> 4);
+  const _Float16 *xrow = s.xs + (arow < B ? arow : 0) * (H + 8) + acol;
+  unsigned long long best[4] = {0, 0, 0, 0};
+  auto tile = [&](const u32x4 (&wt)[kLH], float scale, int j) {
+    constexpr int kCh = 4;
+    f32x4 part[kCh];
+#pragma unroll
+    for (int c = 0; c < kCh; c++) part[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kLH; u++)
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const f16x8 af = *reinterpret_cast<const f16x8 *>(xrow + u * 64 + 32 * h);
+        part[(2 * u + h) % kCh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            af, e4m3x8_to_f16(wt[u][2 * h], wt[u][2 * h + 1]), part[(2 * u + h) % kCh], 0, 0, 0);
+      }
+    const f32x4 acc = (part[0] + part[1]) + (part[2] + part[3]);
+    const int n = j * 16 + (lane & 15);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int b = 4 * (lane >> 4) + r;
+      if (b < B && n < a.n_valid) {
+        const float v = acc[r] * scale;
+        gbl(a.logits)[(size_t)b * a.logits_ld + n] = v;
+        const unsigned long long key = argmax_key(v, n);
+        best[r] = key > best[r] ? key : best[r];
+      }
+    }
+  };
+  for (int j = first; j < nT; j += 2 * step) {
+    load_tile(wb[1], sc[1], j + step);
+    tile(wb[0], sc[0], j);
+    load_tile(wb[0], sc[0], j + 2 * step);
+    if (j + step < nT) tile(wb[1], sc[1], j + step);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    unsigned long long k = best[r];
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) {
+      const unsigned long long o = __shfl_xor(k, off, 64);
+      k = o > k ? o : k;
+    }
+    const int b = 4 * (lane >> 4) + r;
+    if ((lane & 15) == 0 && b < B && k != 0 &&
+        k > __hip_atomic_load(a.keys + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+      atomicMax(a.keys + b, k);
+  }
+  return true;
+}
+
 // Runs f(i) for this workgroup's items i = first, first + G, .. < n. With
 // kOne the host has checked that every phase has at most G items, so there
 // is at most one: no loop, whose preheader would make the compiler wait for
@@ -1134,6 +1217,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
       return;
     if (hasC && next && w < nA) load_weights<kLA, 1>(wa, layer_g(a, l + 1).wqkv, H, w);
   }
+  if (a.head_on && !head_phase<kLA, kRows>(a, ep, lds)) return;
 #ifdef SH_DECODE_TRACE
   lds_barrier();
   if (w < kTraceWgs)

@@ -113,6 +113,16 @@ struct LayersArgs {
   unsigned *err = nullptr;             // set when a wait timed out (sticky)
   unsigned long long spin_ticks = 0;   // wall-clock ticks a wait may take
   int lds_misc = 0;                    // byte offset of the small LDS scratch words
+  // final RMSNorm + LM head inside the kernel (steps with logits; head_on 0:
+  // the kernel ends with the last layer)
+  int head_on = 0;
+  const uint8_t *head_w = nullptr;     // FP8 tiled [head_tiles * 16][H]
+  const float *head_scale = nullptr;   // per row
+  const float *final_g = nullptr;      // final RMSNorm gains [H]
+  int head_tiles = 0, n_valid = 0;     // 16-row tiles; columns that are real tokens
+  float *logits = nullptr;             // [B][logits_ld]
+  int logits_ld = 0;
+  unsigned long long *keys = nullptr;  // [B] greedy argmax keys (zeroed by the embed kernel)
 };
 
 // Model shapes the kernel is instantiated for (16-byte weight loads per lane

@@ -80,6 +80,7 @@ struct sh_llm {
   // persistent decode-layers kernel (Qwen3 shapes it is built for;
   // STRICT_HIP_LLM_LAYERS=0 keeps the per-op kernels)
   bool layers_kernel = false;
+  bool head_in_layers = false;  // final norm + LM head inside the layers kernel
   LayersArgs la{};
   int layers_grid = 0;
   size_t layers_lds = 0;
@@ -175,7 +176,10 @@ int enqueue_step(sh_llm *m, bool logits) {
   if (m->layers_kernel) e.epoch = m->epoch;
   SH_HIP_TRY(launch_embed(s, e, B));
 
-  if (m->layers_kernel) SH_HIP_TRY(launch_decode_layers(s, m->la, m->layers_grid, m->layers_lds));
+  if (m->layers_kernel) {
+    m->la.head_on = logits && m->head_in_layers ? 1 : 0;
+    SH_HIP_TRY(launch_decode_layers(s, m->la, m->layers_grid, m->layers_lds));
+  }
   for (Layer &L : m->layers) {
     if (m->layers_kernel) break;  // every layer ran in the kernel above
     GemvArgs g;
@@ -259,7 +263,7 @@ int enqueue_step(sh_llm *m, bool logits) {
     SH_HIP_TRY(launch_gemv(s, dn, m->wtype, kProNone, kEpiResidual, 0));
   }
 
-  if (logits) {
+  if (logits && !(m->layers_kernel && m->head_in_layers)) {
     GemvArgs nrm;
     nrm.x = x_final;
     nrm.x_ld = H;
@@ -351,6 +355,18 @@ int setup_layers_kernel(sh_llm *m) {
   SH_HIP_TRY(hipStreamSynchronize(stream_of(m->ctx)));
   a.layers = dl;
   a.epoch = m->epoch;
+  // the final norm and LM head run inside the kernel on steps with logits
+  // (STRICT_HIP_LLM_HEAD=0: separate kernels, as the per-op path)
+  const char *he = getenv("STRICT_HIP_LLM_HEAD");
+  m->head_in_layers = !(he && he[0] == '0');
+  a.head_w = m->head.w;
+  a.head_scale = m->head.scale;
+  a.final_g = m->final_g;
+  a.head_tiles = m->head.N / 16;
+  a.n_valid = c.vocab;
+  a.logits = m->logits;
+  a.logits_ld = m->vocab_pad;
+  a.keys = m->keys;
   m->layers_grid = cus;
   m->layers_kernel = true;
   return SH_OK;

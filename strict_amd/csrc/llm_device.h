@@ -76,6 +76,14 @@ __device__ __forceinline__ float wave_max_rows(float v) {
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 
+// Order-preserving key of an fp32 logit with its column: larger logits give
+// larger keys; among equal logits the smaller column wins (as argmax does).
+__device__ __forceinline__ unsigned long long argmax_key(float v, int n) {
+  uint32_t u = __builtin_bit_cast(uint32_t, v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)n);
+}
+
 __device__ __forceinline__ float gelu_tanh(float x) {
   const float c = 0.7978845608028654f;  // sqrt(2 / pi)
   return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));

@@ -256,14 +256,6 @@ struct Stager {
   }
 };
 
-// Order-preserving key of an fp32 logit with its column: larger logits give
-// larger keys; among equal logits the smaller column wins (as argmax does).
-__device__ __forceinline__ unsigned long long argmax_key(float v, int n) {
-  uint32_t u = __builtin_bit_cast(uint32_t, v);
-  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)n);
-}
-
 // A workgroup handles kNT row tiles (two for the gate/up pair) at a time,
 // grid-striding over tile groups; its 4 waves split K in four and the partial
 // 16x16 accumulators are summed in LDS, wave 0 running the epilogue.
