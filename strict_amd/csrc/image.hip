@@ -200,8 +200,11 @@ __device__ __forceinline__ void expand_row(const u32x4 v, int y, int height, uin
 }
 
 // Input rows y0 - 2 .. y0 + kR + 1 are loaded once per wave (kR + 4 loads
-// for kR output rows; the halo rows are shared with the neighbouring bands
-// through L2), each 5 steps before its use.
+// for kR output rows), each 5 steps before its use. The halo rows are shared
+// with the neighbouring bands through L2: odd bands sweep upwards, so two
+// neighbours reach their shared rows together (both at the start or both at
+// the end of the sweep; a band's bottom halo read at the end of a downward
+// sweep would be long evicted from L2 by the time the band below started).
 template <int kMode, int kFuse, int kR>
 __global__ __launch_bounds__(kBlock) void blur_rgba_rows_kernel(const StreamArgs a) {
   constexpr int kQ = 10;
@@ -220,6 +223,9 @@ __global__ __launch_bounds__(kBlock) void blur_rgba_rows_kernel(const StreamArgs
   // halo pixels: lane 0 the two left of the strip, lane 63 the two right of it
   const int hx = lane == 0 ? max(x0 - 2, 0) : min(x0 + kStripPx, a.width - 2);
   const int y0 = band * kR;
+  // load j of the sweep reads row ys + dy * j
+  const int dy = (band & 1) ? -1 : 1;
+  const int ys = (band & 1) ? y0 + kR + 1 : y0 - 2;
   const bool writer = cx < a.width;
   const int out_rows = min(kR, a.height - y0);
 
@@ -262,35 +268,36 @@ __global__ __launch_bounds__(kBlock) void blur_rgba_rows_kernel(const StreamArgs
   u32x2 hraw[kQ];
 #pragma unroll
   for (int i = 0; i < 5; i++) {
-    raw[i] = load_row<kMode>(a, y0 - 2 + i, lx);
-    hraw[i] = load_halo(y0 - 2 + i);
+    raw[i] = load_row<kMode>(a, ys + dy * i, lx);
+    hraw[i] = load_halo(ys + dy * i);
   }
 #pragma unroll
   for (int i = 0; i < kR + 4; i++) {
     if (i >= 5) {
       uint32_t e[8], eh[4];
-      expand_row<kMode, kFuse>(raw[(i - 5) % kQ], y0 - 7 + i, a.height, e, a.d_lo, a.d_hi);
-      expand_halo(hraw[(i - 5) % kQ], y0 - 7 + i, eh);
+      expand_row<kMode, kFuse>(raw[(i - 5) % kQ], ys + dy * (i - 5), a.height, e, a.d_lo,
+                               a.d_hi);
+      expand_halo(hraw[(i - 5) % kQ], ys + dy * (i - 5), eh);
 #pragma unroll
       for (int k = 0; k < 8; k++) vs[k] -= e[k];
 #pragma unroll
       for (int k = 0; k < 4; k++) hs[k] -= eh[k];
     }
     if (i + 5 < kR + 4) {
-      raw[(i + 5) % kQ] = load_row<kMode>(a, y0 + 3 + i, lx);
-      hraw[(i + 5) % kQ] = load_halo(y0 + 3 + i);
+      raw[(i + 5) % kQ] = load_row<kMode>(a, ys + dy * (i + 5), lx);
+      hraw[(i + 5) % kQ] = load_halo(ys + dy * (i + 5));
     }
     {
       uint32_t e[8], eh[4];
-      expand_row<kMode, kFuse>(raw[i % kQ], y0 - 2 + i, a.height, e, a.d_lo, a.d_hi);
-      expand_halo(hraw[i % kQ], y0 - 2 + i, eh);
+      expand_row<kMode, kFuse>(raw[i % kQ], ys + dy * i, a.height, e, a.d_lo, a.d_hi);
+      expand_halo(hraw[i % kQ], ys + dy * i, eh);
 #pragma unroll
       for (int k = 0; k < 8; k++) vs[k] += e[k];
 #pragma unroll
       for (int k = 0; k < 4; k++) hs[k] += eh[k];
     }
     if (i >= 4) {
-      const int row = i - 4, y = y0 + row;
+      const int y = ys + dy * (i - 2), row = y - y0;  // the window's centre row
       // columns cx-2, cx-1 and cx+4, cx+5: neighbours' sums, the halo sums
       // at the strip's ends, the edge rule at the image's
       uint32_t lo[8], hi[8];
