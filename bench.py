@@ -485,8 +485,9 @@ def main() -> int:
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                     "traffic": read_traffic("qwen3_decode_step"),
-                    "kernel": "decode step: embed, decode_layers_kernel (all 28 layers in one "
-                              "persistent cooperative launch), final RMSNorm, LM-head GEMV"}
+                    "kernel": "decode step: embed, then decode_layers_kernel (all 28 layers, "
+                              "final RMSNorm and LM head with greedy argmax in one persistent "
+                              "cooperative launch)"}
         log(f"headline: {value:.1f} tokens/s, {achieved:.1f} GB/s algorithmic")
         if not args.no_extra:
             for b, st in ((4, 32), (16, 16)):

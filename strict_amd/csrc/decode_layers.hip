@@ -1,6 +1,6 @@
 // Persistent decode-layers kernel: all decoder layers of one Qwen3 decode
-// step (FP8 weights, head_dim 128) in one cooperative launch, one workgroup
-// per CU. It replaces the six kernels per layer of the per-op path (norm +
+// step (FP8 weights, head_dim 128) in one launch, one workgroup per CU, all
+// resident together. It replaces the six kernels per layer of the per-op path (norm +
 // QKV GEMV, attention, split merge, O GEMV, norm + gate/up GEMV, down GEMV).
 //
 // Work per layer, as items spread over the workgroups:
@@ -1328,11 +1328,13 @@ hipError_t decode_layers_trace(void *dst, size_t bytes) {
 }
 #endif
 
-hipError_t launch_decode_layers(hipStream_t s, const LayersArgs &a, int grid, size_t lds) {
+hipError_t launch_decode_layers(hipStream_t s, const LayersArgs &a, int grid, size_t lds,
+                                bool cooperative) {
   const void *k = kernel_for(shape_of(a.H, a.heads, a.kv_heads, a.inter), a.B, one_item_each(a, grid), nullptr);
   if (!k) return hipErrorInvalidValue;
   void *args[] = {const_cast<LayersArgs *>(&a)};
-  return hipLaunchCooperativeKernel(k, dim3(grid), dim3(kT), args, (unsigned)lds, s);
+  if (cooperative) return hipLaunchCooperativeKernel(k, dim3(grid), dim3(kT), args, (unsigned)lds, s);
+  return hipLaunchKernel(k, dim3(grid), dim3(kT), args, (unsigned)lds, s);
 }
 
 }  // namespace sh

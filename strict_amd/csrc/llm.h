@@ -140,8 +140,16 @@ hipError_t decode_layers_occupancy(const LayersArgs &a, size_t lds, int *blocks_
 // Diagnostic builds: copies the last step's phase timeline to the host.
 hipError_t decode_layers_trace(void *dst, size_t bytes);
 #endif
-// Cooperative launch (all `grid` workgroups resident together) on stream s.
-hipError_t launch_decode_layers(hipStream_t s, const LayersArgs &a, int grid, size_t lds);
+// Launch on stream s. The kernel needs all `grid` workgroups resident
+// together. cooperative: HIP's cooperative launch, which guarantees it (and
+// runs on a queue of its own, ~11 us to switch to and from it, ~20 us between
+// two cooperative launches). Otherwise an ordinary launch: grid is at most one
+// workgroup per CU of an occupancy >= 1 and stream order has drained this
+// stream's earlier work, so the workgroups are resident together unless other
+// streams or processes hold the CUs; then a wait times out, sets `err`, every
+// later wait gives up at once and the kernel ends with the step reported failed.
+hipError_t launch_decode_layers(hipStream_t s, const LayersArgs &a, int grid, size_t lds,
+                                bool cooperative);
 
 // Lets every GEMV instantiation use up to 160 KiB of dynamic LDS (current device).
 hipError_t prepare_gemv_kernels();

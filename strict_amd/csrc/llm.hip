@@ -6,8 +6,9 @@
 // on the context's stream. Every per-step quantity (tokens, positions, argmax
 // keys) lives in device memory, so a step of the per-op path is captured once
 // per batch size as a HIP graph and replayed. With the decode-layers kernel
-// (a cooperative launch, which stream capture does not take) a step is four
-// eager launches: embed, the layers kernel, final norm, LM head.
+// a step is two eager launches, embed and the layers kernel, which also runs
+// the final norm and LM head (not captured: with STRICT_HIP_LLM_COOP=1 the
+// layers kernel is a cooperative launch, which stream capture does not take).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -81,6 +82,7 @@ struct sh_llm {
   // STRICT_HIP_LLM_LAYERS=0 keeps the per-op kernels)
   bool layers_kernel = false;
   bool head_in_layers = false;  // final norm + LM head inside the layers kernel
+  bool coop_layers = false;     // cooperative launch of the layers kernel
   LayersArgs la{};
   int layers_grid = 0;
   size_t layers_lds = 0;
@@ -178,7 +180,7 @@ int enqueue_step(sh_llm *m, bool logits) {
 
   if (m->layers_kernel) {
     m->la.head_on = logits && m->head_in_layers ? 1 : 0;
-    SH_HIP_TRY(launch_decode_layers(s, m->la, m->layers_grid, m->layers_lds));
+    SH_HIP_TRY(launch_decode_layers(s, m->la, m->layers_grid, m->layers_lds, m->coop_layers));
   }
   for (Layer &L : m->layers) {
     if (m->layers_kernel) break;  // every layer ran in the kernel above
@@ -359,6 +361,10 @@ int setup_layers_kernel(sh_llm *m) {
   // (STRICT_HIP_LLM_HEAD=0: separate kernels, as the per-op path)
   const char *he = getenv("STRICT_HIP_LLM_HEAD");
   m->head_in_layers = !(he && he[0] == '0');
+  // ordinary launches by default (back to back with the embed kernel on one
+  // queue); STRICT_HIP_LLM_COOP=1: cooperative launches
+  const char *co = getenv("STRICT_HIP_LLM_COOP");
+  m->coop_layers = co && co[0] == '1';
   a.head_w = m->head.w;
   a.head_scale = m->head.scale;
   a.final_g = m->final_g;
