@@ -487,7 +487,7 @@ def main() -> int:
                     "traffic": read_traffic("qwen3_decode_step"),
                     "kernel": "decode step: embed, then decode_layers_kernel (all 28 layers, "
                               "final RMSNorm and LM head with greedy argmax in one persistent "
-                              "cooperative launch)"}
+                              "launch)"}
         log(f"headline: {value:.1f} tokens/s, {achieved:.1f} GB/s algorithmic")
         if not args.no_extra:
             for b, st in ((4, 32), (16, 16)):
