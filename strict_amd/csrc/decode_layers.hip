@@ -683,9 +683,8 @@ struct AttnLds {
 constexpr int kMergeParts = 4;
 
 struct MergeLds {
-  float m[kMaxSplits], l[kMaxSplits], w[kMaxSplits];
-  float lsum;
-  float acc[kT][2];  // [split group][column pair]
+  float gm[kT];             // per split group: max m_j of its active splits
+  float part[4][kT][3];     // per wave: column pair's two sums and the l sum
 };
 
 // K and V^T registers of one block (the first block of an item is
@@ -948,18 +947,18 @@ __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, 
   return true;
 }
 
-// M: item = (b, query head): combines the partials of the active splits
-// (at most kSP),
+// M: item = (row, query head, part): combines the partials of the active
+// splits (at most kSP),
 //   out = sum_j exp(m_j - M) acc_j / sum_j exp(m_j - M) l_j,  M = max_j m_j,
-// and writes the head's 128 outputs as fp16 pairs. Thread t holds column
-// pair t % 64 of splits t / 64, t / 64 + 4, ...; threads t < active also
-// fetch split t's (m, l).
+// for dims [32 part, 32 part + 32) of the head (a head's merge is spread
+// over kMergeParts workgroups, each polling a quarter of the head's
+// partials), written as fp16 pairs. Thread t = (split group sg, column pair
+// q) combines its splits sg, sg + kGroups, .. against their own max M_g;
+// then each column pair rescales the groups: with M = max_g M_g,
+//   out = sum_g exp(M_g - M) S_g / sum_g exp(M_g - M) L_g.
 template <int kSP>
 __device__ __forceinline__ bool merge_item(const LayersArgs &a, int l, int item, unsigned ep,
                                            uint8_t *smem, Misc *misc) {
-  // item = (row, head, part): dims [32 part, 32 part + 32) of one head, so a
-  // head's merge is spread over kMergeParts workgroups (each polls a quarter
-  // of the head's partials)
   constexpr int kPairs = kD / kMergeParts / 2;  // column pairs per item
   constexpr int kGroups = kT / kPairs;           // split groups
   static_assert(kSP % kGroups == 0 && kSP <= kMaxSplits && kSP <= 64, "splits per merge");
@@ -973,57 +972,69 @@ __device__ __forceinline__ bool merge_item(const LayersArgs &a, int l, int item,
   const size_t base = ((size_t)b * a.heads + h) * a.splits * kPStride;
   const int col = kD / kMergeParts * part + 2 * q;  // this thread's column pair
   const unsigned tag = tag_of(ep, l);
-  // cells k < 2 kPer: column pair q of split sg + kGroups (k / 2); the last two:
-  // (m, l) of split t
-  uint64_t mask = (t < active) ? 3ull << (2 * kPer) : 0ull;
+  // cells 4 k .. 4 k + 3 of split sg + kGroups k: its two columns, then (m, l)
+  uint64_t mask = 0;
 #pragma unroll
   for (int k = 0; k < kPer; k++)
-    if (sg + kGroups * k < active) mask |= 3ull << (2 * k);
-  uint64_t cv[2 * kPer + 2];
+    if (sg + kGroups * k < active) mask |= 15ull << (4 * k);
+  uint64_t cv[4 * kPer];
   const bool ok = spin_cells(a, a.partc,
                              [&](int k) {
-                               return k < 2 * kPer
-                                          ? base + (size_t)min(sg + kGroups * (k / 2), active - 1) * kPStride +
-                                                col + (k & 1)
-                                          : base + (size_t)min(t, active - 1) * kPStride + kD + (k & 1);
+                               const int j = min(sg + kGroups * (k / 4), active - 1);
+                               return base + (size_t)j * kPStride +
+                                      ((k & 2) ? kD + (k & 1) : col + (k & 1));
                              },
                              mask, tag, cv);
   if (!waits_ok(a, ok, misc)) return false;
   SH_MARK(misc, l, 14);
-  if (t < active) {
-    S.m[t] = cell_f32(cv[2 * kPer]);
-    S.l[t] = cell_f32(cv[2 * kPer + 1]);
-  }
-  lds_barrier();
-  if (t < 64) {
-    const float mj = t < active ? S.m[t] : -INFINITY;
-    const float lj = t < active ? S.l[t] : 0.0f;
-    const float M = wave_max_rows(mj);
-    const float wj = t < active ? expf(mj - M) : 0.0f;
-    const float lw = wave_sum_rows(wj * lj);
-    S.w[t] = wj;
-    if (t == 0) S.lsum = lw;
-  }
-  lds_barrier();
-  float s0 = 0.0f, s1 = 0.0f;
+  float mg = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < kPer; k++)
+    if (sg + kGroups * k < active) mg = fmaxf(mg, cell_f32(cv[4 * k + 2]));
+  float s0 = 0.0f, s1 = 0.0f, lg = 0.0f;
 #pragma unroll
   for (int k = 0; k < kPer; k++) {
-    const int j = sg + kGroups * k;
-    const float wj = S.w[j];  // 0 past active (the cells there repeat a valid split)
-    s0 += wj * cell_f32(cv[2 * k]);
-    s1 += wj * cell_f32(cv[2 * k + 1]);
+    if (sg + kGroups * k < active) {
+      const float wj = expf(cell_f32(cv[4 * k + 2]) - mg);
+      s0 += wj * cell_f32(cv[4 * k]);
+      s1 += wj * cell_f32(cv[4 * k + 1]);
+      lg += wj * cell_f32(cv[4 * k + 3]);
+    }
   }
-  S.acc[t][0] = s0;  // t = sg * kPairs + q
-  S.acc[t][1] = s1;
+  if (q == 0) S.gm[sg] = mg;  // -inf for a group without active splits (its sums are 0)
+  lds_barrier();
+  // every thread rescales its group's sums by exp(M_g - M); the groups of a
+  // wave (sg = 4 wave .. 4 wave + 3, lanes q + 16 i) sum by lane exchanges
+  float M = -INFINITY;
+#pragma unroll
+  for (int g = 0; g < kGroups; g++) M = fmaxf(M, S.gm[g]);  // finite: split 0 is active
+  const float wg = mg == -INFINITY ? 0.0f : expf(mg - M);
+  s0 *= wg;
+  s1 *= wg;
+  lg *= wg;
+  static_assert(kPairs == 16 && kGroups == 16, "four split groups per wave");
+#pragma unroll
+  for (int off = 16; off <= 32; off <<= 1) {
+    s0 += __shfl_xor(s0, off, 64);
+    s1 += __shfl_xor(s1, off, 64);
+    lg += __shfl_xor(lg, off, 64);
+  }
+  const int wave = t >> 6;
+  if ((t & 63) < kPairs) {
+    S.part[wave][q][0] = s0;
+    S.part[wave][q][1] = s1;
+    S.part[wave][q][2] = lg;
+  }
   lds_barrier();
   if (t < kPairs) {
-    const float inv = 1.0f / S.lsum;
-    float v0 = 0.0f, v1 = 0.0f;
+    float v0 = 0.0f, v1 = 0.0f, lsum = 0.0f;
 #pragma unroll
-    for (int g = 0; g < kGroups; g++) {
-      v0 += S.acc[g * kPairs + q][0];
-      v1 += S.acc[g * kPairs + q][1];
+    for (int w4 = 0; w4 < 4; w4++) {
+      v0 += S.part[w4][q][0];
+      v1 += S.part[w4][q][1];
+      lsum += S.part[w4][q][2];
     }
+    const float inv = 1.0f / lsum;
     const uint32_t packed = (uint32_t)f32_to_f16_bits(v0 * inv) |
                             ((uint32_t)f32_to_f16_bits(v1 * inv) << 16);
     cst1(a.attnc, (size_t)(b * a.heads + h) * (kD / 2) + col / 2, packed, tag);
