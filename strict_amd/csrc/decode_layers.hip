@@ -473,12 +473,18 @@ struct Lds {
   Misc *misc;
 };
 
+// Rows per lane group of an MFMA output (acc[r] is row 4 (lane / 16) + r):
+// the batch-1 variants (kRows == 1) only ever have row 0.
+template <int kRows>
+constexpr int kOutRows = kRows == 1 ? 1 : 4;
+
 // Requests x[b][col] of the four batch rows b = 4 (lane / 16) + r this
 // lane's accumulator holds (used in wave 0): the cells (checked by
 // finish_residual), and for the first layer's O item the plain input xp.
 // Every thread loads its cells, without a branch: a load under a branch
 // made the compiler wait for all outstanding requests (the item's weights)
 // before the poll that follows.
+template <int kR>
 __device__ __forceinline__ void request_residual(const LayersArgs &a, const uint64_t *xc,
                                                  const float *xp, int col, float (&rv)[4],
                                                  uint64_t (&rc)[4]) {
@@ -486,12 +492,12 @@ __device__ __forceinline__ void request_residual(const LayersArgs &a, const uint
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     const int b = min(4 * (lane >> 4) + r, a.B - 1);
-    rc[r] = cld(xc, (size_t)b * a.H + col);
+    rc[r] = r < kR ? cld(xc, (size_t)b * a.H + col) : 0ull;  // rows past kR: unused
     rv[r] = 0.0f;
   }
   if (xp) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
+    for (int r = 0; r < kR; r++) {
       const int b = min(4 * (lane >> 4) + r, a.B - 1);
       rv[r] = gbl(xp)[(size_t)b * a.H + col];
     }
@@ -500,12 +506,13 @@ __device__ __forceinline__ void request_residual(const LayersArgs &a, const uint
 
 // The residual cells of request_residual carry `tag` (they were produced a
 // phase before the current inputs, so this normally returns at once).
+template <int kR>
 __device__ __forceinline__ bool finish_residual(const LayersArgs &a, const uint64_t *xc, int col,
                                                 unsigned tag, float (&rv)[4], uint64_t (&rc)[4]) {
   const int lane = threadIdx.x & 63;
   bool ok = true;
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
+  for (int r = 0; r < kR; r++) {
     const int b = min(4 * (lane >> 4) + r, a.B - 1);
     ok = ok && finish_cell(a, xc, (size_t)b * a.H + col, tag, rc[r]);
     rv[r] = f32_of((uint32_t)rc[r]);
@@ -542,7 +549,7 @@ __device__ __forceinline__ bool qkv_item(const LayersArgs &a, const LayerG &P, i
   if (threadIdx.x < 64) {
     const unsigned tag = tag_of(ep, l);
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
+    for (int r = 0; r < kOutRows<kRows>; r++) {
       const int b = 4 * (lane >> 4) + r;
       if (b < a.B) cst1(a.qkvc, (size_t)b * a.qkv_n + i * 16 + col, bits_of(acc[0][r] * sc), tag);
     }
@@ -561,18 +568,18 @@ __device__ __forceinline__ bool o_item(const LayersArgs &a, const LayerG &P, int
   const float sc = P.so[i * 16 + col];
   float rv[4];
   uint64_t rc[4];
-  request_residual(a, a.x0c, l == 0 ? a.x_in : nullptr, i * 16 + col, rv, rc);
+  request_residual<kOutRows<kRows>>(a, a.x0c, l == 0 ? a.x_in : nullptr, i * 16 + col, rv, rc);
   __builtin_amdgcn_sched_barrier(0);
   if (!stage_f16<(kL + 3) / 4, kRows>(a, a.attnc, tag_of(ep, l), K, s.xs, s.misc)) return false;
   f32x4 acc[1];
   mfma_weights<kL, 1>(w, s.xs, K + 8, a.B, acc);
   reduce_waves<1>(acc, s.red);
   if (threadIdx.x < 64) {
-    if (l > 0) finish_residual(a, a.x0c, i * 16 + col, tag_of(ep, l - 1), rv, rc);
+    if (l > 0) finish_residual<kOutRows<kRows>>(a, a.x0c, i * 16 + col, tag_of(ep, l - 1), rv, rc);
     else consume_cells(rc);  // unused at the first layer, but the loads must retire here
     const unsigned tag = tag_of(ep, l);
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
+    for (int r = 0; r < kOutRows<kRows>; r++) {
       const int b = 4 * (lane >> 4) + r;
       if (b < a.B) cst1(a.x1c, (size_t)b * a.H + i * 16 + col, bits_of(rv[r] + acc[0][r] * sc), tag);
     }
@@ -599,7 +606,7 @@ __device__ __forceinline__ bool up_item(const LayersArgs &a, const LayerG &P, in
   if (threadIdx.x < 64) {
     const unsigned tag = tag_of(ep, l);
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
+    for (int r = 0; r < kOutRows<kRows>; r++) {
       const int b = 4 * (lane >> 4) + r;
       const uint32_t h = f32_to_f16_bits(silu(acc[0][r] * sg) * (acc[1][r] * su));
       const uint32_t nb = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)h, 0xB1, 0xf, 0xf, false);
@@ -622,7 +629,7 @@ __device__ __forceinline__ bool down_item(const LayersArgs &a, const LayerG &P, 
   const unsigned tag = tag_of(ep, l);
   float rv[4];
   uint64_t rc[4];
-  request_residual(a, a.x1c, nullptr, i * 16 + col, rv, rc);
+  request_residual<kOutRows<kRows>>(a, a.x1c, nullptr, i * 16 + col, rv, rc);
   __builtin_amdgcn_sched_barrier(0);
   if (!stage_f16<(kL + 3) / 4, kRows>(a, a.actc, tag, K, s.xs, s.misc)) return false;
   SH_MARK(s.misc, l, 4);
@@ -632,10 +639,10 @@ __device__ __forceinline__ bool down_item(const LayersArgs &a, const LayerG &P, 
   reduce_waves<1>(acc, s.red);
   SH_MARK(s.misc, l, 6);
   if (threadIdx.x < 64) {
-    finish_residual(a, a.x1c, i * 16 + col, tag, rv, rc);
+    finish_residual<kOutRows<kRows>>(a, a.x1c, i * 16 + col, tag, rv, rc);
     const bool last = l + 1 == a.n_layers;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
+    for (int r = 0; r < kOutRows<kRows>; r++) {
       const int b = 4 * (lane >> 4) + r;
       const float v = rv[r] + acc[0][r] * sc;
       if (b < a.B) {
@@ -1093,7 +1100,7 @@ __device__ __forceinline__ bool head_phase(const LayersArgs &a, unsigned ep, con
     const f32x4 acc = (part[0] + part[1]) + (part[2] + part[3]);
     const int n = j * 16 + (lane & 15);
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
+    for (int r = 0; r < kOutRows<kRows>; r++) {
       const int b = 4 * (lane >> 4) + r;
       if (b < B && n < a.n_valid) {
         const float v = acc[r] * scale;
@@ -1110,7 +1117,7 @@ __device__ __forceinline__ bool head_phase(const LayersArgs &a, unsigned ep, con
     if (j + step < nT) tile(wb[1], sc[1], j + step);
   }
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
+  for (int r = 0; r < kOutRows<kRows>; r++) {
     unsigned long long k = best[r];
 #pragma unroll
     for (int off = 8; off >= 1; off >>= 1) {
