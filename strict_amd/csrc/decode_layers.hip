@@ -354,7 +354,7 @@ __device__ __forceinline__ bool stage_rms(const LayersArgs &a, const uint64_t *x
   typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
   constexpr int kN = kRows * kChunks * 4;
   static_assert(kN <= 64, "cells per thread");
-  const int B = a.B, c4 = K >> 2, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int B = kRows == 1 ? 1 : a.B, c4 = K >> 2, t = threadIdx.x, lane = t & 63, wave = t >> 6;
   f32x4 gv[kChunks];
 #pragma unroll
   for (int j = 0; j < kChunks; j++)
@@ -436,7 +436,7 @@ __device__ __forceinline__ bool stage_f16(const LayersArgs &a, const uint64_t *c
                           _Float16 *xs, Misc *misc) {
   constexpr int kN = kRows * kChunks * 2;
   static_assert(kN <= 64, "cells per thread");
-  const int B = a.B, c4 = K >> 2, t = threadIdx.x, row_cells = K >> 1;
+  const int B = kRows == 1 ? 1 : a.B, c4 = K >> 2, t = threadIdx.x, row_cells = K >> 1;
   for (int b0 = 0; b0 < B; b0 += kRows) {
     // cells of chunk (r, j): row b0 + r, cells 2 c, 2 c + 1, c = t + 256 j
     uint64_t cv[kN];
@@ -474,7 +474,8 @@ struct Lds {
 };
 
 // Rows per lane group of an MFMA output (acc[r] is row 4 (lane / 16) + r):
-// the batch-1 variants (kRows == 1) only ever have row 0.
+// the batch-1 variants (kRows == 1, chosen only for B == 1) only ever have
+// row 0, and their staging and MFMA code takes B as the constant 1.
 template <int kRows>
 constexpr int kOutRows = kRows == 1 ? 1 : 4;
 
@@ -542,7 +543,7 @@ __device__ __forceinline__ bool qkv_item(const LayersArgs &a, const LayerG &P, i
     return false;
   SH_MARK(s.misc, l, 0);
   f32x4 acc[1];
-  mfma_weights<kL, 1>(w, s.xs, a.H + 8, a.B, acc);
+  mfma_weights<kL, 1>(w, s.xs, a.H + 8, kRows == 1 ? 1 : a.B, acc);
   SH_MARK(s.misc, l, 1);
   reduce_waves<1>(acc, s.red);
   SH_MARK(s.misc, l, 2);
@@ -572,7 +573,7 @@ __device__ __forceinline__ bool o_item(const LayersArgs &a, const LayerG &P, int
   __builtin_amdgcn_sched_barrier(0);
   if (!stage_f16<(kL + 3) / 4, kRows>(a, a.attnc, tag_of(ep, l), K, s.xs, s.misc)) return false;
   f32x4 acc[1];
-  mfma_weights<kL, 1>(w, s.xs, K + 8, a.B, acc);
+  mfma_weights<kL, 1>(w, s.xs, K + 8, kRows == 1 ? 1 : a.B, acc);
   reduce_waves<1>(acc, s.red);
   if (threadIdx.x < 64) {
     if (l > 0) finish_residual<kOutRows<kRows>>(a, a.x0c, i * 16 + col, tag_of(ep, l - 1), rv, rc);
@@ -601,7 +602,7 @@ __device__ __forceinline__ bool up_item(const LayersArgs &a, const LayerG &P, in
   if (!stage_rms<(kL + 3) / 4, kRows>(a, a.x1c, nullptr, tag_of(ep, l), P.norm2, a.H, s.xs, s.misc))
     return false;
   f32x4 acc[2];
-  mfma_weights<kL, 2>(w, s.xs, a.H + 8, a.B, acc);
+  mfma_weights<kL, 2>(w, s.xs, a.H + 8, kRows == 1 ? 1 : a.B, acc);
   reduce_waves<2>(acc, s.red);
   if (threadIdx.x < 64) {
     const unsigned tag = tag_of(ep, l);
@@ -634,7 +635,7 @@ __device__ __forceinline__ bool down_item(const LayersArgs &a, const LayerG &P, 
   if (!stage_f16<(kL + 3) / 4, kRows>(a, a.actc, tag, K, s.xs, s.misc)) return false;
   SH_MARK(s.misc, l, 4);
   f32x4 acc[1];
-  mfma_weights<kL, 1>(w, s.xs, K + 8, a.B, acc);
+  mfma_weights<kL, 1>(w, s.xs, K + 8, kRows == 1 ? 1 : a.B, acc);
   SH_MARK(s.misc, l, 5);
   reduce_waves<1>(acc, s.red);
   SH_MARK(s.misc, l, 6);
@@ -1063,7 +1064,7 @@ template <int kLA, int kRows>
 __device__ __forceinline__ bool head_phase(const LayersArgs &a, unsigned ep, const Lds &s) {
   constexpr int kLH = 4 * kLA;  // K / 64
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, G = gridDim.x, w = blockIdx.x;
-  const int nT = a.head_tiles, H = a.H, B = a.B;
+  const int nT = a.head_tiles, H = a.H, B = kRows == 1 ? 1 : a.B;
   const SH_GLOBAL uint8_t *W = gbl(a.head_w);
   const int first = w + G * wave, step = 4 * G;
   u32x4 wb[2][kLH];
