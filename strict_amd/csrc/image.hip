@@ -128,13 +128,14 @@ __device__ __forceinline__ uint32_t brighten_lanes(uint32_t w, uint32_t d) {
 }
 
 // Whole-wave lane shifts by DPP (GFX9 wave_shr:1 / wave_shl:1): lane i gets
-// lane i-1 (from_left) or lane i+1 (from_right); lanes 0 / 63 keep their own
-// value, which the streaming kernel never uses.
-__device__ __forceinline__ uint32_t from_left(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x138, 0xf, 0xf, false);
+// lane i-1 (from_left) or lane i+1 (from_right); lane 0 (from_left) / lane
+// 63 (from_right), which have no such neighbour, get `edge` (DPP with
+// bound_ctrl off keeps the old value in a lane whose source is out of range)
+__device__ __forceinline__ uint32_t from_left(uint32_t v, uint32_t edge) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)edge, (int)v, 0x138, 0xf, 0xf, false);
 }
-__device__ __forceinline__ uint32_t from_right(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x130, 0xf, 0xf, false);
+__device__ __forceinline__ uint32_t from_right(uint32_t v, uint32_t edge) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)edge, (int)v, 0x130, 0xf, 0xf, false);
 }
 
 struct StreamArgs {
@@ -308,22 +309,15 @@ __global__ __launch_bounds__(kBlock) void blur_rgba_rows_kernel(const StreamArgs
       }
       // (the lane moves run in every lane first: a move under a branch would
       // read an inactive neighbour)
-      lo[0] = from_left(lo[4]);
-      lo[1] = from_left(lo[5]);
-      hi[0] = from_left(hi[4]);
-      hi[1] = from_left(hi[5]);
-      lo[6] = from_right(lo[2]);
-      lo[7] = from_right(lo[3]);
-      hi[6] = from_right(hi[2]);
-      hi[7] = from_right(hi[3]);
-      lo[0] = lane == 0 ? hs[0] : lo[0];
-      lo[1] = lane == 0 ? hs[2] : lo[1];
-      hi[0] = lane == 0 ? hs[1] : hi[0];
-      hi[1] = lane == 0 ? hs[3] : hi[1];
-      lo[6] = lane == 63 ? hs[0] : lo[6];
-      lo[7] = lane == 63 ? hs[2] : lo[7];
-      hi[6] = lane == 63 ? hs[1] : hi[6];
-      hi[7] = lane == 63 ? hs[3] : hi[7];
+      // (lane 0 and lane 63 take the halo sums in the same DPP moves)
+      lo[0] = from_left(lo[4], hs[0]);
+      lo[1] = from_left(lo[5], hs[2]);
+      hi[0] = from_left(hi[4], hs[1]);
+      hi[1] = from_left(hi[5], hs[3]);
+      lo[6] = from_right(lo[2], hs[0]);
+      lo[7] = from_right(lo[3], hs[2]);
+      hi[6] = from_right(hi[2], hs[1]);
+      hi[7] = from_right(hi[3], hs[3]);
       if (kMode == SH_BLUR_CONFIG) {
         lo[0] = left_edge ? lo[2] : lo[0];
         lo[1] = left_edge ? lo[2] : lo[1];
