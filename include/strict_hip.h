@@ -186,6 +186,25 @@ SH_API int sh_instructions_to_hip(const char *method_name, const char *const *pa
                                   const sh_bc_instruction *instructions, int instruction_count,
                                   char *source, size_t capacity, size_t *length);
 
+/* ---- range-loop dispatch ---------------------------------------------------- */
+
+/* Where a range loop of the VM runs (VirtualMachine.Loops.cs:111+), by the
+ * rule of the reference's MLIR backend (InstructionsToMlir.cs:397-418):
+ * complexity = iterations x max(body_instructions, 1), body_instructions
+ * being the instructions between the loop's begin and end
+ * (CountLoopBodyInstructions, :420-432); above SH_GPU_COMPLEXITY_THRESHOLD
+ * the body runs as a generated GPU kernel (gpu.launch there), above
+ * SH_PARALLEL_COMPLEXITY_THRESHOLD as a CPU-parallel loop (scf.parallel),
+ * otherwise as a serial loop (scf.for). Negative arguments count as 0. */
+#define SH_GPU_COMPLEXITY_THRESHOLD 10000000LL    /* GpuComplexityThreshold, :418 */
+#define SH_PARALLEL_COMPLEXITY_THRESHOLD 100000LL /* ComplexityThreshold, :414 */
+typedef enum sh_loop_target {
+  SH_LOOP_SERIAL = 0,
+  SH_LOOP_PARALLEL = 1,
+  SH_LOOP_GPU = 2,
+} sh_loop_target;
+SH_API int sh_range_loop_target(long long iterations, int body_instructions);
+
 /* ---- typed ops: elementwise ------------------------------------------------ */
 
 typedef enum sh_binary_op {

@@ -89,6 +89,7 @@ _U = ctypes.c_uint
 SIGNATURES = {
     "sh_last_error": (ctypes.c_char_p, []),
     "sh_version": (_I, []),
+    "sh_range_loop_target": (_I, [ctypes.c_longlong, _I]),
     "sh_device_count": (_I, [ctypes.POINTER(_I)]),
     "sh_create": (_I, [_I, _PP]),
     "sh_destroy": (_I, [_P]),

@@ -3,6 +3,7 @@
 // (Strict.Compiler.Cuda/InstructionsToCuda.cs:19-74). Host code only; the
 // text it writes is compiled for gfx950 by sh_compile (hipRTC).
 #include <cmath>
+#include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -195,4 +196,15 @@ extern "C" SH_API int sh_instructions_to_hip(const char *method_name,
                 text.size() + 1);
   std::memcpy(source, text.c_str(), text.size() + 1);
   return SH_OK;
+}
+
+// InstructionsToMlir.cs:397-408: complexity = iterations * max(body, 1),
+// compared strictly against the two thresholds. The product saturates.
+extern "C" SH_API int sh_range_loop_target(long long iterations, int body_instructions) {
+  const long long n = iterations > 0 ? iterations : 0;
+  const long long body = body_instructions > 1 ? body_instructions : 1;
+  const long long complexity = n > INT64_MAX / body ? INT64_MAX : n * body;
+  if (complexity > SH_GPU_COMPLEXITY_THRESHOLD) return SH_LOOP_GPU;
+  if (complexity > SH_PARALLEL_COMPLEXITY_THRESHOLD) return SH_LOOP_PARALLEL;
+  return SH_LOOP_SERIAL;
 }
