@@ -256,6 +256,26 @@ SH_API int sh_box_blur5_u8(sh_ctx *ctx, const uint8_t *in, uint8_t *out, int wid
 SH_API int sh_brightness_blur5_u8(sh_ctx *ctx, const uint8_t *in, uint8_t *out, int width,
                                   int height, int channels, int delta, int flags, int mode);
 
+/* ---- image layout adapters ----------------------------------------------------
+ * The steps either side of the image kernels in the reference's blur test. */
+
+/* Bitmap pixels to the test's RGBA byte image (CreateColorImageFromBitmapData,
+ * Cuda.Tests/BlurPerformanceTests.cs:87-101): for each pixel, dst R, G, B =
+ * src bytes 2, 1, 0 (BGR order), alpha 0 (the reference writes into a new,
+ * zeroed array). bytes_per_pixel: 3 (24 bpp) or 4 (32 bpp, the fourth byte
+ * ignored); rows src_stride bytes apart (the reference's pointer walks the
+ * pixels without row padding: src_stride = width * bytes_per_pixel). dst holds
+ * width * height * 4 bytes, 4-byte aligned; src and dst must not overlap;
+ * height <= 65535 (for both adapters). */
+SH_API int sh_bgr_to_rgba_u8(sh_ctx *ctx, const uint8_t *src, int bytes_per_pixel,
+                             size_t src_stride, uint8_t *dst, int width, int height);
+/* Packed RGB bytes to 24-bpp bitmap rows (SwitchRgbToBgr,
+ * Cuda.Tests/BlurPerformanceTests.cs:191-213): dst[y * dst_stride + 3 x + c] =
+ * src[3 (y * width + x) + 2 - c]; the row padding past 3 * width is left as it
+ * was. dst_stride >= 3 * width; src and dst must not overlap. */
+SH_API int sh_rgb_to_bgr_u8(sh_ctx *ctx, const uint8_t *src, uint8_t *dst, int width, int height,
+                            size_t dst_stride);
+
 /* ---- typed ops: dense GEMM --------------------------------------------------
  * The reference's only GEMM hook is the cuBLAS handle of Kernel.Handle
  * (Kernel.cs:10-11, :16), never used; BASELINE configs[2] fixes the op. */

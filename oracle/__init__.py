@@ -142,6 +142,28 @@ def brightness_blur5_config(img, width: int, height: int, delta: int, channels: 
     return out
 
 
+def bgr_to_rgba(src, width: int, height: int, bytes_per_pixel: int, src_stride: int) -> np.ndarray:
+    """CreateColorImageFromBitmapData (Cuda.Tests/BlurPerformanceTests.cs:87-101):
+    R, G, B = bitmap bytes 2, 1, 0 of each pixel, alpha 0 (a new zeroed array)."""
+    src = np.asarray(src, np.uint8)
+    rows = np.lib.stride_tricks.as_strided(
+        src, (height, width, bytes_per_pixel), (src_stride, bytes_per_pixel, 1))
+    out = np.zeros((height, width, 4), np.uint8)
+    out[..., 0], out[..., 1], out[..., 2] = rows[..., 2], rows[..., 1], rows[..., 0]
+    return out.reshape(-1)
+
+
+def rgb_to_bgr(src, width: int, height: int, dst_stride: int, dst) -> np.ndarray:
+    """SwitchRgbToBgr (Cuda.Tests/BlurPerformanceTests.cs:202-213) into a copy
+    of `dst`: bitmap byte y * stride + 3 x + c = RGB byte 3 (y w + x) + 2 - c;
+    the row padding keeps dst's bytes."""
+    rgb = np.asarray(src, np.uint8).reshape(height, width, 3)
+    out = np.array(dst, np.uint8, copy=True)
+    for y in range(height):
+        out[y * dst_stride:y * dst_stride + 3 * width] = rgb[y, :, ::-1].reshape(-1)
+    return out
+
+
 def f32_to_bf16(x) -> np.ndarray:
     x = np.ascontiguousarray(x, np.float32)
     out = np.empty(x.shape, np.uint16)

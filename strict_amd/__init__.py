@@ -374,6 +374,17 @@ class Context:
         _check(self._l.sh_adjust_brightness_u8(self.handle, _ptr(src), _ptr(dst), width, height,
                                                channels, delta, flags))
 
+    def bgr_to_rgba(self, src, bytes_per_pixel: int, src_stride: int, dst, width: int,
+                    height: int) -> None:
+        """Bitmap BGR(A) pixels to RGBA with alpha 0 (sh_bgr_to_rgba_u8)."""
+        _check(self._l.sh_bgr_to_rgba_u8(self.handle, _ptr(src), bytes_per_pixel, src_stride,
+                                         _ptr(dst), width, height))
+
+    def rgb_to_bgr(self, src, dst, width: int, height: int, dst_stride: int) -> None:
+        """Packed RGB to 24-bpp bitmap rows (sh_rgb_to_bgr_u8)."""
+        _check(self._l.sh_rgb_to_bgr_u8(self.handle, _ptr(src), _ptr(dst), width, height,
+                                        dst_stride))
+
     def box_blur5(self, src, dst, width: int, height: int, channels: int,
                   mode: int = BLUR_CONFIG) -> None:
         _check(self._l.sh_box_blur5_u8(self.handle, _ptr(src), _ptr(dst), width, height,

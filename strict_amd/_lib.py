@@ -128,6 +128,8 @@ SIGNATURES = {
     "sh_sigmoid_f32": (_I, [_P, _P, _P, _SZ]),
     "sh_adjust_brightness_u8": (_I, [_P, _P, _P, _I, _I, _I, _I, _I]),
     "sh_box_blur5_u8": (_I, [_P, _P, _P, _I, _I, _I, _I]),
+    "sh_bgr_to_rgba_u8": (_I, [_P, _P, _I, ctypes.c_size_t, _P, _I, _I]),
+    "sh_rgb_to_bgr_u8": (_I, [_P, _P, _P, _I, _I, ctypes.c_size_t]),
     "sh_brightness_blur5_u8": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I]),
     "sh_gemm_bf16": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I]),
     "sh_gemm_fp8": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I]),

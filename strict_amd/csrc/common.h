@@ -60,6 +60,10 @@ int blaslt_gemm_fp8(sh_ctx *ctx, hipStream_t s, const uint8_t *A, const float *s
                     int ldb, int ldc);
 void blaslt_release(sh_ctx *ctx);
 
+hipError_t launch_bgr_to_rgba_u8(hipStream_t s, const uint8_t *src, int bpp, size_t src_stride,
+                                 uint32_t *dst, int width, int height);
+hipError_t launch_rgb_to_bgr_u8(hipStream_t s, const uint8_t *src, uint8_t *dst, int width,
+                                int height, size_t dst_stride);
 hipError_t launch_brightness_u8(hipStream_t s, const uint8_t *in, uint8_t *out, size_t bytes,
                                 int channels, int delta, int all_channels);
 hipError_t launch_blur5_u8(hipStream_t s, const uint8_t *in, uint8_t *out, int width, int height,

@@ -365,6 +365,33 @@ __global__ __launch_bounds__(kBlock) void blur_rgba_rows_kernel(const StreamArgs
 }
 
 // ---------------------------------------------------------------------------
+// Layout adapters (bitmap BGR(A) <-> the blur test's RGBA / RGB byte images).
+// One pixel per thread, rows by blockIdx.y: byte gathers, one 4-byte store
+// per pixel on the RGBA side.
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(kBlock) void bgr_to_rgba_kernel(const uint8_t *__restrict__ src, int bpp,
+                                                             size_t src_stride,
+                                                             uint32_t *__restrict__ dst, int width) {
+  const int x = blockIdx.x * kBlock + threadIdx.x, y = blockIdx.y;
+  if (x >= width) return;
+  const uint8_t *p = src + (size_t)y * src_stride + (size_t)x * bpp;
+  dst[(size_t)y * width + x] = (uint32_t)p[2] | ((uint32_t)p[1] << 8) | ((uint32_t)p[0] << 16);
+}
+
+__global__ __launch_bounds__(kBlock) void rgb_to_bgr_kernel(const uint8_t *__restrict__ src,
+                                                            uint8_t *__restrict__ dst, int width,
+                                                            size_t dst_stride) {
+  const int x = blockIdx.x * kBlock + threadIdx.x, y = blockIdx.y;
+  if (x >= width) return;
+  const uint8_t *p = src + ((size_t)y * width + x) * 3;
+  uint8_t *q = dst + (size_t)y * dst_stride + (size_t)x * 3;
+  q[0] = p[2];
+  q[1] = p[1];
+  q[2] = p[0];
+}
+
+// ---------------------------------------------------------------------------
 // Blur, direct kernel for any channel count / width (one pixel per thread).
 // ---------------------------------------------------------------------------
 
@@ -509,6 +536,22 @@ hipError_t launch_blur5_u8(hipStream_t s, const uint8_t *in, uint8_t *out, int w
     blur_direct_kernel<<<(unsigned)((pixels + kBlock - 1) / kBlock), kBlock, 0, s>>>(
         in, out, width, height, channels, mode, fuse ? 1 : 0, delta, all_channels);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_bgr_to_rgba_u8(hipStream_t s, const uint8_t *src, int bpp, size_t src_stride,
+                                 uint32_t *dst, int width, int height) {
+  if (width > 0 && height > 0)
+    bgr_to_rgba_kernel<<<dim3((width + kBlock - 1) / kBlock, height), kBlock, 0, s>>>(
+        src, bpp, src_stride, dst, width);
+  return hipGetLastError();
+}
+
+hipError_t launch_rgb_to_bgr_u8(hipStream_t s, const uint8_t *src, uint8_t *dst, int width,
+                                int height, size_t dst_stride) {
+  if (width > 0 && height > 0)
+    rgb_to_bgr_kernel<<<dim3((width + kBlock - 1) / kBlock, height), kBlock, 0, s>>>(
+        src, dst, width, dst_stride);
   return hipGetLastError();
 }
 

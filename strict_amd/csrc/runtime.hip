@@ -580,6 +580,57 @@ SH_API int sh_adjust_brightness_u8(sh_ctx *ctx, const uint8_t *in, uint8_t *out,
                   "adjust_brightness_u8");
 }
 
+// Image layout adapters. Sizes are checked in size_t before any launch; a
+// stride must cover its row.
+static int check_adapter_size(int width, int height) {
+  if (width < 0 || height < 0)
+    return fail(SH_ERR_INVALID_ARGUMENT, "negative image size %dx%d", width, height);
+  if (height > 65535) return fail(SH_ERR_INVALID_ARGUMENT, "height %d above 65535", height);
+  return SH_OK;
+}
+
+SH_API int sh_bgr_to_rgba_u8(sh_ctx *ctx, const uint8_t *src, int bytes_per_pixel,
+                             size_t src_stride, uint8_t *dst, int width, int height) {
+  SH_CHECK(enter(ctx));
+  SH_CHECK(check_adapter_size(width, height));
+  if (bytes_per_pixel != 3 && bytes_per_pixel != 4)
+    return fail(SH_ERR_INVALID_ARGUMENT, "bytes_per_pixel %d is not 3 or 4", bytes_per_pixel);
+  if (width == 0 || height == 0) return SH_OK;
+  if (src_stride < (size_t)width * bytes_per_pixel)
+    return fail(SH_ERR_INVALID_ARGUMENT, "src_stride %zu below %d x %d", src_stride, width,
+                bytes_per_pixel);
+  if (reinterpret_cast<uintptr_t>(dst) % 4)
+    return fail(SH_ERR_INVALID_ARGUMENT, "dst is not 4-byte aligned");
+  const size_t in_bytes = (size_t)(height - 1) * src_stride + (size_t)width * bytes_per_pixel;
+  const size_t out_bytes = (size_t)width * height * 4;
+  SH_CHECK(check_range(ctx, src, in_bytes, "src"));
+  SH_CHECK(check_range(ctx, dst, out_bytes, "dst"));
+  if (reinterpret_cast<uintptr_t>(src) < reinterpret_cast<uintptr_t>(dst) + out_bytes &&
+      reinterpret_cast<uintptr_t>(dst) < reinterpret_cast<uintptr_t>(src) + in_bytes)
+    return fail(SH_ERR_INVALID_ARGUMENT, "src and dst overlap");
+  return launched(launch_bgr_to_rgba_u8(ctx->stream, src, bytes_per_pixel, src_stride,
+                                        reinterpret_cast<uint32_t *>(dst), width, height),
+                  "bgr_to_rgba_u8");
+}
+
+SH_API int sh_rgb_to_bgr_u8(sh_ctx *ctx, const uint8_t *src, uint8_t *dst, int width, int height,
+                            size_t dst_stride) {
+  SH_CHECK(enter(ctx));
+  SH_CHECK(check_adapter_size(width, height));
+  if (width == 0 || height == 0) return SH_OK;
+  if (dst_stride < (size_t)width * 3)
+    return fail(SH_ERR_INVALID_ARGUMENT, "dst_stride %zu below 3 x %d", dst_stride, width);
+  const size_t in_bytes = (size_t)width * height * 3;
+  const size_t out_bytes = (size_t)(height - 1) * dst_stride + (size_t)width * 3;
+  SH_CHECK(check_range(ctx, src, in_bytes, "src"));
+  SH_CHECK(check_range(ctx, dst, out_bytes, "dst"));
+  if (reinterpret_cast<uintptr_t>(src) < reinterpret_cast<uintptr_t>(dst) + out_bytes &&
+      reinterpret_cast<uintptr_t>(dst) < reinterpret_cast<uintptr_t>(src) + in_bytes)
+    return fail(SH_ERR_INVALID_ARGUMENT, "src and dst overlap");
+  return launched(launch_rgb_to_bgr_u8(ctx->stream, src, dst, width, height, dst_stride),
+                  "rgb_to_bgr_u8");
+}
+
 static int blur_common(sh_ctx *ctx, const uint8_t *in, uint8_t *out, int width, int height,
                        int channels, int mode, bool fuse, int delta, int flags) {
   SH_CHECK(enter(ctx));
