@@ -65,6 +65,16 @@ def _declare(l) -> None:
     l.or_e4m3_to_f32.restype = f
     l.or_quantize_e4m3_rows.argtypes = [P, i, i, P, P, i]
     l.or_gemm_f32.argtypes = [P, P, P, i, i, i, i]
+    lg = ctypes.c_long
+    d = ctypes.c_double
+    l.or_perf_sigmoid.argtypes = [i, P, P, lg, i, i]
+    l.or_perf_sigmoid.restype = d
+    l.or_perf_brightness.argtypes = [i, P, P, lg, i, i, i, i]
+    l.or_perf_brightness.restype = d
+    l.or_perf_blur5.argtypes = [i, i, P, P, i, i, i, i, lg, i, i]
+    l.or_perf_blur5.restype = d
+    l.or_perf_cross_blur.argtypes = [i, P, i, i, lg, i, i]
+    l.or_perf_cross_blur.restype = d
 
 
 def _p(a: np.ndarray):
@@ -223,3 +233,36 @@ def gemm_f32(a, b, nthreads: int | None = None) -> np.ndarray:
     c = np.empty((m, n), np.float32)
     lib().or_gemm_f32(_p(a), _p(b), _p(c), m, n, k, nthreads or default_threads())
     return c
+
+
+# ---- TestPerformance's CPU modes (Strict.Compiler.Cuda.Tests/TestPerformance.cs:34-49) ----
+
+PERF_MODES = ("SingleThread", "SingleThreadChunks", "ParallelCpu", "ParallelCpuChunks")
+CHUNK_SIZE = 100  # the reference tests' ChunkSize (SigmoidPerformanceTests.cs:20, Cuda BlurPerformanceTests.cs:40)
+BLUR_REFERENCE, BLUR_CONFIG, BLUR_FUSED = 0, 1, 2
+
+
+def perf_sigmoid(mode: int, x, y, nthreads: int, chunk: int = CHUNK_SIZE) -> float:
+    """ms for one TestPerformance mode of sigmoid over the array x -> y."""
+    return lib().or_perf_sigmoid(mode, _p(x), _p(y), x.size, chunk, nthreads)
+
+
+def perf_brightness(mode: int, img, out, channels: int, delta: int, nthreads: int,
+                    pixels: int | None = None, chunk: int = CHUNK_SIZE) -> float:
+    n = img.size // channels if pixels is None else pixels
+    return lib().or_perf_brightness(mode, _p(img), _p(out), n, channels, delta, chunk, nthreads)
+
+
+def perf_blur5(mode: int, kind: int, img, out, width: int, height: int, channels: int,
+               nthreads: int, delta: int = 0, pixels: int | None = None,
+               chunk: int = CHUNK_SIZE) -> float:
+    n = width * height if pixels is None else pixels
+    return lib().or_perf_blur5(mode, kind, _p(img), _p(out), width, height, channels, delta, n,
+                               chunk, nthreads)
+
+
+def perf_cross_blur(mode: int, image, width: int, height: int, iterations: int, nthreads: int,
+                    chunk: int = CHUNK_SIZE) -> float:
+    """ms for one mode of the CUDA harness's in-place cross blur (modifies image)."""
+    assert image.size == width * height * 4
+    return lib().or_perf_cross_blur(mode, _p(image), width, height, iterations, chunk, nthreads)

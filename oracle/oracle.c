@@ -7,6 +7,7 @@
 
 #include <math.h>
 #include <pthread.h>
+#include <time.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -225,6 +226,184 @@ void or_brightness_blur5_config(const uint8_t *in, uint8_t *out, int width, int 
                        nthreads);
   or_blur5_config(tmp, out, width, height, channels, nthreads);
   free(tmp);
+}
+
+/* ---- TestPerformance's CPU modes ----------------------------------------
+ *
+ * Strict.Compiler.Cuda.Tests/TestPerformance.cs:34-49 times one workload
+ * `RunChunk(start, chunkSize)` four ways: SingleThread (RunChunk(i, 1) for
+ * every i), SingleThreadChunks (RunChunk(i * ChunkSize, ChunkSize) for every
+ * chunk), ParallelCpu (Parallel.For over i, RunChunk(i, 1)) and
+ * ParallelCpuChunks (Parallel.For over chunks). The chunk functions are
+ * called through a function pointer, as the C# delegate is, and are never
+ * inlined into the loops. Parallel.For is restated as a pool of `nthreads`
+ * threads taking ranges of indices from a shared counter (dynamic range
+ * partitioning). Each run returns its wall time in ms (Stopwatch, :26-29). */
+
+typedef void (*chunk_fn)(void *ctx, long start, long chunk);
+
+typedef struct {
+  chunk_fn fn;
+  void *ctx;
+  long items;  /* indices handed out: iterations, or chunks */
+  long grain;  /* indices per grab */
+  int chunk;   /* 0: fn(i, 1) per index; else fn(i * chunk, chunk) */
+  long next;   /* shared counter (atomic) */
+} perf_job;
+
+static void run_indices(perf_job *j, long b, long e) {
+  if (j->chunk)
+    for (long k = b; k < e; k++) j->fn(j->ctx, k * (long)j->chunk, j->chunk);
+  else
+    for (long k = b; k < e; k++) j->fn(j->ctx, k, 1);
+}
+
+static void *perf_worker(void *p) {
+  perf_job *j = (perf_job *)p;
+  for (;;) {
+    long b = __atomic_fetch_add(&j->next, j->grain, __ATOMIC_RELAXED);
+    if (b >= j->items) break;
+    long e = b + j->grain < j->items ? b + j->grain : j->items;
+    run_indices(j, b, e);
+  }
+  return NULL;
+}
+
+static double now_ms(void) {
+  struct timespec ts;
+  clock_gettime(CLOCK_MONOTONIC, &ts);
+  return (double)ts.tv_sec * 1e3 + (double)ts.tv_nsec * 1e-6;
+}
+
+__attribute__((noipa)) static double perf_run(int mode, long iterations, int chunk_size, chunk_fn fn,
+                                              void *ctx, int nthreads) {
+  perf_job j;
+  j.fn = fn;
+  j.ctx = ctx;
+  j.next = 0;
+  const int chunked = mode == OR_SINGLE_THREAD_CHUNKS || mode == OR_PARALLEL_CPU_CHUNKS;
+  j.chunk = chunked ? chunk_size : 0;
+  j.items = chunked ? iterations / chunk_size : iterations; /* :41, :48 */
+  j.grain = chunked ? 16 : 4096;
+  const double t0 = now_ms();
+  if (mode == OR_SINGLE_THREAD || mode == OR_SINGLE_THREAD_CHUNKS || nthreads <= 1) {
+    run_indices(&j, 0, j.items);
+  } else {
+    pthread_t *threads = (pthread_t *)calloc((size_t)nthreads, sizeof(pthread_t));
+    int started = 0;
+    for (int t = 0; t < nthreads; t++)
+      if (pthread_create(&threads[t], NULL, perf_worker, &j) == 0) started++;
+      else break;
+    if (started == 0) run_indices(&j, 0, j.items);
+    for (int t = 0; t < started; t++) pthread_join(threads[t], NULL);
+    free(threads);
+  }
+  return now_ms() - t0;
+}
+
+/* SigmoidPerformanceTests.SigmoidOutput (:24-28) over the config's array:
+ * element n of x -> y[n], the arithmetic of or_sigmoid_f32. */
+__attribute__((noinline)) static void sigmoid_chunk(void *p, long start, long chunk) {
+  sigmoid_range(p, (size_t)start, (size_t)(start + chunk));
+}
+
+double or_perf_sigmoid(int mode, const float *x, float *y, long n, int chunk, int nthreads) {
+  sigmoid_ctx c = {x, y};
+  return perf_run(mode, n, chunk, sigmoid_chunk, &c, nthreads);
+}
+
+/* AdjustPixelBrightness (Assembly.Tests/BlurPerformanceTests.cs:287-294),
+ * one pixel per index. */
+__attribute__((noinline)) static void brightness_chunk(void *p, long start, long chunk) {
+  brightness_range(p, (size_t)start, (size_t)(start + chunk));
+}
+
+double or_perf_brightness(int mode, const uint8_t *in, uint8_t *out, long pixels, int channels,
+                          int delta, int chunk, int nthreads) {
+  brightness_ctx c = {in, out, channels, delta, 0};
+  return perf_run(mode, pixels, chunk, brightness_chunk, &c, nthreads);
+}
+
+/* 5x5 blurs, one output pixel per index (pixel n = row n / width, column
+ * n % width): the reference semantics of or_blur5_reference
+ * (BlurPerformanceTests.cs:85-141), the config semantics of or_blur5_config,
+ * and the config blur of brightened taps (the fused kernel's result). */
+typedef struct {
+  const uint8_t *in;
+  uint8_t *out;
+  int width, height, channels, delta, kind;
+} blur_px_ctx;
+
+static void blur_pixel(const blur_px_ctx *c, int row, int col) {
+  const int w = c->width, h = c->height, ch = c->channels;
+  const size_t stride = (size_t)w * (size_t)ch, base = (size_t)row * stride + (size_t)col * (size_t)ch;
+  const int interior = row >= 2 && row < h - 2 && col >= 2 && col < w - 2;
+  for (int k = 0; k < ch; k++) {
+    int sum = 0, count = 0;
+    for (int ky = -2; ky <= 2; ky++)
+      for (int kx = -2; kx <= 2; kx++) {
+        int ny = row + ky, nx = col + kx;
+        if (c->kind == 0) { /* reference: in-bounds taps only */
+          if ((unsigned)nx >= (unsigned)w || (unsigned)ny >= (unsigned)h) continue;
+        } else {
+          ny = clampi(ny, 0, h - 1);
+          nx = clampi(nx, 0, w - 1);
+        }
+        int v = c->in[(size_t)ny * stride + (size_t)nx * (size_t)ch + (size_t)k];
+        if (c->kind == 2 && k < 3) v = clampi(v + c->delta, 0, 255);
+        sum += v;
+        count++;
+      }
+    c->out[base + (size_t)k] =
+        (uint8_t)(c->kind == 0 ? (interior ? sum / 25 : sum / count) : (sum + 12) / 25);
+  }
+}
+
+__attribute__((noinline)) static void blur_chunk(void *p, long start, long chunk) {
+  const blur_px_ctx *c = (const blur_px_ctx *)p;
+  for (long n = start; n < start + chunk; n++) blur_pixel(c, (int)(n / c->width), (int)(n % c->width));
+}
+
+double or_perf_blur5(int mode, int kind, const uint8_t *in, uint8_t *out, int width, int height,
+                     int channels, int delta, long pixels, int chunk, int nthreads) {
+  blur_px_ctx c = {in, out, width, height, channels, delta, kind};
+  long total = (long)width * (long)height;
+  return perf_run(mode, pixels < total ? pixels : total, chunk, blur_chunk, &c, nthreads);
+}
+
+/* The CUDA harness's CPU blur (Strict.Compiler.Cuda.Tests/BlurPerformanceTests.cs:160-169):
+ * in place over the RGBA byte stream of `size` = width * height * 4 bytes,
+ * for every index n of the chunk (chunks starting below width * 4 are skipped
+ * whole, :162-163):
+ *   image[n % size] = (image[n % size] + image[(n - 4w) % size] + image[(n - 4) % size]
+ *                      + image[(n + 4) % size] + image[(n + 4w) % size]) / 5
+ * The byte accesses are relaxed atomics, so the parallel modes' overlapping
+ * in-place updates (a race in the reference too) stay defined; on x86 they
+ * are plain byte loads and stores. */
+typedef struct {
+  uint8_t *image;
+  long size, w4;
+} cross_ctx;
+
+static inline int cross_ld(const cross_ctx *c, long i) {
+  return __atomic_load_n(c->image + i, __ATOMIC_RELAXED);
+}
+
+__attribute__((noinline)) static void cross_blur_chunk(void *p, long start, long chunk) {
+  const cross_ctx *c = (const cross_ctx *)p;
+  if (start < c->w4) return;
+  const long size = c->size;
+  for (long n = start; n < start + chunk; n++) {
+    int sum = cross_ld(c, n % size) + cross_ld(c, (n - c->w4) % size) + cross_ld(c, (n - 4) % size) +
+              cross_ld(c, (n + 4) % size) + cross_ld(c, (n + c->w4) % size);
+    __atomic_store_n(c->image + n % size, (uint8_t)(sum / 5), __ATOMIC_RELAXED);
+  }
+}
+
+double or_perf_cross_blur(int mode, uint8_t *image, int width, int height, long iterations,
+                          int chunk, int nthreads) {
+  cross_ctx c = {image, (long)width * (long)height * 4, (long)width * 4};
+  return perf_run(mode, iterations, chunk, cross_blur_chunk, &c, nthreads);
 }
 
 /* ---- number formats ------------------------------------------------------ */

@@ -60,6 +60,34 @@ void or_blur5_config(const uint8_t *in, uint8_t *out, int width, int height, int
 void or_brightness_blur5_config(const uint8_t *in, uint8_t *out, int width, int height,
                                 int channels, int delta, int all_channels, int nthreads);
 
+/* TestPerformance's CPU modes (Strict.Compiler.Cuda.Tests/TestPerformance.cs:34-49):
+ * SingleThread, SingleThreadChunks, ParallelCpu, ParallelCpuChunks. Each
+ * or_perf_* call runs one mode of one workload's RunChunk(start, chunk) over
+ * `iterations` indices (chunk = ChunkSize, 100 in the reference's tests) on
+ * up to nthreads threads and returns the wall time in ms. */
+enum {
+  OR_SINGLE_THREAD = 0,
+  OR_SINGLE_THREAD_CHUNKS = 1,
+  OR_PARALLEL_CPU = 2,
+  OR_PARALLEL_CPU_CHUNKS = 3
+};
+/* index n: y[n] = sigmoid(x[n]) (SigmoidPerformanceTests.cs:24-28, over an array) */
+double or_perf_sigmoid(int mode, const float *x, float *y, long n, int chunk, int nthreads);
+/* index n: pixel n of AdjustPixelBrightness (Assembly BlurPerformanceTests.cs:287-294) */
+double or_perf_brightness(int mode, const uint8_t *in, uint8_t *out, long pixels, int channels,
+                          int delta, int chunk, int nthreads);
+/* index n < pixels: output pixel n of a 5x5 blur; kind 0 = reference semantics
+ * (or_blur5_reference), 1 = config semantics (or_blur5_config), 2 = config blur of
+ * the taps brightened by delta on channels 0..2 (the fused brightness + blur) */
+double or_perf_blur5(int mode, int kind, const uint8_t *in, uint8_t *out, int width, int height,
+                     int channels, int delta, long pixels, int chunk, int nthreads);
+/* Cuda.Tests/BlurPerformanceTests.cs:160-169: the in-place 5-point cross /5
+ * over the RGBA byte stream, indices modulo width * height * 4, chunks
+ * starting below width * 4 skipped; the reference runs width * height * 100
+ * (its logged counts) or * 200 (its constant, :106) iterations. */
+double or_perf_cross_blur(int mode, uint8_t *image, int width, int height, long iterations,
+                          int chunk, int nthreads);
+
 /* Number formats (no reference implementation; IEEE 754 / OCP 8-bit FP spec). */
 uint16_t or_f32_to_bf16(float f);   /* round to nearest even, NaN kept quiet */
 float or_bf16_to_f32(uint16_t h);

@@ -50,16 +50,6 @@ hipError_t launch_gemm_fp8(hipStream_t s, const uint8_t *A, const float *sa, con
 bool gemm_fp8_uses_mfma(int M, int N, int K, int lda, int ldb, int ldc, const void *A,
                         const void *Bt, const void *C, const void *sb);
 
-// hipBLASLt backend (blas.cpp), used only with STRICT_HIP_GEMM=blaslt:
-// SH_OK when it ran the product, SH_ERR_UNSUPPORTED when the caller should
-// launch its own kernel, another status on a library failure.
-int blaslt_gemm_bf16(sh_ctx *ctx, hipStream_t s, const uint16_t *A, const uint16_t *B, uint16_t *C,
-                     int M, int N, int K, int lda, int ldb, int ldc);
-int blaslt_gemm_fp8(sh_ctx *ctx, hipStream_t s, const uint8_t *A, const float *sa,
-                    const uint8_t *Bt, const float *sb, uint16_t *C, int M, int N, int K, int lda,
-                    int ldb, int ldc);
-void blaslt_release(sh_ctx *ctx);
-
 hipError_t launch_bgr_to_rgba_u8(hipStream_t s, const uint8_t *src, int bpp, size_t src_stride,
                                  uint32_t *dst, int width, int height);
 hipError_t launch_rgb_to_bgr_u8(hipStream_t s, const uint8_t *src, uint8_t *dst, int width,

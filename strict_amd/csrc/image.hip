@@ -444,18 +444,10 @@ Brightness make_brightness(bool enabled, int channels, int delta, int all_channe
   return br;
 }
 
-// Output rows per wave: 16 by default, which on 4096 x 4096 makes 16 x 256 =
-// 4096 waves, one round at 4 waves per SIMD (measured 29.1 us against 31.3 us
-// with 8 rows, two rounds); the STRICT_HIP_BLUR_ROWS environment variable
-// (8, 16 or 32) overrides it for tuning sweeps.
-int blur_rows() {
-  static const int rows = [] {
-    const char *e = getenv("STRICT_HIP_BLUR_ROWS");
-    const int r = e ? atoi(e) : 16;
-    return (r == 8 || r == 32) ? r : 16;
-  }();
-  return rows;
-}
+// Output rows per wave: 16 make 16 x 256 = 4096 waves on 4096 x 4096, one
+// round at 4 waves per SIMD (measured 29.1 us against 31.3 us with 8 rows,
+// two rounds).
+constexpr int kBlurRows = 16;
 
 template <int kMode, int kR>
 void launch_rows_fuse(hipStream_t s, const StreamArgs &a, int fuse) {
@@ -520,17 +512,7 @@ hipError_t launch_blur5_u8(hipStream_t s, const uint8_t *in, uint8_t *out, int w
   if (channels == 4 && width % 4 == 0 && aligned16(in) && aligned16(out)) {
     const uint32_t *in32 = reinterpret_cast<const uint32_t *>(in);
     uint32_t *out32 = reinterpret_cast<uint32_t *>(out);
-    switch (blur_rows()) {
-      case 8:
-        launch_blur_stream<8>(s, in32, out32, width, height, mode, fuse, delta, all_channels);
-        break;
-      case 32:
-        launch_blur_stream<32>(s, in32, out32, width, height, mode, fuse, delta, all_channels);
-        break;
-      default:
-        launch_blur_stream<16>(s, in32, out32, width, height, mode, fuse, delta, all_channels);
-        break;
-    }
+    launch_blur_stream<kBlurRows>(s, in32, out32, width, height, mode, fuse, delta, all_channels);
   } else {
     const long long pixels = (long long)width * height;
     blur_direct_kernel<<<(unsigned)((pixels + kBlock - 1) / kBlock), kBlock, 0, s>>>(

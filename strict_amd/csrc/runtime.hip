@@ -158,7 +158,6 @@ SH_API int sh_destroy(sh_ctx *ctx) {
   (void)hipStreamSynchronize(ctx->stream);
   std::vector<sh_module *> mods(ctx->modules.begin(), ctx->modules.end());
   for (auto *m : mods) sh_module_unload(m);
-  blaslt_release(ctx);
   for (auto &kv : ctx->owned) (void)hipFree(reinterpret_cast<void *>(kv.first));
   ctx->owned.clear();
   (void)hipEventDestroy(ctx->timer_begin);
@@ -693,8 +692,6 @@ SH_API int sh_gemm_bf16(sh_ctx *ctx, const uint16_t *A, const uint16_t *B, uint1
   }
   SH_CHECK(check_range(ctx, A, span_elems(M, K, lda) * 2, "A"));
   SH_CHECK(check_range(ctx, B, span_elems(K, N, ldb) * 2, "B"));
-  const int lib = blaslt_gemm_bf16(ctx, ctx->stream, A, B, C, M, N, K, lda, ldb, ldc);
-  if (lib != SH_ERR_UNSUPPORTED) return lib;
   return launched(launch_gemm_bf16(ctx->stream, A, B, C, M, N, K, lda, ldb, ldc), "gemm_bf16");
 }
 
@@ -718,8 +715,6 @@ SH_API int sh_gemm_fp8(sh_ctx *ctx, const uint8_t *A, const float *sa, const uin
   SH_CHECK(check_range(ctx, Bt, span_elems(N, K, ldb), "Bt"));
   SH_CHECK(check_range(ctx, sa, (size_t)M * 4, "sa"));
   SH_CHECK(check_range(ctx, sb, (size_t)N * 4, "sb"));
-  const int lib = blaslt_gemm_fp8(ctx, ctx->stream, A, sa, Bt, sb, C, M, N, K, lda, ldb, ldc);
-  if (lib != SH_ERR_UNSUPPORTED) return lib;
   return launched(launch_gemm_fp8(ctx->stream, A, sa, Bt, sb, C, M, N, K, lda, ldb, ldc),
                   "gemm_fp8");
 }

@@ -1,9 +1,16 @@
-// Plain GEMMs through hipBLASLt: the counterpart of the cuBLAS handle the
-// reference keeps in Kernel.Handle (Kernel.cs:10-11, :16). The hand-written
-// MFMA kernels (gemm.hip, gemm_fp8.hip) are the default; STRICT_HIP_GEMM=blaslt
-// routes sh_gemm_bf16 / sh_gemm_fp8 here for the shapes hipBLASLt's heuristic
-// has a gfx950 algorithm for (the others still take the hand-written kernels).
-// The bench times both, so the library's figure is the yardstick for ours.
+// hipBLASLt GEMMs as the benchmark's yardstick for the hand-written MFMA
+// kernels (gemm.hip, gemm_fp8.hip). Built into its own library,
+// libsh_blaslt_yardstick.so, which bench.py and the yardstick parity tests
+// load; libstrict_hip.so neither links nor loads it, and sh_gemm_bf16 /
+// sh_gemm_fp8 always run the hand-written kernels.
+//
+// C ABI (status 0 = ok, 7 = hipBLASLt has no algorithm for the shape, 3 = a
+// hipBLASLt / HIP call failed; shy_last_error() has the text):
+//   shy_gemm_bf16(stream, A, B, C, M, N, K, lda, ldb, ldc)
+//   shy_gemm_fp8(stream, A, sa, Bt, sb, C, M, N, K, lda, ldb, ldc)
+//   shy_release()   destroys every handle, plan and workspace
+// with the operand conventions of sh_gemm_bf16 / sh_gemm_fp8
+// (include/strict_hip.h): device pointers, row-major, enqueued on `stream`.
 //
 // Row-major C = A B is the column-major product C^T = B^T A^T, so the
 // hipBLASLt call's first operand is B (bf16: B row-major [K][N] is B^T in
@@ -14,18 +21,29 @@
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
-#include <cstdlib>
-#include <cstring>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
 #include <map>
 #include <mutex>
 #include <tuple>
 
-#include "common.h"
+#define SHY_API extern "C" __attribute__((visibility("default")))
 
-namespace sh {
 namespace {
 
+constexpr int kOk = 0, kErrHip = 3, kUnsupported = 7;
 constexpr size_t kWorkspaceBytes = 64ull << 20;
+
+thread_local char g_error[512];
+
+int fail(int status, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof g_error, fmt, ap);
+  va_end(ap);
+  return status;
+}
 
 struct Plan {
   hipblasLtMatmulDesc_t op = nullptr;
@@ -34,22 +52,17 @@ struct Plan {
   bool ok = false;  // an algorithm exists for this shape
 };
 
-// (kind, M, N, K, lda, ldb, ldc)
-typedef std::tuple<int, int, int, int, int, int, int> PlanKey;
+// (device, kind, M, N, K, lda, ldb, ldc)
+typedef std::tuple<int, int, int, int, int, int, int, int> PlanKey;
 
 struct State {
   hipblasLtHandle_t handle = nullptr;
   void *workspace = nullptr;
-  std::map<PlanKey, Plan> plans;
 };
 
 std::mutex g_mu;
-std::map<const sh_ctx *, State> g_states;
-
-bool enabled() {
-  const char *e = getenv("STRICT_HIP_GEMM");
-  return e && std::strcmp(e, "blaslt") == 0;
-}
+std::map<int, State> g_states;  // per device
+std::map<PlanKey, Plan> g_plans;
 
 void destroy_plan(Plan &p) {
   if (p.a) hipblasLtMatrixLayoutDestroy(p.a);
@@ -59,10 +72,8 @@ void destroy_plan(Plan &p) {
   p = Plan{};
 }
 
-// The plan for kind 0 (bf16) or 1 (fp8 with vector scales); nullptr when the
-// state cannot be created.
-Plan *plan_for(sh_ctx *ctx, int kind, int M, int N, int K, int lda, int ldb, int ldc) {
-  State &st = g_states[ctx];
+State *state_for(int device) {
+  State &st = g_states[device];
   if (!st.handle) {
     if (hipblasLtCreate(&st.handle) != HIPBLAS_STATUS_SUCCESS) return nullptr;
     if (hipMalloc(&st.workspace, kWorkspaceBytes) != hipSuccess) {
@@ -71,10 +82,15 @@ Plan *plan_for(sh_ctx *ctx, int kind, int M, int N, int K, int lda, int ldb, int
       return nullptr;
     }
   }
-  const PlanKey key{kind, M, N, K, lda, ldb, ldc};
-  auto it = st.plans.find(key);
-  if (it != st.plans.end()) return &it->second;
-  Plan &p = st.plans[key];
+  return &st;
+}
+
+// The plan for kind 0 (bf16) or 1 (fp8 with vector scales).
+Plan *plan_for(int device, State &st, int kind, int M, int N, int K, int lda, int ldb, int ldc) {
+  const PlanKey key{device, kind, M, N, K, lda, ldb, ldc};
+  auto it = g_plans.find(key);
+  if (it != g_plans.end()) return &it->second;
+  Plan &p = g_plans[key];
   const hipDataType in = kind == 0 ? HIP_R_16BF : HIP_R_8F_E4M3;
   const hipblasOperation_t opa = kind == 0 ? HIPBLAS_OP_N : HIPBLAS_OP_T, opb = HIPBLAS_OP_N;
   bool ok = hipblasLtMatmulDescCreate(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS;
@@ -123,50 +139,53 @@ Plan *plan_for(sh_ctx *ctx, int kind, int M, int N, int K, int lda, int ldb, int
   return &p;
 }
 
-int run(sh_ctx *ctx, hipStream_t s, int kind, const void *first, const void *second,
-        const float *first_scale, const float *second_scale, void *C, int M, int N, int K,
-        int lda, int ldb, int ldc) {
-  if (!enabled()) return SH_ERR_UNSUPPORTED;
+int run(hipStream_t s, int kind, const void *first, const void *second, const float *first_scale,
+        const float *second_scale, void *C, int M, int N, int K, int lda, int ldb, int ldc) {
+  if (M <= 0 || N <= 0 || K <= 0) return fail(kUnsupported, "empty GEMM");
   std::lock_guard<std::mutex> lock(g_mu);
-  Plan *p = plan_for(ctx, kind, M, N, K, lda, ldb, ldc);
-  if (!p || !p->ok) return SH_ERR_UNSUPPORTED;
-  State &st = g_states[ctx];
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return fail(kErrHip, "hipGetDevice failed");
+  State *st = state_for(device);
+  if (!st) return fail(kErrHip, "creating the hipBLASLt handle / workspace failed");
+  Plan *p = plan_for(device, *st, kind, M, N, K, lda, ldb, ldc);
+  if (!p->ok) return fail(kUnsupported, "hipBLASLt has no algorithm for this shape");
   if (kind == 1) {
     if (hipblasLtMatmulDescSetAttribute(p->op, HIPBLASLT_MATMUL_DESC_A_SCALE_POINTER, &first_scale,
                                         sizeof first_scale) != HIPBLAS_STATUS_SUCCESS ||
         hipblasLtMatmulDescSetAttribute(p->op, HIPBLASLT_MATMUL_DESC_B_SCALE_POINTER, &second_scale,
                                         sizeof second_scale) != HIPBLAS_STATUS_SUCCESS)
-      return fail(SH_ERR_HIP, "hipBLASLt: setting the scale vectors failed");
+      return fail(kErrHip, "hipBLASLt: setting the scale vectors failed");
   }
   const float alpha = 1.0f, beta = 0.0f;
-  const hipblasStatus_t r = hipblasLtMatmul(st.handle, p->op, &alpha, first, p->a, second, p->b,
-                                            &beta, C, p->c, C, p->c, &p->algo, st.workspace,
+  const hipblasStatus_t r = hipblasLtMatmul(st->handle, p->op, &alpha, first, p->a, second, p->b,
+                                            &beta, C, p->c, C, p->c, &p->algo, st->workspace,
                                             kWorkspaceBytes, s);
-  if (r != HIPBLAS_STATUS_SUCCESS) return fail(SH_ERR_HIP, "hipblasLtMatmul failed (status %d)", (int)r);
-  return SH_OK;
+  if (r != HIPBLAS_STATUS_SUCCESS) return fail(kErrHip, "hipblasLtMatmul failed (status %d)", (int)r);
+  return kOk;
 }
 
 }  // namespace
 
-int blaslt_gemm_bf16(sh_ctx *ctx, hipStream_t s, const uint16_t *A, const uint16_t *B, uint16_t *C,
-                     int M, int N, int K, int lda, int ldb, int ldc) {
-  return run(ctx, s, 0, B, A, nullptr, nullptr, C, M, N, K, lda, ldb, ldc);
+SHY_API const char *shy_last_error(void) { return g_error; }
+
+SHY_API int shy_gemm_bf16(void *stream, const uint16_t *A, const uint16_t *B, uint16_t *C, int M,
+                          int N, int K, int lda, int ldb, int ldc) {
+  return run(static_cast<hipStream_t>(stream), 0, B, A, nullptr, nullptr, C, M, N, K, lda, ldb, ldc);
 }
 
-int blaslt_gemm_fp8(sh_ctx *ctx, hipStream_t s, const uint8_t *A, const float *sa,
-                    const uint8_t *Bt, const float *sb, uint16_t *C, int M, int N, int K, int lda,
-                    int ldb, int ldc) {
-  return run(ctx, s, 1, Bt, A, sb, sa, C, M, N, K, lda, ldb, ldc);
+SHY_API int shy_gemm_fp8(void *stream, const uint8_t *A, const float *sa, const uint8_t *Bt,
+                         const float *sb, uint16_t *C, int M, int N, int K, int lda, int ldb,
+                         int ldc) {
+  return run(static_cast<hipStream_t>(stream), 1, Bt, A, sb, sa, C, M, N, K, lda, ldb, ldc);
 }
 
-void blaslt_release(sh_ctx *ctx) {
+SHY_API void shy_release(void) {
   std::lock_guard<std::mutex> lock(g_mu);
-  auto it = g_states.find(ctx);
-  if (it == g_states.end()) return;
-  for (auto &kv : it->second.plans) destroy_plan(kv.second);
-  if (it->second.handle) hipblasLtDestroy(it->second.handle);
-  if (it->second.workspace) (void)hipFree(it->second.workspace);
-  g_states.erase(it);
+  for (auto &kv : g_plans) destroy_plan(kv.second);
+  g_plans.clear();
+  for (auto &kv : g_states) {
+    if (kv.second.handle) hipblasLtDestroy(kv.second.handle);
+    if (kv.second.workspace) (void)hipFree(kv.second.workspace);
+  }
+  g_states.clear();
 }
-
-}  // namespace sh

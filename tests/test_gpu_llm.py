@@ -189,6 +189,75 @@ def test_qwen3_small_per_op_kernels_greedy(ctx, monkeypatch):
         _greedy_check(m, prompt, 96, "qwen3-small-per-op")
 
 
+def test_qwen3_small_head_as_separate_kernels(ctx, monkeypatch):
+    # STRICT_HIP_LLM_HEAD=0: the decode-layers kernel ends with the last layer
+    # and the final norm and LM head run as their own kernels
+    monkeypatch.setenv("STRICT_HIP_LLM_HEAD", "0")
+    with llm.Model(ctx, QWEN_SMALL) as m:
+        assert m.uses_layers_kernel
+        m.init_random(seed=7, stddev=0.02)
+        _randomize_small_params(m, 1)
+        prompt = np.random.default_rng(3).integers(0, QWEN_SMALL.vocab, 16)
+        _greedy_check(m, prompt, 64, "qwen3-small-head-separate")
+
+
+def test_qwen3_small_cooperative_launch(ctx, monkeypatch):
+    # STRICT_HIP_LLM_COOP=1: the decode-layers kernel goes through HIP's
+    # cooperative launch (residency guaranteed)
+    monkeypatch.setenv("STRICT_HIP_LLM_COOP", "1")
+    with llm.Model(ctx, QWEN_SMALL) as m:
+        assert m.uses_layers_kernel
+        m.init_random(seed=7, stddev=0.02)
+        _randomize_small_params(m, 1)
+        prompt = np.random.default_rng(3).integers(0, QWEN_SMALL.vocab, 16)
+        _greedy_check(m, prompt, 64, "qwen3-small-coop")
+
+
+@pytest.mark.parametrize("cfg", [QWEN_SMALL, GPT2_SMALL_TEST], ids=["qwen3", "gpt2"])
+def test_per_op_path_without_graphs(ctx, monkeypatch, cfg):
+    # STRICT_HIP_LLM_GRAPHS=0: the per-op path enqueues every kernel of a
+    # step eagerly instead of replaying its captured graph; tokens and
+    # logits equal the graph-replayed run's
+    monkeypatch.setenv("STRICT_HIP_LLM_LAYERS", "0")
+    prompt = np.random.default_rng(21).integers(0, cfg.vocab, 10)
+    runs = []
+    for graphs in ("1", "0"):
+        monkeypatch.setenv("STRICT_HIP_LLM_GRAPHS", graphs)
+        with llm.Model(ctx, cfg) as m:
+            m.init_random(seed=9, stddev=0.02)
+            m.reset(1)
+            toks = m.generate(prompt[None, :], 24)[0]
+            runs.append((toks, m.logits()[0].copy()))
+    assert np.array_equal(runs[0][0], runs[1][0])
+    assert np.array_equal(runs[0][1], runs[1][1])
+
+
+def test_decode_layers_wait_failure_reported_and_reset_recovers(ctx):
+    # The bounded waits of the decode-layers kernel: the host sets the sticky
+    # error word before a step, so every wait between workgroups gives up
+    # after a few polls and the kernel ends normally; sh_llm_next_tokens
+    # reports the failed step, and sh_llm_reset clears the error.
+    prompt = np.random.default_rng(5).integers(0, QWEN_SMALL.vocab, 12)
+    with llm.Model(ctx, QWEN_SMALL) as m:
+        assert m.uses_layers_kernel
+        m.init_random(seed=7, stddev=0.02)
+        m.reset(1)
+        expected = m.generate(prompt[None, :], 6)[0]
+        m.reset(1)
+        for i, t in enumerate(prompt):
+            m.step([int(t)], logits=(i == len(prompt) - 1))
+        m.write("layers.err", 0, np.array([1], np.uint32))
+        m.step(None, logits=True)
+        with pytest.raises(strict_amd.StrictHipError) as e:
+            m.next_tokens()
+        assert "timed out" in str(e.value)
+        assert m.read("layers.err", 0, np.uint32)[0] != 0
+        m.reset(1)
+        assert m.read("layers.err", 0, np.uint32)[0] == 0
+        again = m.generate(prompt[None, :], 6)[0]
+        assert np.array_equal(again, expected)
+
+
 def test_gpt2_small_shape_greedy_256(ctx):
     with llm.Model(ctx, GPT2_SMALL_TEST) as m:
         m.init_random(seed=8, stddev=0.02)
@@ -207,26 +276,136 @@ def test_gpt2_config3_greedy_256(ctx):
         _greedy_check(m, prompt, 256, "gpt2-config3")
 
 
-def test_qwen3_config4_greedy(ctx):
-    # BASELINE configs[4] model at batch 1 (short prompt and 32 steps here; the
-    # 4096-token KV cache is covered by test_qwen3_long_context_step)
-    cfg = llm.QWEN3_0_6B.with_(max_positions=512)
-    with llm.Model(ctx, cfg) as m:
-        assert m.uses_layers_kernel
-        m.init_random(seed=42, stddev=0.02)
-        prompt = np.random.default_rng(42).integers(0, cfg.vocab, 32)
-        _greedy_check(m, prompt, 32, "qwen3-config4")
+# ---- configs[4] at its own shape: one model, max_batch 16, KV room for 4096+ --------
+
+QWEN_CONFIG4 = llm.QWEN3_0_6B.with_(max_positions=4096 + 64, max_batch=16)
 
 
-def test_qwen3_long_context_step(ctx):
+@pytest.fixture(scope="module")
+def config4(ctx):
+    """The configs[4] model (28 layers, hidden 1024, 16 Q / 8 KV heads, head_dim
+    128, SwiGLU 3072, vocab 151936, FP8 weights) and its dequantized weights
+    for the oracle, shared by the configs[4] tests."""
+    m = llm.Model(ctx, QWEN_CONFIG4)
+    m.init_random(seed=42, stddev=0.02)
+    assert m.uses_layers_kernel
+    weights = ollm.load_from_model(m)
+    yield m, weights
+    m.close()
+
+
+def _batch_greedy_check(model, weights, prompts, steps, label):
+    """Every row of a batched GPU run against its own teacher-forced oracle
+    decoder: logits within LOGIT_REL_TOL, greedy tokens identical except at
+    oracle near-ties. Returns (max logit diff, mismatches, near-ties, decoders)."""
+    B = prompts.shape[0]
+    model.reset(B)
+    for i in range(prompts.shape[1]):
+        model.step(prompts[:, i], logits=(i == prompts.shape[1] - 1))
+    gpu_tokens, gpu_logits = [], []
+    for j in range(steps):
+        gpu_logits.append(model.logits().copy())
+        gpu_tokens.append(model.next_tokens().copy())
+        if j + 1 < steps:
+            model.step(None, logits=True)
+    gpu_tokens = np.array(gpu_tokens)  # [steps, B]
+    max_diff, scale, mism, ties, decs = 0.0, 0.0, 0, 0, []
+    for b in range(B):
+        dec = ollm.Decoder(weights)
+        ours, margins, ref = ollm.greedy_compare(gpu_tokens[:, b], dec, prompts[b], steps)
+        d = max(float(np.max(np.abs(g[b] - r))) for g, r in zip(gpu_logits, ref))
+        sc = max(float(np.max(np.abs(r))) for r in ref)
+        bad = gpu_tokens[:, b] != ours
+        assert d <= LOGIT_REL_TOL * sc, (b, d, sc)
+        assert not np.any(bad & (margins >= 2 * d)), (b, np.nonzero(bad)[0])
+        max_diff, scale = max(max_diff, d), max(scale, sc)
+        mism += int(bad.sum())
+        ties += int(np.sum(bad & (margins < 2 * d)))
+        decs.append(dec)
+    print(f"[{label}] B={B}, {steps} steps: logit max-abs-diff {max_diff:.3e} (max |logit| "
+          f"{scale:.3f}), token mismatches {mism} (near-ties {ties})")
+    return max_diff, mism, ties, decs
+
+
+def _check_kv_cache(model, decs, label):
+    """The K and V^T caches the decode-layers kernel appended (q/k RMSNorm,
+    RoPE, cache layout) against the oracle decoders' caches, every layer and
+    row: max |gpu - oracle| <= 1e-2 * max |oracle| (attention's bar)."""
+    c = model.cfg
+    vt = (c.max_positions + 15) // 16 * 16
+    worst = 0.0
+    for li in range(c.layers):
+        k = oracle.f16_to_f32(model.read("kcache", li, np.uint16)).reshape(
+            c.max_batch, c.kv_heads, -1, c.head_dim)
+        v = oracle.f16_to_f32(model.read("vcache", li, np.uint16)).reshape(
+            c.max_batch, c.kv_heads, c.head_dim, vt)
+        for b, dec in enumerate(decs):
+            P = dec.k[li].shape[0]  # prompt + steps - 1 positions on both sides
+            kr = dec.k[li][:P].transpose(1, 0, 2)       # [kvh, P, d]
+            vr = dec.v[li][:P].transpose(1, 2, 0)       # [kvh, d, P]
+            for got, ref in ((k[b, :, :P], kr), (v[b, :, :, :P], vr)):
+                rel = float(np.max(np.abs(got - ref)) / np.max(np.abs(ref)))
+                assert rel <= 1e-2, (li, b, rel)
+                worst = max(worst, rel)
+    print(f"[{label}] K / V caches: max |gpu - oracle| / max |oracle| = {worst:.3e}")
+
+
+def test_qwen3_config4_greedy_256(ctx, config4):
+    # BASELINE configs[4] at batch 1: 32-token prompt, 256 greedy steps
+    m, w = config4
+    prompt = np.random.default_rng(42).integers(0, QWEN_CONFIG4.vocab, (1, 32))
+    _batch_greedy_check(m, w, prompt, 256, "qwen3-config4-b1")
+
+
+@pytest.mark.parametrize("batch", [4, 16])
+def test_qwen3_config4_batch_vs_oracle(ctx, config4, batch):
+    # configs[4] at batch 4 and 16: every row its own prompt, each checked
+    # against its own oracle decoder (b = 16: four staging passes of 4 rows)
+    m, w = config4
+    prompts = np.random.default_rng(100 + batch).integers(0, QWEN_CONFIG4.vocab, (batch, 12))
+    _, _, _, decs = _batch_greedy_check(m, w, prompts, 8, f"qwen3-config4-b{batch}")
+    _check_kv_cache(m, decs, f"qwen3-config4-b{batch}")
+
+
+def test_qwen3_config4_batch16_kv4096_rows_match_single(ctx, config4):
+    # configs[4] at batch 16 over a 4096-token KV cache: rows from every
+    # staging pass (0, 5, 10, 15) against batch-1 runs of the same prompts
+    m, _ = config4
+    prompts = np.random.default_rng(7).integers(0, QWEN_CONFIG4.vocab, (16, 4096))
+    steps = 4
+    m.reset(16)
+    for i in range(prompts.shape[1]):
+        m.step(prompts[:, i], logits=(i == prompts.shape[1] - 1))
+    toks, logits = [], []
+    for j in range(steps):
+        logits.append(m.logits().copy())
+        toks.append(m.next_tokens().copy())
+        if j + 1 < steps:
+            m.step(None, logits=True)
+    worst = 0.0
+    for b in (0, 5, 10, 15):
+        m.reset(1)
+        for i in range(prompts.shape[1]):
+            m.step(prompts[b:b + 1, i], logits=(i == prompts.shape[1] - 1))
+        for j in range(steps):
+            single = m.logits()[0]
+            d = float(np.max(np.abs(single - logits[j][b])))
+            assert d <= LOGIT_REL_TOL * float(np.max(np.abs(single))), (b, j, d)
+            worst = max(worst, d)
+            assert int(m.next_tokens()[0]) == int(toks[j][b]), (b, j)
+            if j + 1 < steps:
+                m.step(None, logits=True)
+    print(f"[qwen3-config4-b16-kv4096] rows 0/5/10/15 vs batch 1: tokens identical, "
+          f"logit max-abs-diff {worst:.3e}")
+
+
+def test_qwen3_long_context_step(ctx, config4):
     # BASELINE configs[4] KV length: a 4096-token prompt fills the cache, then
     # greedy steps attend over 4096+ positions (split-K attention with many
     # splits and the cross-workgroup merge)
-    cfg = llm.QWEN3_0_6B.with_(max_positions=4096 + 8)
-    with llm.Model(ctx, cfg) as m:
-        m.init_random(seed=5, stddev=0.02)
-        prompt = np.random.default_rng(6).integers(0, cfg.vocab, 4096)
-        _greedy_check(m, prompt, 4, "qwen3-config4-kv4096")
+    m, w = config4
+    prompt = np.random.default_rng(6).integers(0, QWEN_CONFIG4.vocab, (1, 4096))
+    _batch_greedy_check(m, w, prompt, 4, "qwen3-config4-kv4096")
 
 
 def test_inv_freq_table(ctx):

@@ -261,3 +261,79 @@ def test_gemm_matches_numpy():
     assert np.max(np.abs(oracle.gemm_f32(a, b) - ref)) < 1e-5
     eye = np.eye(53, dtype=np.float32)
     assert np.array_equal(oracle.gemm_f32(a, eye), a)
+
+
+# ---- TestPerformance's CPU modes and the CUDA harness's cross blur ------------------
+
+def _chunked_prefix(n, mode, chunk=oracle.CHUNK_SIZE):
+    """Indices a mode computes: all of them, or whole chunks only (Iterations /
+    ChunkSize chunks, TestPerformance.cs:41, :48)."""
+    return n if mode in (0, 2) else n // chunk * chunk
+
+
+@pytest.mark.parametrize("mode", range(4))
+def test_perf_modes_sigmoid_equal_the_array_oracle(mode):
+    # every mode computes SigmoidPerformanceTests.cs:27 per element: the same
+    # bits as or_sigmoid_f32 on the indices it covers (parallel == serial)
+    x = np.random.default_rng(1).uniform(-8, 8, 100_037).astype(np.float32)
+    y = np.full_like(x, np.nan)
+    oracle.perf_sigmoid(mode, x, y, nthreads=4)
+    n = _chunked_prefix(x.size, mode)
+    ref = oracle.sigmoid_f32(x)
+    assert np.array_equal(y[:n].view(np.uint32), ref[:n].view(np.uint32))
+    assert np.all(np.isnan(y[n:]))
+
+
+@pytest.mark.parametrize("mode", range(4))
+def test_perf_modes_brightness_and_blurs_equal_the_image_oracles(mode):
+    w, h = 61, 23
+    img = np.random.default_rng(2).integers(0, 256, w * h * 4, dtype=np.uint8)
+    n = _chunked_prefix(w * h, mode)
+    out = np.zeros_like(img)
+    oracle.perf_brightness(mode, img, out, 4, -40, nthreads=3)
+    assert np.array_equal(out[:n * 4], oracle.adjust_brightness(img, -40, 4)[:n * 4])
+    cases = [(oracle.BLUR_REFERENCE, 0, oracle.blur5_reference(img, w, h, 4)),
+             (oracle.BLUR_CONFIG, 0, oracle.blur5_config(img, w, h, 4)),
+             (oracle.BLUR_FUSED, 40, oracle.brightness_blur5_config(img, w, h, 40, 4))]
+    for kind, delta, ref in cases:
+        out = np.zeros_like(img)
+        oracle.perf_blur5(mode, kind, img, out, w, h, 4, nthreads=3, delta=delta)
+        assert np.array_equal(out[:n * 4], ref[:n * 4]), kind
+        assert not out[n * 4:].any()
+
+
+def test_cross_blur_hand_worked_single_thread():
+    # Cuda.Tests/BlurPerformanceTests.cs:160-169 worked by hand on a 2x1 RGBA
+    # image (size 8, width * 4 = 8): indices 0..7 are skipped (:162), and for
+    # n >= 8 the five taps are n % 8 three times and (n + 4) % 8 twice, so
+    # b[n % 8] = (3 b[n % 8] + 2 b[(n + 4) % 8]) / 5, in place:
+    #   n=8: b0 = (30 + 100) / 5 = 26   n=12: b4 = (150 + 2*26) / 5 = 40
+    #   n=9: b1 = (60 + 120) / 5 = 36   n=13: b5 = (180 + 2*36) / 5 = 50
+    #  n=10: b2 = (90 + 140) / 5 = 46   n=14: b6 = (210 + 2*46) / 5 = 60
+    #  n=11: b3 = (120 + 160) / 5 = 56  n=15: b7 = (240 + 2*56) / 5 = 70
+    img = np.array([10, 20, 30, 40, 50, 60, 70, 80], np.uint8)
+    oracle.perf_cross_blur(oracle.PERF_MODES.index("SingleThread"), img, 2, 1, 16, nthreads=1)
+    assert img.tolist() == [26, 36, 46, 56, 40, 50, 60, 70]
+
+
+def test_cross_blur_hand_worked_chunks_skip_whole_chunks():
+    # SingleThreadChunks with ChunkSize 5 and 20 iterations: chunks start at
+    # 0, 5, 10, 15; the chunks at 0 and 5 start below width * 4 = 8 and are
+    # skipped whole (so n = 8, 9 never run), then n = 10..19 in order:
+    #  n=10: b2 = (90 + 2*70) / 5 = 46   n=15: b7 = (240 + 2*56) / 5 = 70
+    #  n=11: b3 = (120 + 2*80) / 5 = 56  n=16: b0 = (30 + 2*34) / 5 = 19
+    #  n=12: b4 = (150 + 2*10) / 5 = 34  n=17: b1 = (60 + 2*44) / 5 = 29
+    #  n=13: b5 = (180 + 2*20) / 5 = 44  n=18: b2 = (138 + 2*60) / 5 = 51
+    #  n=14: b6 = (210 + 2*46) / 5 = 60  n=19: b3 = (168 + 2*70) / 5 = 61
+    img = np.array([10, 20, 30, 40, 50, 60, 70, 80], np.uint8)
+    oracle.perf_cross_blur(oracle.PERF_MODES.index("SingleThreadChunks"), img, 2, 1, 20,
+                           nthreads=1, chunk=5)
+    assert img.tolist() == [19, 29, 51, 61, 34, 44, 60, 70]
+
+
+@pytest.mark.parametrize("mode", range(4))
+def test_cross_blur_keeps_a_constant_image(mode):
+    # five equal taps average to the same value, in every mode (even racing)
+    img = np.full(64 * 32 * 4, 173, np.uint8)
+    oracle.perf_cross_blur(mode, img, 64, 32, 64 * 32 * 4 * 3, nthreads=4)
+    assert np.all(img == 173)
