@@ -19,6 +19,14 @@ configs[1], the unfused pipeline, sigmoid, the bf16 GEMM
 (configs[2]), the FP8 GEMV at the LM-head shape, Qwen3 decode at b=4 and
 b=16, GPT-2 (configs[3]) decode.
 
+Every row carries a cpu_baseline timed on this host after the GPU work: the
+reference's own CPU code restated in C (oracle/oracle.c) in TestPerformance's
+four modes (SingleThread, SingleThreadChunks, ParallelCpu, ParallelCpuChunks;
+TestPerformance.cs:34-49) for sigmoid, brightness and the blurs, plus the
+CUDA harness's cross blur at its own 2048x1024 size; the build's numpy
+oracle ("port") for the GEMMs, the GEMV and the decoders, which the
+reference does not have.
+
 Timing: two HIP events on the library context's stream (where the kernels
 run) bracket K back-to-back launches after W warmup launches. Inputs of the
 memory-bound kernels rotate over >= 1 GiB of buffers so the 256 MB MALL
@@ -423,39 +431,203 @@ def cpu_baseline_decode(seconds: float):
                       f"dequantized weights, BLAS over up to {nt} threads, {t_total:.1f} s"}
 
 
-def cpu_baseline_image(seconds: float):
+def _modes_entry(times_ms: dict, unit_per_ms: float, unit: str, sample: str, nt: int) -> dict:
+    """A cpu_baseline object from TestPerformance's four modes: `value` is the
+    best mode's rate, `modes` every mode's rate and wall time."""
+    rates = {m: round(unit_per_ms / t, 4) for m, t in times_ms.items()}
+    best = max(rates, key=rates.get)
+    return {"value": rates[best], "unit": unit, "cores": nt, "host_cpus": os.cpu_count(),
+            "kind": "port", "best_mode": best, "modes": rates,
+            "modes_ms": {m: round(t, 2) for m, t in times_ms.items()}, "sample": sample}
+
+
+def cpu_modes(fn) -> dict:
     import oracle
 
-    img = np.random.default_rng(42).integers(0, 256, IMG_BYTES, dtype=np.uint8)
+    return {name: fn(mode) for mode, name in enumerate(oracle.PERF_MODES)}
+
+
+def cpu_baseline_sigmoid():
+    """SigmoidPerformanceTests.cs:24-28 over the config's 2^24-float array in
+    TestPerformance's four modes (TestPerformance.cs:34-49), C restatement."""
+    import oracle
+
     nt = cpu_threads()
-    reps, t_total = 0, 0.0
-    while t_total < seconds and reps < 50:
-        t0 = time.perf_counter()
-        oracle.brightness_blur5_config(img, IMG_W, IMG_H, 40, 4, nthreads=nt)
-        t_total += time.perf_counter() - t0
-        reps += 1
-    gbs = 2 * IMG_BYTES * reps / t_total / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": nt, "kind": "port",
-            "sample": f"{reps} x fused brightness(+40)+5x5 blur on the 4096x4096 RGBA8 config "
-                      f"image, C restatement (oracle/oracle.c) over {nt} threads, "
-                      f"{t_total:.1f} s wall"}
-
-
-def cpu_baseline_sigmoid(seconds: float):
-    import oracle
-
     x = np.random.default_rng(42).uniform(-8, 8, SIGMOID_N).astype(np.float32)
+    y = np.empty_like(x)
+    t = cpu_modes(lambda m: oracle.perf_sigmoid(m, x, y, nt))
+    return _modes_entry(t, 8 * SIGMOID_N / 1e6, "GB/s", (
+        f"sigmoid over all 2^24 config floats (SigmoidPerformanceTests.cs:27 restated in C, "
+        f"double exp), each TestPerformance mode (chunk {oracle.CHUNK_SIZE}) once, parallel "
+        f"modes over {nt} threads"), nt)
+
+
+def cpu_baseline_image_rows():
+    """CPU baselines of the image rows: brightness over the whole config image,
+    the blurs on a 256-row band of it, each in the four TestPerformance modes;
+    plus the CUDA harness's own CPU blur (the cross stencil behind the
+    reference's published blur timings) at the reference's 2048x1024 size."""
+    import oracle
+
     nt = cpu_threads()
+    img = np.random.default_rng(42).integers(0, 256, IMG_BYTES, dtype=np.uint8)
+    out = np.empty_like(img)
+    px = IMG_W * IMG_H
+    band = 256 * IMG_W  # pixels of the blur sample
+    res = {}
+    t = cpu_modes(lambda m: oracle.perf_brightness(m, img, out, 4, 40, nt))
+    res["brightness"] = _modes_entry(t, 8 * px / 1e6, "GB/s", (
+        f"AdjustPixelBrightness (Assembly BlurPerformanceTests.cs:287-294) +40 on all "
+        f"{IMG_W}x{IMG_H} RGBA pixels, C restatement, each mode once, {nt} threads"), nt)
+    for key, kind, delta, what in (
+            ("box_blur", oracle.BLUR_CONFIG, 0, "5x5 box blur, config semantics"),
+            ("fused", oracle.BLUR_FUSED, 40, "brightness(+40) then 5x5 box blur (config)"),
+            ("blur_reference", oracle.BLUR_REFERENCE, 0,
+             "5x5 blur, reference semantics (Assembly BlurPerformanceTests.cs:53-141)")):
+        t = cpu_modes(lambda m: oracle.perf_blur5(m, kind, img, out, IMG_W, IMG_H, 4, nt,
+                                                  delta=delta, pixels=band))
+        res[key] = _modes_entry(t, 8 * band / 1e6, "GB/s", (
+            f"{what}: output pixels of the first 256 rows of the {IMG_W}x{IMG_H} RGBA image "
+            f"(8 B/px), C restatement, each mode once, {nt} threads"), nt)
+    w, h = 2048, 1024
+    iters = w * h * 100
+    base = np.random.default_rng(42).integers(0, 256, w * h * 4, dtype=np.uint8)
+    t = {}
+    for mode, name in enumerate(oracle.PERF_MODES):
+        im = base.copy()
+        t[name] = oracle.perf_cross_blur(mode, im, w, h, iters, nt)
+    e = _modes_entry(t, iters / 1e6, "G updates/s", (
+        f"the CUDA harness's CPU blur (Cuda BlurPerformanceTests.cs:160-169: in-place 5-point "
+        f"cross /5 over the RGBA bytes, modulo-wrapped) on {w}x{h}, {iters} iterations "
+        f"(width*height*100, its logged count), C restatement, each mode once, {nt} threads"), nt)
+    e["reference_published_ms"] = {"SingleThread": 4594, "SingleThreadChunks": 2234,
+                                   "ParallelCpu": 701, "ParallelCpuChunks": 296,
+                                   "hardware": "unstated (Cuda BlurPerformanceTests.cs:20-24)"}
+    res["cross_blur"] = e
+    return res
+
+
+def cpu_baseline_gemm():
+    """The oracle's fp32 product (numpy BLAS) of the 4096^3 operands: the
+    reference has no GEMM, so the build's own fp32 path is the baseline."""
+    nt = cpu_threads()
+    rng = np.random.default_rng(42)
+    a = rng.standard_normal((GEMM_N, GEMM_N), dtype=np.float32)
+    b = rng.standard_normal((GEMM_N, GEMM_N), dtype=np.float32)
+    a @ b[:, :256]  # BLAS threads up
+    t0 = time.perf_counter()
+    a @ b
+    dt = time.perf_counter() - t0
+    return {"value": round(2.0 * GEMM_N ** 3 / dt / 1e12, 4), "unit": "TFLOP/s", "cores": nt,
+            "host_cpus": os.cpu_count(), "kind": "port",
+            "sample": f"one fp32 4096^3 product of dequantized operands (numpy BLAS, the "
+                      f"tests' fp32 reference), {dt * 1e3:.0f} ms, BLAS over up to {nt} threads"}
+
+
+def cpu_baseline_gemv():
+    """The oracle's LM-head GEMV: fp32 dequantized [151936 x 1024] weights times
+    one fp16 row (numpy BLAS); algorithmic bytes counted as the FP8 kernel's."""
+    nt = cpu_threads()
+    n, k = 151936, 1024
+    w = np.random.default_rng(1).standard_normal((n, k), dtype=np.float32)
+    x = np.random.default_rng(2).standard_normal(k).astype(np.float32)
+    w @ x
     reps, t_total = 0, 0.0
-    while t_total < seconds and reps < 50:
+    while reps < 5:
         t0 = time.perf_counter()
-        oracle.sigmoid_f32(x, nthreads=nt)
+        w @ x
         t_total += time.perf_counter() - t0
         reps += 1
-    gbs = 8 * SIGMOID_N * reps / t_total / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": nt, "kind": "port",
-            "sample": f"{reps} x sigmoid over 2^24 floats (SigmoidPerformanceTests.cs:27 "
-                      f"restated in C, double exp) over {nt} threads, {t_total:.1f} s wall"}
+    ms = t_total / reps * 1e3
+    alg = n * k + n * 4 + k * 2 + n * 4
+    return {"value": round(alg / (ms * 1e-3) / 1e9, 3), "unit": "GB/s (FP8-equivalent bytes)",
+            "cores": nt, "host_cpus": os.cpu_count(), "kind": "port",
+            "sample": f"{reps} fp32 GEMVs 151936x1024 (numpy BLAS, dequantized weights), "
+                      f"{ms:.1f} ms each, up to {nt} threads"}
+
+
+def cpu_baseline_gpt2(seconds: float):
+    """numpy oracle of the GPT-2 configs[3] decode step at b=1 after a 128-token prompt."""
+    import oracle.llm as ollm
+    from strict_amd import llm
+
+    cfg = llm.GPT2_SMALL
+    nt = cpu_threads()
+    rng = np.random.default_rng(0)
+    shapes = llm.linear_shapes(cfg)
+    layers = []
+    for _ in range(cfg.layers):
+        L = {}
+        for name in ("qkv", "o", "fc", "proj"):
+            r, c = shapes[name]
+            L[name] = rng.standard_normal((r, c), dtype=np.float32) * np.float32(0.02)
+            L[name + ".scale"] = np.ones(r, np.float32)
+            L[name + ".bias"] = np.zeros(r, np.float32)
+        for name in ("norm1", "norm2"):
+            L[name + ".g"] = np.ones(cfg.hidden, np.float32)
+            L[name + ".b"] = np.zeros(cfg.hidden, np.float32)
+        layers.append(L)
+    r, c = shapes["head"]
+    w = ollm.Weights(cfg, layers, rng.standard_normal((r, c), dtype=np.float32) * np.float32(0.02),
+                     np.ones(r, np.float32), np.ones(cfg.hidden, np.float32),
+                     np.zeros(cfg.hidden, np.float32),
+                     wpe=rng.standard_normal((cfg.max_positions, cfg.hidden), dtype=np.float32)
+                     * np.float32(0.02))
+    dec = ollm.Decoder(w)
+    logits = dec.forward(rng.integers(0, cfg.vocab, 128))[-1]
+    steps, t_total = 0, 0.0
+    while t_total < seconds and steps < 128:
+        t0 = time.perf_counter()
+        logits = dec.forward([int(np.argmax(logits))])[-1]
+        t_total += time.perf_counter() - t0
+        steps += 1
+    return {"value": round(steps / t_total, 3), "unit": "tokens/s", "cores": nt,
+            "host_cpus": os.cpu_count(), "kind": "port",
+            "sample": f"{steps} greedy steps of the numpy oracle (oracle/llm.py) of GPT-2 small "
+                      f"after a 128-token prompt, fp32 weights, BLAS over up to {nt} threads, "
+                      f"{t_total:.1f} s"}
+
+
+def attach_cpu_baselines(kernels, headline_cpu, seconds):
+    """One cpu_baseline per kernels[] row (reported beside the GPU figure, not a target)."""
+    rows = {}
+    log("cpu baselines: image rows (TestPerformance modes)")
+    img = cpu_baseline_image_rows()
+    log("cpu baselines: sigmoid")
+    rows["sigmoid"] = cpu_baseline_sigmoid()
+    log("cpu baselines: GEMM / GEMV")
+    gemm = cpu_baseline_gemm()
+    gemv = cpu_baseline_gemv()
+    log("cpu baselines: GPT-2 oracle")
+    gpt2 = cpu_baseline_gpt2(min(seconds, 5.0))
+    for e in kernels:
+        name = e["kernel"]
+        if name.startswith("copy_u8"):
+            cb = dict(img["cross_blur"])
+            cb["sample"] = ("the reference's CudaGpu leg is this same byte copy; its CPU side is "
+                            "the cross blur: " + cb["sample"])
+        elif name.startswith("brightness_u8"):
+            cb = img["brightness"]
+        elif name.startswith("box_blur5_u8"):
+            cb = img["box_blur"]
+        elif name.startswith("brightness_blur5_u8") or name.startswith("brightness_then_blur"):
+            cb = img["fused"]
+        elif name.startswith("sigmoid"):
+            cb = rows["sigmoid"]
+        elif name.startswith("gemm_"):
+            cb = gemm
+        elif name.startswith("gemv"):
+            cb = gemv
+        elif name.startswith("gpt2"):
+            cb = gpt2
+        elif name.startswith("qwen3") and headline_cpu is not None:
+            cb = dict(headline_cpu)
+            cb["sample"] = ("the oracle decodes every row on its own, so its rate at any batch "
+                            "is its batch-1 rate: " + headline_cpu["sample"])
+        else:
+            continue
+        e["cpu_baseline"] = cb
+    return img
 
 
 def main() -> int:
@@ -550,9 +722,15 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = {"decode": cpu_baseline_decode, "image": cpu_baseline_image,
-               "sigmoid": cpu_baseline_sigmoid}[args.workload](args.cpu_seconds)
+        if args.workload == "decode":
+            cpu = cpu_baseline_decode(args.cpu_seconds)
+        elif args.workload == "sigmoid":
+            cpu = cpu_baseline_sigmoid()
         log(f"cpu baseline: {cpu}")
+        if kernels or args.workload == "image":
+            img_rows = attach_cpu_baselines(kernels, cpu, args.cpu_seconds)
+            if args.workload == "image":
+                cpu = img_rows["fused"]
 
     line = {
         "metric": "HBM GB/s (% peak) per kernel; decode tokens/s Qwen3-0.6B-shape FP8 b=1",

@@ -321,6 +321,46 @@ SH_API int sh_pack_e4m3_tiles(sh_ctx *ctx, const uint8_t *q, int N, int K, uint8
 SH_API int sh_gemv_w8a16(sh_ctx *ctx, const uint16_t *x, const uint8_t *w_tiled,
                          const float *scales, float *y, int batch, int K, int N);
 
+/* ---- typed ops: decoder building blocks ---------------------------------------
+ * No reference counterpart (Strict has no LLM path): the operations of the
+ * GPT-2 and Qwen3 decoders, which the model runners below fuse into their
+ * kernels, as ops on the caller's device buffers. fp32 in and out; the norms
+ * take their statistics in fp64 and RoPE its cos / sin in fp64, every other
+ * product and sum is rounded in fp32 on its own. */
+
+/* y[r][i] = (x[r][i] * inv_r) * gain[i], inv_r = fp32(1 / sqrt(mean_i x[r][i]^2 + eps))
+ * (RMSNorm), rows of n values. in-place (y == x) is allowed. */
+SH_API int sh_rmsnorm_f32(sh_ctx *ctx, const float *x, const float *gain, float *y, int rows,
+                          int n, float eps);
+/* y[r][i] = ((x[r][i] - mean_r) * inv_r) * gain[i] + bias[i], inv_r = fp32(1 /
+ * sqrt(var_r + eps)) (LayerNorm, population variance). y == x is allowed. */
+SH_API int sh_layernorm_f32(sh_ctx *ctx, const float *x, const float *gain, const float *bias,
+                            float *y, int rows, int n, float eps);
+/* In place on x[rows][heads][head_dim]: rotate-half RoPE at positions[r]
+ * (device int32 per row): for i < head_dim / 2, angle = fp32(pos) *
+ * fp32(theta^(-2i / head_dim)), (x_i, x_{i+d/2}) <- (x_i c - x_{i+d/2} s,
+ * x_{i+d/2} c + x_i s). head_dim even, <= 512. */
+SH_API int sh_rope_f32(sh_ctx *ctx, float *x, const int32_t *positions, int rows, int heads,
+                       int head_dim, float theta);
+/* out[i] = silu(gate[i]) * up[i], silu(g) = g / (1 + exp(-g)) (SwiGLU). */
+SH_API int sh_swiglu_f32(sh_ctx *ctx, const float *gate, const float *up, float *out, size_t n);
+/* y[i] = 0.5 x (1 + tanh(sqrt(2 / pi) (x + 0.044715 x^3))) (GELU, tanh form). */
+SH_API int sh_gelu_f32(sh_ctx *ctx, const float *x, float *y, size_t n);
+/* index[r] = the first i of the largest x[r][i] (NaN counts as the largest,
+ * as numpy.argmax), rows of n >= 1 values (greedy decoding). */
+SH_API int sh_argmax_f32(sh_ctx *ctx, const float *x, int rows, int n, int32_t *index);
+/* Decode attention, grouped-query: for row b and query head h (KV head
+ * h / (heads / kv_heads)), with L = min(lengths[b], max_positions),
+ *   out[b][h] = sum_p softmax_p(fp32(q[b][h] * scale) . k[b][kvh][p]) v[b][kvh][p],  p < L
+ * (zeros for L <= 0). q, out fp32 [batch][heads][head_dim]; k, v fp16 [batch]
+ * [kv_heads][max_positions][head_dim] (the runners' cache layout), 16-byte
+ * aligned; lengths a device int32 [batch]. head_dim 64 or 128, heads /
+ * kv_heads <= 16. Split-K over positions: the split partials go to the
+ * context's work buffer (allocated on first use, grown on demand). */
+SH_API int sh_attn_decode_f16(sh_ctx *ctx, const float *q, const uint16_t *k, const uint16_t *v,
+                              const int32_t *lengths, float *out, int batch, int heads,
+                              int kv_heads, int head_dim, int max_positions, float scale);
+
 /* ---- LLM decode (model runners) ------------------------------------------------
  * No reference counterpart: BASELINE configs[3] (GPT-2 small, fp16 weights)
  * and configs[4] (Qwen3-0.6B shape, FP8-E4M3 weights with per-output-channel

@@ -80,6 +80,35 @@ def rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
     return np.concatenate([x1 * c - x2 * s, x2 * c + x1 * s], axis=-1).astype(np.float32)
 
 
+def attend(q: np.ndarray, k: np.ndarray, v: np.ndarray, visible=None) -> np.ndarray:
+    """softmax(q k^T) v in fp64 for query rows q [T, d] (already scaled) over
+    keys / values [P, d]; visible [T, P] (bool) hides positions where False."""
+    s = q.astype(np.float64) @ k.astype(np.float64).T
+    if visible is not None:
+        s = np.where(visible, s, -np.inf)
+    s = s - s.max(axis=1, keepdims=True)
+    e = np.exp(s)
+    return (e @ v.astype(np.float64)) / e.sum(axis=1, keepdims=True)
+
+
+def attn_decode(q: np.ndarray, k: np.ndarray, v: np.ndarray, lengths, scale: float) -> np.ndarray:
+    """Grouped-query decode attention: out[b, h] = attend(fp32(q[b, h] * scale),
+    k[b, h // G, :L], v[b, h // G, :L]) with L = min(lengths[b], P), zeros for
+    L <= 0; q [B, H, d] fp32, k / v [B, KVH, P, d], G = H / KVH."""
+    B, H, d = q.shape
+    KVH, P = k.shape[1], k.shape[2]
+    G = H // KVH
+    qs = (q.astype(np.float32) * np.float32(scale)).astype(np.float32)
+    out = np.zeros((B, H, d), np.float32)
+    for b in range(B):
+        L = min(int(lengths[b]), P)
+        if L <= 0:
+            continue
+        for h in range(H):
+            out[b, h] = attend(qs[b, h][None, :], k[b, h // G, :L], v[b, h // G, :L])[0]
+    return out
+
+
 class Weights:
     """Dequantized per-layer weights as fp32 [rows, cols] (logical order) with
     per-row scales (1 for fp16 models), norms and biases."""
@@ -153,15 +182,11 @@ class Decoder:
             K_, V_ = self.k[li], self.v[li]  # [P, KVH, d]
             P = K_.shape[0]
             out = np.empty((T, H, d), np.float32)
+            # causal: token t (absolute pos self.pos + t) sees positions <= it
+            visible = np.arange(P)[None, :] <= (self.pos + np.arange(T))[:, None]
             for hh in range(H):
                 kv = hh // G
-                s = (q[:, hh, :].astype(np.float64) @ K_[:, kv, :].astype(np.float64).T)
-                # causal: token t (absolute pos self.pos + t) sees positions <= it
-                mask = np.arange(P)[None, :] > (self.pos + np.arange(T))[:, None]
-                s = np.where(mask, -np.inf, s)
-                s = s - s.max(axis=1, keepdims=True)
-                e = np.exp(s)
-                out[:, hh, :] = (e @ V_[:, kv, :].astype(np.float64)) / e.sum(axis=1, keepdims=True)
+                out[:, hh, :] = attend(q[:, hh, :], K_[:, kv, :], V_[:, kv, :], visible)
             attn = f16(out.reshape(T, H * d))
             x = x + linear(attn, L["o"], L["o.scale"], L.get("o.bias"))
             h2 = self.norm(x, L["norm2.g"], L.get("norm2.b"))

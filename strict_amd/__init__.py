@@ -425,6 +425,37 @@ class Context:
         _check(self._l.sh_gemv_w8a16(self.handle, _ptr(x), _ptr(w_tiled), _ptr(scales), _ptr(y),
                                      batch, k, n))
 
+    # -- decoder building blocks (fp32 device buffers) --
+    def rmsnorm(self, x, gain, y, rows: int, n: int, eps: float) -> None:
+        """y = (x * fp32(1 / sqrt(mean(x^2) + eps))) * gain, per row of n."""
+        _check(self._l.sh_rmsnorm_f32(self.handle, _ptr(x), _ptr(gain), _ptr(y), rows, n, eps))
+
+    def layernorm(self, x, gain, bias, y, rows: int, n: int, eps: float) -> None:
+        _check(self._l.sh_layernorm_f32(self.handle, _ptr(x), _ptr(gain), _ptr(bias), _ptr(y),
+                                        rows, n, eps))
+
+    def rope(self, x, positions, rows: int, heads: int, head_dim: int, theta: float) -> None:
+        """Rotate-half RoPE in place on x [rows, heads, head_dim] at positions [rows] (int32)."""
+        _check(self._l.sh_rope_f32(self.handle, _ptr(x), _ptr(positions), rows, heads, head_dim,
+                                   theta))
+
+    def swiglu(self, gate, up, out, n: int) -> None:
+        _check(self._l.sh_swiglu_f32(self.handle, _ptr(gate), _ptr(up), _ptr(out), n))
+
+    def gelu(self, x, y, n: int) -> None:
+        _check(self._l.sh_gelu_f32(self.handle, _ptr(x), _ptr(y), n))
+
+    def argmax(self, x, rows: int, n: int, index) -> None:
+        _check(self._l.sh_argmax_f32(self.handle, _ptr(x), rows, n, _ptr(index)))
+
+    def attn_decode(self, q, k, v, lengths, out, batch: int, heads: int, kv_heads: int,
+                    head_dim: int, max_positions: int, scale: float) -> None:
+        """Grouped-query decode attention of q [batch, heads, d] (fp32) over fp16
+        caches [batch, kv_heads, max_positions, d] up to lengths [batch] (int32)."""
+        _check(self._l.sh_attn_decode_f16(self.handle, _ptr(q), _ptr(k), _ptr(v), _ptr(lengths),
+                                          _ptr(out), batch, heads, kv_heads, head_dim,
+                                          max_positions, scale))
+
 
 class Event:
     """A HIP event on a context's stream (per-launch timing)."""

@@ -136,6 +136,13 @@ SIGNATURES = {
     "sh_quantize_e4m3": (_I, [_P, _P, _I, _I, _P, _P]),
     "sh_pack_e4m3_tiles": (_I, [_P, _P, _I, _I, _P]),
     "sh_gemv_w8a16": (_I, [_P, _P, _P, _P, _P, _I, _I, _I]),
+    "sh_rmsnorm_f32": (_I, [_P, _P, _P, _P, _I, _I, _F]),
+    "sh_layernorm_f32": (_I, [_P, _P, _P, _P, _P, _I, _I, _F]),
+    "sh_rope_f32": (_I, [_P, _P, _P, _I, _I, _I, _F]),
+    "sh_swiglu_f32": (_I, [_P, _P, _P, _P, _SZ]),
+    "sh_gelu_f32": (_I, [_P, _P, _P, _SZ]),
+    "sh_argmax_f32": (_I, [_P, _P, _I, _I, _P]),
+    "sh_attn_decode_f16": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F]),
     "sh_llm_create": (_I, [_P, ctypes.POINTER(LlmConfig), _PP]),
     "sh_llm_destroy": (_I, [_P]),
     "sh_llm_init_random": (_I, [_P, ctypes.c_uint64, _F]),

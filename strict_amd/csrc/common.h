@@ -27,6 +27,9 @@ struct Context;
 // Checks that [ptr, ptr + bytes) lies inside one tracked allocation of ctx.
 int check_range(sh_ctx *ctx, const void *ptr, size_t bytes, const char *name);
 hipStream_t stream_of(sh_ctx *ctx);
+// The context's work buffer of at least `bytes` (grown on demand, freed by
+// sh_destroy). Typed ops ordered on the context's stream share it.
+int context_scratch(sh_ctx *ctx, size_t bytes, void **ptr);
 int device_of(sh_ctx *ctx);
 // Makes ctx's device current on the calling thread.
 int enter(sh_ctx *ctx);

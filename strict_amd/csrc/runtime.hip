@@ -40,6 +40,8 @@ struct sh_ctx {
   std::map<uintptr_t, size_t> owned;     // sh_alloc'd ranges
   std::map<uintptr_t, size_t> external;  // sh_register_external ranges
   std::set<sh_module *> modules;
+  void *scratch = nullptr;  // work buffer of typed ops (context_scratch)
+  size_t scratch_bytes = 0;
 };
 
 namespace sh {
@@ -85,6 +87,22 @@ int check_range(sh_ctx *ctx, const void *ptr, size_t bytes, const char *name) {
 }
 
 hipStream_t stream_of(sh_ctx *ctx) { return ctx->stream; }
+
+int context_scratch(sh_ctx *ctx, size_t bytes, void **ptr) {
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  if (ctx->scratch_bytes < bytes) {
+    // the old buffer may still be read by work queued on the stream
+    SH_HIP_TRY(hipStreamSynchronize(ctx->stream));
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    ctx->scratch = nullptr;
+    ctx->scratch_bytes = 0;
+    const size_t grown = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+    SH_HIP_TRY(hipMalloc(&ctx->scratch, grown));
+    ctx->scratch_bytes = grown;
+  }
+  *ptr = ctx->scratch;
+  return SH_OK;
+}
 int device_of(sh_ctx *ctx) { return ctx->device; }
 
 int enter(sh_ctx *ctx) {
@@ -160,6 +178,7 @@ SH_API int sh_destroy(sh_ctx *ctx) {
   for (auto *m : mods) sh_module_unload(m);
   for (auto &kv : ctx->owned) (void)hipFree(reinterpret_cast<void *>(kv.first));
   ctx->owned.clear();
+  if (ctx->scratch) (void)hipFree(ctx->scratch);
   (void)hipEventDestroy(ctx->timer_begin);
   (void)hipEventDestroy(ctx->timer_end);
   (void)hipStreamDestroy(ctx->stream);

@@ -160,3 +160,58 @@ def test_decode_step_bytes_config4():
     b = llm.decode_step_bytes(llm.QWEN3_0_6B, 1, 4096)
     assert b["kv"] == 469_762_048
     assert abs(b["weights"] - 598_099_456) / 598_099_456 < 1e-3
+
+
+# ---- the decoder building blocks, one at a time (torch CPU as an independent check) ----
+
+def test_norms_and_activations_match_torch():
+    F = torch.nn.functional
+    rng = np.random.default_rng(3)
+    x = rng.normal(0, 2, (9, 1024)).astype(np.float32)
+    g = (1 + rng.normal(0, 0.1, 1024)).astype(np.float32)
+    b = rng.normal(0, 0.1, 1024).astype(np.float32)
+    xt = torch.from_numpy(x).double()
+    ref = F.rms_norm(xt, (1024,), torch.from_numpy(g).double(), eps=1e-6).numpy()
+    assert np.max(np.abs(ollm.rms_norm(x, g, 1e-6) - ref)) <= 1e-6 * np.max(np.abs(ref))
+    ref = F.layer_norm(xt, (1024,), torch.from_numpy(g).double(), torch.from_numpy(b).double(),
+                       eps=1e-5).numpy()
+    assert np.max(np.abs(ollm.layer_norm(x, g, b, 1e-5) - ref)) <= 1e-6 * np.max(np.abs(ref))
+    z = np.linspace(-12, 12, 100_001).astype(np.float32)
+    zt = torch.from_numpy(z).double()
+    assert np.max(np.abs(ollm.silu(z) - F.silu(zt).numpy())) <= 4e-6
+    assert np.max(np.abs(ollm.gelu_tanh(z) - F.gelu(zt, approximate="tanh").numpy())) <= 4e-6
+
+
+def test_attn_decode_matches_torch_sdpa_gqa():
+    # grouped-query decode attention with ragged lengths against torch's
+    # scaled_dot_product_attention (fp64, K / V repeated per query group)
+    F = torch.nn.functional
+    rng = np.random.default_rng(4)
+    B, H, KVH, P, d = 3, 8, 2, 50, 64
+    q = rng.normal(0, 1, (B, H, d)).astype(np.float32)
+    k = rng.normal(0, 1, (B, KVH, P, d)).astype(np.float32)
+    v = rng.normal(0, 1, (B, KVH, P, d)).astype(np.float32)
+    lengths = [50, 1, 17]
+    scale = 1 / np.sqrt(d)
+    got = ollm.attn_decode(q, k, v, lengths, scale)
+    for b, L in enumerate(lengths):
+        qt = torch.from_numpy((q[b] * np.float32(scale)).astype(np.float32)).double()[:, None, :]
+        kt = torch.from_numpy(np.repeat(k[b, :, :L], H // KVH, axis=0)).double()
+        vt = torch.from_numpy(np.repeat(v[b, :, :L], H // KVH, axis=0)).double()
+        ref = F.scaled_dot_product_attention(qt, kt, vt, scale=1.0)[:, 0].numpy()
+        assert np.max(np.abs(got[b] - ref)) <= 1e-6
+
+
+def test_attn_decode_closed_forms():
+    rng = np.random.default_rng(5)
+    B, H, KVH, P, d = 3, 4, 4, 9, 64
+    q = rng.normal(0, 1, (B, H, d)).astype(np.float32)
+    v = rng.normal(0, 1, (B, KVH, P, d)).astype(np.float32)
+    k = np.broadcast_to(rng.normal(0, 1, d).astype(np.float32), (B, KVH, P, d)).copy()
+    out = ollm.attn_decode(q, k, v, [9, 1, 0], 0.125)
+    # identical keys: uniform weights, the mean of V
+    assert np.allclose(out[0], v[0].mean(axis=1), atol=1e-6)
+    # one position: that position's V
+    assert np.array_equal(out[1], v[1, :, 0])
+    # no positions: zeros
+    assert not out[2].any()
