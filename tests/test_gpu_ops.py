@@ -8,7 +8,9 @@ decoders define them. Bars, stated per test:
     (fp64 statistics, fp64 cos / sin, each fp32 product and sum rounded), so
     at most 1 ulp apart (an fp64 sum in another order can flip the last bit
     of the fp32 scale);
-  - SwiGLU: at most 4 ulp of the result (device exp against numpy's);
+  - SwiGLU: at most 8 ulp of the result (the device's expf and numpy's
+    float32 exp each err by up to a few ulp, and the divide and the product
+    by up to half an ulp each);
   - GELU: |gpu - oracle| <= 4 ulp(1) * |x| (1 + tanh cancels near the
     negative tail, so the error is bounded relative to x, not the result);
   - argmax: identical indices (first maximum, NaN largest);
@@ -111,8 +113,9 @@ def test_swiglu_and_gelu_vs_oracle(ctx):
                 out_shapes=[((n,), np.float32)])
     ref = ollm.silu(gate) * up
     u = _ulps(y, ref)
-    print(f"swiglu: max {u.max()} ulp")
-    assert u.max() <= 4
+    print(f"swiglu: max {u.max()} ulp, {np.mean(u == 0):.4f} bit-exact, {np.sum(u > 2)} above 2 ulp "
+          f"(worst at gate={gate[np.argmax(u)]!r})")
+    assert u.max() <= 8
     x = np.concatenate([np.linspace(-10, 10, 200_001), rng.normal(0, 3, n)]).astype(np.float32)
     (y,) = _run(ctx, lambda dx, dy: ctx.gelu(dx, dy, x.size), x,
                 out_shapes=[((x.size,), np.float32)])
