@@ -361,6 +361,23 @@ SH_API int sh_attn_decode_f16(sh_ctx *ctx, const float *q, const uint16_t *k, co
                               const int32_t *lengths, float *out, int batch, int heads,
                               int kv_heads, int head_dim, int max_positions, float scale);
 
+/* sh_attn_decode_f16 without any allocation. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments, kernels and results as sh_attn_decode_f16, but the split partials
+ * go to a fixed device array of SH_ATTN_NOALLOC_MAX_BYTES per GPU, held from
+ * the library's load until the process ends; calls whose partials
+ * (batch * heads * splits * (head_dim + 2) * 4 bytes) exceed it fail with
+ * SH_ERR_INVALID_ARGUMENT. Calls no hipMalloc / hipFree. Every call on one
+ * GPU shares that GPU's array (nothing in it needs clearing between calls:
+ * each call writes every partial it reads): calls that overlap on one GPU,
+ * from different streams or contexts, race. */
+#define SH_ATTN_NOALLOC_MAX_BYTES ((size_t)16 << 20)
+SH_API int sh_attn_decode_f16_noalloc(sh_ctx *ctx, const float *q, const uint16_t *k,
+                                      const uint16_t *v, const int32_t *lengths, float *out,
+                                      int batch, int heads, int kv_heads, int head_dim,
+                                      int max_positions, float scale);
+
 /* ---- LLM decode (model runners) ------------------------------------------------
  * No reference counterpart: BASELINE configs[3] (GPT-2 small, fp16 weights)
  * and configs[4] (Qwen3-0.6B shape, FP8-E4M3 weights with per-output-channel

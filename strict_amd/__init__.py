@@ -456,6 +456,14 @@ class Context:
                                           _ptr(out), batch, heads, kv_heads, head_dim,
                                           max_positions, scale))
 
+    def attn_decode_noalloc(self, q, k, v, lengths, out, batch: int, heads: int, kv_heads: int,
+                            head_dim: int, max_positions: int, scale: float) -> None:
+        """attn_decode without allocating: the partials use the library's fixed
+        per-GPU array (SH_ATTN_NOALLOC_MAX_BYTES); concurrent calls on one GPU race."""
+        _check(self._l.sh_attn_decode_f16_noalloc(self.handle, _ptr(q), _ptr(k), _ptr(v),
+                                                  _ptr(lengths), _ptr(out), batch, heads,
+                                                  kv_heads, head_dim, max_positions, scale))
+
 
 class Event:
     """A HIP event on a context's stream (per-launch timing)."""

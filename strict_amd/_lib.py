@@ -143,6 +143,7 @@ SIGNATURES = {
     "sh_gelu_f32": (_I, [_P, _P, _P, _SZ]),
     "sh_argmax_f32": (_I, [_P, _P, _I, _I, _P]),
     "sh_attn_decode_f16": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F]),
+    "sh_attn_decode_f16_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F]),
     "sh_llm_create": (_I, [_P, ctypes.POINTER(LlmConfig), _PP]),
     "sh_llm_destroy": (_I, [_P]),
     "sh_llm_init_random": (_I, [_P, ctypes.c_uint64, _F]),

@@ -14,12 +14,14 @@
 // each workgroup streams its split's positions in 64-position tiles of K and
 // V through LDS with a running softmax (max, sum, unnormalised V sum) per
 // query head, and writes those three as a partial; a merge kernel per
-// (row, head) combines the partials. The partials live in the context's
-// work buffer.
+// (row, head) combines the partials. The partials live in a work buffer:
+// the context's (sh_attn_decode_f16) or a fixed device array
+// (sh_attn_decode_f16_noalloc).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 #include "common.h"
 #include "llm_device.h"
@@ -379,6 +381,36 @@ int run_attn(sh_ctx *ctx, const float *q, const uint16_t *k, const uint16_t *v,
   return e == hipSuccess ? SH_OK : hip_fail(e, "attention decode");
 }
 
+// ---- the allocation-free attention's work buffer --------------------------------
+
+// Partials of sh_attn_decode_f16_noalloc: one array per device, held from the
+// library's load until the process ends. Host code never passes `scratch`
+// itself to a kernel (in host code the name is a stand-in, not a device
+// address): the device address comes from hipGetSymbolAddress, once per
+// device with that device current, and is kept in g_scratch_dev.
+constexpr size_t kNoAllocScratchBytes = SH_ATTN_NOALLOC_MAX_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_dev[kMaxDevices] = {};
+
+// The current device's address of `scratch` (ctx's device is current).
+int noalloc_scratch(sh_ctx *ctx, void **ptr) {
+  const int dev = device_of(ctx);
+  if (dev < 0 || dev >= kMaxDevices) return fail(SH_ERR_NO_DEVICE, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(SH_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_dev[dev] = p;
+  }
+  *ptr = g_scratch_dev[dev];
+  return SH_OK;
+}
+
 }  // namespace
 }  // namespace sh
 
@@ -486,6 +518,28 @@ SH_API int sh_attn_decode_f16(sh_ctx *ctx, const float *q, const uint16_t *k, co
   attn_split(batch, kv_heads, max_positions, &splits, &chunk);
   void *part = nullptr;
   if ((rc = context_scratch(ctx, attn_part_bytes(batch, heads, head_dim, splits), &part))) return rc;
+  return run_attn(ctx, q, k, v, lengths, out, batch, heads, kv_heads, head_dim, max_positions, scale,
+                  static_cast<float *>(part), splits, chunk);
+}
+
+SH_API int sh_attn_decode_f16_noalloc(sh_ctx *ctx, const float *q, const uint16_t *k,
+                                      const uint16_t *v, const int32_t *lengths, float *out,
+                                      int batch, int heads, int kv_heads, int head_dim,
+                                      int max_positions, float scale) {
+  int rc = enter(ctx);
+  if (rc != SH_OK) return rc;
+  if ((rc = check_attn(ctx, q, k, v, lengths, out, batch, heads, kv_heads, head_dim, max_positions)))
+    return rc;
+  int splits = 0, chunk = 0;
+  attn_split(batch, kv_heads, max_positions, &splits, &chunk);
+  const size_t need = attn_part_bytes(batch, heads, head_dim, splits);
+  if (need > kNoAllocScratchBytes)
+    return fail(SH_ERR_INVALID_ARGUMENT,
+                "attention partials need %zu bytes, more than the %zu-byte allocation-free "
+                "work buffer (batch * heads * splits * (head_dim + 2) * 4, %d splits)",
+                need, kNoAllocScratchBytes, splits);
+  void *part = nullptr;
+  if ((rc = noalloc_scratch(ctx, &part))) return rc;
   return run_attn(ctx, q, k, v, lengths, out, batch, heads, kv_heads, head_dim, max_positions, scale,
                   static_cast<float *>(part), splits, chunk);
 }
