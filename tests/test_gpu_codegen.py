@@ -174,3 +174,26 @@ def test_nested_expressions_match_c_semantics(ctx, body, max_ulp):
         print(f"[codegen] {body}: max ulp {int(d.max())}")
         assert d.max() <= max_ulp
     k.module.unload()
+
+
+@pytest.mark.parametrize("count", [1, 1000, 1 << 20])
+def test_compile_binary_entry_point_runs(ctx, count):
+    # Compile(BinaryExecutable, Platform) (InstructionsToCuda.cs:14-15): the
+    # entry point with no parameters plus `count`, launched over count
+    # elements with a partial last block; every element holds the entry
+    # point's value (2.5 * 4 - 1.25 = 8.75, exact in float)
+    I = cg.InstructionType
+    hip = cg.InstructionsToHip().compile_binary([
+        cg.load_constant(0, 2.5), cg.load_constant(1, 4.0), cg.binary(I.Multiply, 0, 1, 2),
+        cg.load_constant(3, 1.25), cg.binary(I.Subtract, 2, 3, 4), cg.return_register(4)])
+    kernel = load_generated(ctx, hip, "Run", cg.InstructionsToHip.run_method)
+    sentinel = np.full(count + 64, -7.0, np.float32)
+    out = ctx.upload(sentinel)
+    kernel.grid_dimensions = ((count + 255) // 256, 1, 1)
+    kernel.block_dimensions = (256, 1, 1)
+    kernel.run(out, count)
+    got = out.to_host()
+    assert np.all(got[:count] == np.float32(8.75))
+    assert np.all(got[count:] == np.float32(-7.0))  # the bounds check held
+    out.free()
+    kernel.module.unload()
