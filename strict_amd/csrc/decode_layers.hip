@@ -704,12 +704,14 @@ struct AttnKV {
   f16x8 v[2][kVS];
 };
 
-__device__ __forceinline__ void attn_load_k(const LayersArgs &a, const SH_GLOBAL uint16_t *kb, int pb,
-                                            AttnKV &kv) {
+// Positions are clamped to the split's own range, [pb, pe_k) of the K
+// cache and [pb, pe_v) of V^T: positions past the split re-read its last
+// ones (already requested) instead of fetching the next split's.
+__device__ __forceinline__ void attn_load_k(const SH_GLOBAL uint16_t *kb, int pb, int pe_k, AttnKV &kv) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, grp = lane >> 4;
 #pragma unroll
   for (int tt = 0; tt < kKT; tt++) {
-    const int p = min(pb + 16 * (wave + 4 * tt) + r, a.max_pos - 1);
+    const int p = min(pb + 16 * (wave + 4 * tt) + r, pe_k - 1);
 #pragma unroll
     for (int kk = 0; kk < 4; kk++)
       kv.k[tt][kk] = *reinterpret_cast<const SH_GLOBAL f16x8 *>(kb + (size_t)p * kD + 32 * kk + 8 * grp);
@@ -717,17 +719,27 @@ __device__ __forceinline__ void attn_load_k(const LayersArgs &a, const SH_GLOBAL
 }
 
 __device__ __forceinline__ void attn_load_v(const LayersArgs &a, const SH_GLOBAL uint16_t *vtb, int pb,
-                                            AttnKV &kv) {
+                                            int pe_v, AttnKV &kv) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, grp = lane >> 4;
 #pragma unroll
   for (int nt = 0; nt < 2; nt++) {
     const SH_GLOBAL uint16_t *row = vtb + (size_t)(32 * wave + 16 * nt + r) * a.vt_stride;
 #pragma unroll
     for (int ks = 0; ks < kVS; ks++) {
-      const int p = min(pb + 32 * ks + 8 * grp, a.vt_stride - 8);
+      const int p = min(pb + 32 * ks + 8 * grp, pe_v - 8);
       kv.v[nt][ks] = *reinterpret_cast<const SH_GLOBAL f16x8 *>(row + p);
     }
   }
+}
+
+// The split's ends: the K cache holds max_pos positions, a V^T row
+// vt_stride (both ends multiples of 16 or max_pos, so 8-position V loads
+// stay aligned).
+__device__ __forceinline__ int split_end_k(const LayersArgs &a, int s) {
+  return min(s * a.chunk + a.chunk, a.max_pos);
+}
+__device__ __forceinline__ int split_end_v(const LayersArgs &a, int s) {
+  return min(s * a.chunk + a.chunk, a.vt_stride);
 }
 
 // Requests K / V^T of the first block of attention item `item`.
@@ -736,9 +748,9 @@ __device__ __forceinline__ void attn_prefetch(const LayersArgs &a, const LayerG 
   const int splits = a.splits, kvn = a.kv_heads;
   const int s = item % splits, kvh = (item / splits) % kvn, b = item / (splits * kvn);
   const size_t kv_row = (size_t)b * kvn + kvh;
-  const int pb = min(s * a.chunk, a.max_pos - 1);
-  attn_load_k(a, P.kcache + kv_row * a.max_pos * kD, pb, kv);
-  attn_load_v(a, P.vcache + kv_row * kD * a.vt_stride, pb, kv);
+  const int p0 = s * a.chunk;
+  attn_load_k(P.kcache + kv_row * a.max_pos * kD, min(p0, a.max_pos - 1), split_end_k(a, s), kv);
+  attn_load_v(a, P.vcache + kv_row * kD * a.vt_stride, p0, split_end_v(a, s), kv);
 }
 
 // B: item = (b, KV head, split), its first K / V^T block requested by
@@ -855,7 +867,7 @@ __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, 
   for (int g = 0; g < kG; g++) M[g] = -INFINITY;
   for (int bb = 0; bb < nblk; bb++) {
     const int pb = p0 + bb * kBlk;
-    if (bb > 0) attn_load_k(a, kb, pb, kv);
+    if (bb > 0) attn_load_k(kb, pb, split_end_k(a, s), kv);
 #pragma unroll
     for (int tt = 0; tt < kKT; tt++) {
       const int tile = wave + 4 * tt;
@@ -920,7 +932,7 @@ __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, 
   const _Float16 vn[2] = {S.vnew[32 * wave + r], S.vnew[32 * wave + 16 + r]};
   for (int bb = 0; bb < nblk; bb++) {
     const int pb = p0 + bb * kBlk;
-    if (bb > 0) attn_load_v(a, vtb, pb, kv);
+    if (bb > 0) attn_load_v(a, vtb, pb, split_end_v(a, s), kv);
 #pragma unroll
     for (int ks = 0; ks < kVS; ks++) {
       const int q0 = pb + 32 * ks + 8 * grp;
