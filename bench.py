@@ -65,6 +65,11 @@ def parse_args():
     p.add_argument("--workload", default="decode", choices=["decode", "image", "sigmoid"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extra", action="store_true", help="skip the kernels table")
+    p.add_argument("--part", default=None,
+                   choices=["qwen3_b4", "qwen3_b16", "gpt2", "gemm", "gemm_fp8", "gemv", "image",
+                            "sigmoid"],
+                   help="time one row of the kernels table alone (for profiling runs) and print "
+                        "its entry")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="approximate CPU time budget of the cpu_baseline sample")
     return p.parse_args()
@@ -630,6 +635,48 @@ def attach_cpu_baselines(kernels, headline_cpu, seconds):
     return img
 
 
+def qwen3_batch_entry(ctx, batch, steps):
+    from strict_amd import llm
+
+    c = llm.QWEN3_0_6B.with_(max_positions=KV_PROMPT + 4 + steps + 1, max_batch=batch)
+    bms, bctx = decode_run(ctx, c, batch, KV_PROMPT, steps, 4)
+    e = hbm_entry(f"qwen3 decode step b={batch} (configs[4])",
+                  llm.decode_step_bytes(c, batch, bctx)["total"], bms)
+    e["tokens/s"] = round(batch * 1e3 / bms, 1)
+    return e
+
+
+def gpt2_entry(ctx):
+    from strict_amd import llm
+
+    g = llm.GPT2_SMALL
+    gms, gctx = decode_run(ctx, g, 1, 128, 256, 0)
+    e = hbm_entry("gpt2 decode step b=1 (configs[3], 128-token prompt, 256 steps)",
+                  llm.decode_step_bytes(g, 1, gctx)["total"], gms)
+    e["tokens/s"] = round(1e3 / gms, 1)
+    return e
+
+
+def run_part(ctx, part, steps):
+    """One row of the kernels table on its own (profiling runs)."""
+    rng = np.random.default_rng(42)
+    if part == "qwen3_b4":
+        return [qwen3_batch_entry(ctx, 4, 32)]
+    if part == "qwen3_b16":
+        return [qwen3_batch_entry(ctx, 16, 16)]
+    if part == "gpt2":
+        return [gpt2_entry(ctx)]
+    if part == "gemm":
+        return [gemm_kernel(ctx, rng)]
+    if part == "gemm_fp8":
+        return [gemm_fp8_kernel(ctx, rng)]
+    if part == "gemv":
+        return [gemv_kernel(ctx, rng, steps)]
+    if part == "image":
+        return [v[0] for v in image_kernels(ctx, rng, steps).values()]
+    return [sigmoid_kernel(ctx, rng, steps)[0]]
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -637,6 +684,17 @@ def main() -> int:
               f"kernel path has no multi-GPU leg (asked for --gpus {args.gpus}).",
               file=sys.stderr)
         return 2
+    if args.part:
+        import strict_amd
+
+        ctx = strict_amd.Context(0)
+        entries = run_part(ctx, args.part, args.steps)
+        from strict_amd import yardstick
+
+        yardstick.release()
+        ctx.dispose()
+        print(json.dumps({"part": args.part, "kernels": entries}), flush=True)
+        return 0
 
     import strict_amd
     from strict_amd import llm
@@ -670,19 +728,9 @@ def main() -> int:
                               "launch)"}
         log(f"headline: {value:.1f} tokens/s, {achieved:.1f} GB/s algorithmic")
         if not args.no_extra:
-            for b, st in ((4, 32), (16, 16)):
-                c = llm.QWEN3_0_6B.with_(max_positions=KV_PROMPT + 4 + st + 1, max_batch=b)
-                bms, bctx = decode_run(ctx, c, b, KV_PROMPT, st, 4)
-                by = llm.decode_step_bytes(c, b, bctx)["total"]
-                e = hbm_entry(f"qwen3 decode step b={b} (configs[4])", by, bms)
-                e["tokens/s"] = round(b * 1e3 / bms, 1)
-                kernels.append(e)
-            g = llm.GPT2_SMALL
-            gms, gctx = decode_run(ctx, g, 1, 128, 256, 0)
-            e = hbm_entry("gpt2 decode step b=1 (configs[3], 128-token prompt, 256 steps)",
-                          llm.decode_step_bytes(g, 1, gctx)["total"], gms)
-            e["tokens/s"] = round(1e3 / gms, 1)
-            kernels.append(e)
+            kernels.append(qwen3_batch_entry(ctx, 4, 32))
+            kernels.append(qwen3_batch_entry(ctx, 16, 16))
+            kernels.append(gpt2_entry(ctx))
     if not args.no_extra or args.workload != "decode":
         img = image_kernels(ctx, rng, table_steps if args.workload != "image" else steps)
         kernels += [v[0] for v in img.values()]

@@ -45,11 +45,15 @@ struct Layer {
 // to 5120 tokens, so each workgroup's K and V fit one batch of loads issued
 // together), at least enough that no split exceeds kMaxSplitChunk positions,
 // at most 64 (the merge kernel's limit).
+// Splits per (row, KV head) of the per-op attention kernel: as few as keep a
+// split within kMaxSplitChunk positions. Each kernel of a per-op step costs
+// ~4-6 us whatever its size (measured on GPT-2's step), so one split per
+// head up to 1024 positions, which writes the head's output directly, beats
+// many short splits plus the merge kernel they need.
 int attention_splits(int batch, int kv_heads, int max_pos) {
-  int s = 512 / (batch * kv_heads);
-  if (s > 64) s = 64;
-  const int min_s = (max_pos + kMaxSplitChunk - 1) / kMaxSplitChunk;
-  if (s < min_s) s = min_s;
+  (void)batch;
+  (void)kv_heads;
+  const int s = (max_pos + kMaxSplitChunk - 1) / kMaxSplitChunk;
   return s < 1 ? 1 : s;
 }
 
@@ -289,7 +293,9 @@ int enqueue_step(sh_llm *m, bool logits) {
     h.out = m->logits;
     h.out_ld = m->vocab_pad;
     h.argmax = m->keys;
-    SH_HIP_TRY(launch_gemv(s, h, m->wtype, kProNone, kEpiLogits, 0));
+    // grid-striding over the head's tiles (one tile per workgroup ran the
+    // fp16 GPT-2 head at 2 TB/s)
+    SH_HIP_TRY(launch_gemv(s, h, m->wtype, kProNone, kEpiLogits, 2048));
   }
   return SH_OK;
 }
