@@ -1070,8 +1070,8 @@ __device__ __forceinline__ bool merge_item(const LayersArgs &a, int l, int item,
 // RMSNorm(x; final_g))[b][n] for the 16-row tiles j = w, w + G, .. of this
 // workgroup, each wave taking every fourth of them over the whole K (kLH
 // 16-byte loads per lane and tile), the next tile's weights requested while
-// the current one is multiplied; the running argmax keys go to keys[b]
-// (read first, atomicMax only when larger).
+// the current one is multiplied; the running argmax keys go to the wave's
+// slot of keys (read first, atomicMax only when larger).
 template <int kLA, int kRows>
 __device__ __forceinline__ bool head_phase(const LayersArgs &a, unsigned ep, const Lds &s) {
   constexpr int kLH = 4 * kLA;  // K / 64
@@ -1138,9 +1138,10 @@ __device__ __forceinline__ bool head_phase(const LayersArgs &a, unsigned ep, con
       k = o > k ? o : k;
     }
     const int b = 4 * (lane >> 4) + r;
+    unsigned long long *slot = a.keys + ((w * 4 + wave) % kKeySlots) * kKeyStride + b;
     if ((lane & 15) == 0 && b < B && k != 0 &&
-        k > __hip_atomic_load(a.keys + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-      atomicMax(a.keys + b, k);
+        k > __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+      atomicMax(slot, k);
   }
   return true;
 }

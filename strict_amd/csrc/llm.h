@@ -11,6 +11,15 @@ namespace sh {
 
 constexpr int kMaxBatch = 16;        // rows of the GEMV's MFMA A operand
 constexpr int kMaxSplitChunk = 1024; // positions one attention workgroup may score
+// Greedy argmax keys of the LM head, [kKeySlots][kKeyStride]: key of row b in
+// slot s at keys[s * kKeyStride + b]; the row's token is the largest key over
+// its slots. Workgroups finishing the head together spread their atomicMax
+// over the slots (slot rows 256 bytes apart, on lines of their own): 2048
+// workgroups on one address serialised ~9 ns each, 19 us of a GPT-2 head
+// that streams its weights in 14 us.
+constexpr int kKeySlots = 32;
+constexpr int kKeyStride = 32;
+static_assert(kKeyStride >= kMaxBatch, "a slot row holds every batch row");
 
 enum { kWeightFp8 = 0, kWeightFp16 = 1 };
 enum { kProNone = 0, kProRms = 1, kProLayer = 2 };
@@ -35,7 +44,7 @@ struct GemvArgs {
   float *out = nullptr;      // fp32 output / residual rows
   uint16_t *out16 = nullptr; // fp16 output rows (SwiGLU, GELU)
   int out_ld = 0;
-  unsigned long long *argmax = nullptr;  // logits: per-row argmax keys (atomicMax)
+  unsigned long long *argmax = nullptr;  // logits: [kKeySlots][kKeyStride] argmax keys (atomicMax)
 };
 
 struct AttnArgs {
@@ -58,7 +67,7 @@ struct AttnArgs {
 };
 
 struct EmbedArgs {
-  unsigned long long *keys = nullptr;  // [B] argmax keys (token = ~low word)
+  unsigned long long *keys = nullptr;  // [kKeySlots][kKeyStride] argmax keys (token = ~low word)
   int *lens = nullptr;                 // [B] tokens cached so far (advanced here)
   int *pos = nullptr;                  // [B] position of this step's token (written here)
   int *hist = nullptr;                 // [B][hist_len] token history
@@ -122,7 +131,7 @@ struct LayersArgs {
   int head_tiles = 0, n_valid = 0;     // 16-row tiles; columns that are real tokens
   float *logits = nullptr;             // [B][logits_ld]
   int logits_ld = 0;
-  unsigned long long *keys = nullptr;  // [B] greedy argmax keys (zeroed by the embed kernel)
+  unsigned long long *keys = nullptr;  // [kKeySlots][kKeyStride] greedy argmax keys (zeroed by the embed kernel)
 };
 
 // Model shapes the kernel is instantiated for (16-byte weight loads per lane

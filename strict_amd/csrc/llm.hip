@@ -11,6 +11,7 @@
 // layers kernel is a cooperative launch, which stream capture does not take).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -559,7 +560,7 @@ SH_API int sh_llm_create(sh_ctx *ctx, const sh_llm_config *config, sh_llm **out)
       (rc = alloc_n(m, (size_t)B * c.kv_heads, &m->counters)) ||
       (rc = alloc_n(m, (size_t)B, &m->lens)) || (rc = alloc_n(m, (size_t)B, &m->pos)) ||
       (rc = alloc_n(m, (size_t)B * c.max_positions, &m->hist)) ||
-      (rc = alloc_n(m, (size_t)B, &m->keys)))
+      (rc = alloc_n(m, (size_t)kKeySlots * kKeyStride, &m->keys)))
     return cleanup(rc);
   // norm gains start at 1 (biases and weights at 0)
   for (Layer &L : m->layers) {
@@ -712,7 +713,7 @@ SH_API int sh_llm_reset(sh_llm *m, int batch) {
     return fail(SH_ERR_INVALID_ARGUMENT, "batch %d outside 1..%d", batch, m->cfg.max_batch);
   hipStream_t s = stream_of(m->ctx);
   SH_HIP_TRY(hipMemsetAsync(m->lens, 0, (size_t)m->cfg.max_batch * 4, s));
-  SH_HIP_TRY(hipMemsetAsync(m->keys, 0, (size_t)m->cfg.max_batch * 8, s));
+  SH_HIP_TRY(hipMemsetAsync(m->keys, 0, (size_t)kKeySlots * kKeyStride * 8, s));
   SH_HIP_TRY(hipMemsetAsync(m->counters, 0, (size_t)m->cfg.max_batch * m->cfg.kv_heads * 4, s));
   m->batch = batch;
   m->splits = attention_splits(batch, m->cfg.kv_heads, m->cfg.max_positions);
@@ -748,13 +749,14 @@ SH_API int sh_llm_step(sh_llm *m, const int32_t *tokens, int want_logits) {
     return fail(SH_ERR_INVALID_ARGUMENT, "KV cache full (%d positions)", m->cfg.max_positions);
   hipStream_t s = stream_of(m->ctx);
   if (tokens) {
-    unsigned long long keys[kMaxBatch];
+    // the token in slot 0, every other slot cleared (a previous head's keys)
+    unsigned long long keys[kKeySlots * kKeyStride] = {};
     for (int b = 0; b < m->batch; b++) {
       if (tokens[b] < 0 || tokens[b] >= m->cfg.vocab)
         return fail(SH_ERR_INVALID_ARGUMENT, "token %d of row %d outside the vocabulary", tokens[b], b);
       keys[b] = (unsigned long long)(0xffffffffu - (uint32_t)tokens[b]);
     }
-    SH_HIP_TRY(hipMemcpyAsync(m->keys, keys, (size_t)m->batch * 8, hipMemcpyHostToDevice, s));
+    SH_HIP_TRY(hipMemcpyAsync(m->keys, keys, sizeof(keys), hipMemcpyHostToDevice, s));
     SH_HIP_TRY(hipStreamSynchronize(s));  // `keys` is a stack array
   }
   const int g = want_logits ? 1 : 0;
@@ -790,9 +792,9 @@ SH_API int sh_llm_next_tokens(sh_llm *m, int32_t *tokens) {
   if (!m || !tokens) return fail(SH_ERR_INVALID_ARGUMENT, "NULL argument");
   int rc = enter(m->ctx);
   if (rc != SH_OK) return rc;
-  unsigned long long keys[kMaxBatch];
+  unsigned long long keys[kKeySlots * kKeyStride];
   hipStream_t s = stream_of(m->ctx);
-  SH_HIP_TRY(hipMemcpyAsync(keys, m->keys, (size_t)m->batch * 8, hipMemcpyDeviceToHost, s));
+  SH_HIP_TRY(hipMemcpyAsync(keys, m->keys, sizeof(keys), hipMemcpyDeviceToHost, s));
   unsigned err = 0;
   if (m->layers_kernel)
     SH_HIP_TRY(hipMemcpyAsync(&err, m->la.err, 4, hipMemcpyDeviceToHost, s));
@@ -800,8 +802,10 @@ SH_API int sh_llm_next_tokens(sh_llm *m, int32_t *tokens) {
   if (err)
     return fail(SH_ERR_HIP, "decode-layers kernel: a wait between workgroups timed out (step state lost; reset the model)");
   for (int b = 0; b < m->batch; b++) {
-    if (keys[b] == 0) return fail(SH_ERR_INVALID_ARGUMENT, "no greedy token yet (step without logits?)");
-    tokens[b] = (int32_t)(0xffffffffu - (uint32_t)(keys[b] & 0xffffffffu));
+    unsigned long long key = 0;
+    for (int sl = 0; sl < kKeySlots; sl++) key = std::max(key, keys[sl * kKeyStride + b]);
+    if (key == 0) return fail(SH_ERR_INVALID_ARGUMENT, "no greedy token yet (step without logits?)");
+    tokens[b] = (int32_t)(0xffffffffu - (uint32_t)(key & 0xffffffffu));
   }
   return SH_OK;
 }

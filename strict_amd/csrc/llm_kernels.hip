@@ -403,12 +403,12 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvArgs a) {
         k = o > k ? o : k;
       }
       const int b = 4 * (lane >> 4) + r;
-      // most workgroups finish below the running maximum: read it first and
-      // only those above it update (one device-scope read instead of an
-      // atomic that serialises with every other workgroup's)
+      // this workgroup's slot; most workgroups finish below its running
+      // maximum: read it first and only those above it update
+      unsigned long long *slot = a.argmax + (blockIdx.x % kKeySlots) * kKeyStride + b;
       if ((lane & 15) == 0 && b < B && k != 0 &&
-          k > __hip_atomic_load(a.argmax + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-        atomicMax(a.argmax + b, k);
+          k > __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+        atomicMax(slot, k);
     }
   }
 }
@@ -783,26 +783,37 @@ __global__ __launch_bounds__(kThreads) void norm_rows_kernel(const GemvArgs a) {
 
 // ---- embedding -------------------------------------------------------------
 
-// grid (B): reads the token of row b from its argmax key (the host writes
-// prompt tokens as keys too), records it in the history, clears the key for
-// this step's LM head, advances the row's position and writes the fp32
+// grid (B): reads the token of row b from its argmax keys (the largest over
+// the slots; the host writes prompt tokens as keys too), records it in the
+// history, clears the keys for this step's LM head, advances the row's
+// position and writes the fp32
 // residual stream: Qwen3 dequantises the tied FP8 head row, GPT-2 adds the
 // fp16 token (tied head) and position rows.
 __global__ __launch_bounds__(kThreads) void embed_kernel(const EmbedArgs a) {
   const int b = blockIdx.x, t = threadIdx.x;
   __shared__ int tok_s, pos_s;
-  if (t == 0) {
-    const unsigned long long key = a.keys[b];
-    int tok = (int)(0xffffffffu - (uint32_t)(key & 0xffffffffu));
-    if (tok < 0 || tok >= a.vocab) tok = 0;
-    const int pos = a.lens[b];
-    tok_s = tok;
-    pos_s = pos;
-    if (pos < a.hist_len) a.hist[(size_t)b * a.hist_len + pos] = tok;
-    if (a.epoch && b == 0) a.epoch[0] += 1u;
-    a.pos[b] = pos;
-    a.lens[b] = pos + 1;
-    a.keys[b] = 0;
+  if (t < 64) {  // wave 0: the largest key over the slots, which it clears
+    unsigned long long key = 0;
+    if (t < kKeySlots) {
+      key = a.keys[t * kKeyStride + b];
+      a.keys[t * kKeyStride + b] = 0;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const unsigned long long o = __shfl_xor(key, off, 64);
+      key = o > key ? o : key;
+    }
+    if (t == 0) {
+      int tok = (int)(0xffffffffu - (uint32_t)(key & 0xffffffffu));
+      if (tok < 0 || tok >= a.vocab) tok = 0;
+      const int pos = a.lens[b];
+      tok_s = tok;
+      pos_s = pos;
+      if (pos < a.hist_len) a.hist[(size_t)b * a.hist_len + pos] = tok;
+      if (a.epoch && b == 0) a.epoch[0] += 1u;
+      a.pos[b] = pos;
+      a.lens[b] = pos + 1;
+    }
   }
   __syncthreads();
   const int tok = tok_s, pos = pos_s;
