@@ -40,6 +40,9 @@ typedef enum sh_status {
   SH_ERR_COMPILE = 5,          /* hipRTC compile failed; the program holds the log */
   SH_ERR_NOT_FOUND = 6,        /* unknown kernel name in a module */
   SH_ERR_UNSUPPORTED = 7,      /* valid request this build does not implement */
+  SH_ERR_INVALID_FILE = 8,     /* malformed .strictbinary: the message starts with the
+                                  reference's exception (InvalidFile, InvalidBytecodeEntry,
+                                  InvalidVersion) */
 } sh_status;
 
 typedef struct sh_ctx sh_ctx;
@@ -185,6 +188,90 @@ SH_API int sh_instructions_to_hip(const char *method_name, const char *const *pa
                                   int parameter_count, int add_count_parameter,
                                   const sh_bc_instruction *instructions, int instruction_count,
                                   char *source, size_t capacity, size_t *length);
+
+/* ---- .strictbinary loading: replaces BinaryExecutable's loader
+ *      (Strict.Bytecode/BinaryExecutable.cs:40-61) and Serialize (:144-156) -- */
+
+/* A loaded .strictbinary: a ZIP archive whose "<type full name>.bytecode"
+ * entries each hold one type's members and method groups
+ * (Serialization/BinaryType.cs:11-28). Types keep the archive's entry order
+ * (MethodsPerType's order); a type's methods are the overloads of its method
+ * groups, groups in file order, overloads in group order. Errors are
+ * SH_ERR_INVALID_FILE with the reference's exception and message, e.g.
+ * "InvalidBytecodeEntry: Entry does not start with compact 'S' magic byte"
+ * (BinaryType.cs:43-62), "InvalidVersion: File version: 0, ...",
+ * "InvalidFile: Unknown instruction type: 105" (BinaryExecutable.cs:167-203),
+ * "InvalidFile: Unknown ValueKind: ..." (:278-292), "InvalidFile: End of
+ * Central Directory record could not be found." for a file that is no ZIP.
+ * Strings returned by the accessors live until sh_strictbinary_free. A handle
+ * is not safe to use from two threads at once. */
+typedef struct sh_strictbinary sh_strictbinary;
+
+/* One value-carrying instruction (LoadConstantToRegister, StoreConstantToVariable,
+ * Set) of a method, or a member's initial value (method_index -1). */
+typedef struct sh_strictbinary_constant {
+  int instruction;        /* index in the method (member index for members) */
+  int instruction_type;   /* InstructionType: 0 LoadConstant, 2 StoreConstant, 4 Set */
+  int kind;               /* ValueKind as stored: 0 None, 1 SmallNumber, 2 IntegerNumber,
+                             3 Number, 4 Text, 5 Boolean, 6 List, 9 Dictionary */
+  int register_id;        /* LoadConstant / Set: the register; otherwise -1 */
+  const char *identifier; /* StoreConstant: the variable; member: its name; else NULL */
+  size_t count;           /* Numbers held: 1 for a Number, the items of a List of Numbers,
+                             0 otherwise */
+} sh_strictbinary_constant;
+
+/* Parses a whole .strictbinary image held in memory (the bytes of the file). */
+SH_API int sh_strictbinary_load(const void *data, size_t bytes, sh_strictbinary **binary);
+SH_API int sh_strictbinary_free(sh_strictbinary *binary);
+SH_API int sh_strictbinary_type_count(const sh_strictbinary *binary, int *count);
+SH_API int sh_strictbinary_type(const sh_strictbinary *binary, int type_index,
+                                const char **full_name, int *member_count, int *method_count);
+/* A member of the type (method_index -1) or a parameter of a method. */
+SH_API int sh_strictbinary_member(const sh_strictbinary *binary, int type_index, int method_index,
+                                  int member_index, const char **name, const char **full_type_name,
+                                  int *has_initial_value);
+SH_API int sh_strictbinary_method(const sh_strictbinary *binary, int type_index, int method_index,
+                                  const char **name, int *parameter_count,
+                                  const char **return_type, int *instruction_count);
+/* EntryPoint: the first overload of the first Run group, types in order
+ * (BinaryExecutable.cs:113-120); SH_ERR_NOT_FOUND without one. */
+SH_API int sh_strictbinary_entry_point(const sh_strictbinary *binary, int *type_index,
+                                       int *method_index);
+/* FindInstructions (BinaryExecutable.cs:125-138): the first overload of
+ * `method_name` in type `type_full_name` with `parameter_count` parameters
+ * whose return type matches (NULL or "" matches any; "Number" matches
+ * "Strict/Number" either way round); SH_ERR_NOT_FOUND otherwise. */
+SH_API int sh_strictbinary_find(const sh_strictbinary *binary, const char *type_full_name,
+                                const char *method_name, int parameter_count,
+                                const char *return_type, int *type_index, int *method_index);
+/* The method's instructions as sh_instructions_to_hip takes them: type,
+ * register operands in payload order (the first three), identifier (variable,
+ * list or table name; Print's text; Invoke's method name) and number (a Number
+ * constant's value, NaN for other constants; the count of Jump, JumpToId and
+ * LoopEnd). `*count` always receives the instruction count; with
+ * instructions == NULL nothing else is written. */
+SH_API int sh_strictbinary_instructions(const sh_strictbinary *binary, int type_index,
+                                        int method_index, sh_bc_instruction *instructions,
+                                        int capacity, int *count);
+/* The value-carrying instructions of a method (method_index -1: the members'
+ * initial values), in order; `*count` always receives their number. */
+SH_API int sh_strictbinary_constants(sh_strictbinary *binary, int type_index, int method_index,
+                                     sh_strictbinary_constant *constants, int capacity, int *count);
+/* The Numbers of a constant (count > 0, or an empty List) as doubles. */
+SH_API int sh_strictbinary_constant_values(sh_strictbinary *binary, int type_index,
+                                           int method_index, int constant_index, double *values,
+                                           size_t capacity);
+/* Kernel input: the constant's Numbers rounded to fp32 (nearest even) into
+ * device_dst, which holds `capacity` floats; synchronous, as sh_upload. */
+SH_API int sh_strictbinary_upload_f32(sh_ctx *ctx, sh_strictbinary *binary, int type_index,
+                                      int method_index, int constant_index, float *device_dst,
+                                      size_t capacity);
+/* Serialize: the binary as a .strictbinary image (deflated entries, types in
+ * order, each entry as BinaryType.Write lays it out with a name table rebuilt
+ * as the reference builds one). `*bytes` always receives the size; the image
+ * is written only when capacity >= size, else SH_ERR_INVALID_ARGUMENT. */
+SH_API int sh_strictbinary_serialize(sh_strictbinary *binary, void *data, size_t capacity,
+                                     size_t *bytes);
 
 /* ---- range-loop dispatch ---------------------------------------------------- */
 

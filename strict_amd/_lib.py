@@ -22,6 +22,7 @@ SH_ERR_OUT_OF_MEMORY = 4
 SH_ERR_COMPILE = 5
 SH_ERR_NOT_FOUND = 6
 SH_ERR_UNSUPPORTED = 7
+SH_ERR_INVALID_FILE = 8
 
 STATUS_NAMES = {
     SH_OK: "SH_OK",
@@ -32,6 +33,7 @@ STATUS_NAMES = {
     SH_ERR_COMPILE: "SH_ERR_COMPILE",
     SH_ERR_NOT_FOUND: "SH_ERR_NOT_FOUND",
     SH_ERR_UNSUPPORTED: "SH_ERR_UNSUPPORTED",
+    SH_ERR_INVALID_FILE: "SH_ERR_INVALID_FILE",
 }
 
 
@@ -58,6 +60,18 @@ class BcInstruction(ctypes.Structure):
         ("registers", ctypes.c_int * 3),
         ("identifier", ctypes.c_char_p),
         ("number", ctypes.c_double),
+    ]
+
+
+class StrictBinaryConstant(ctypes.Structure):
+    """sh_strictbinary_constant: one value-carrying instruction of a method."""
+    _fields_ = [
+        ("instruction", ctypes.c_int),
+        ("instruction_type", ctypes.c_int),
+        ("kind", ctypes.c_int),
+        ("register_id", ctypes.c_int),
+        ("identifier", ctypes.c_char_p),
+        ("count", ctypes.c_size_t),
     ]
 
 
@@ -117,6 +131,24 @@ SIGNATURES = {
     "sh_program_destroy": (_I, [_P]),
     "sh_instructions_to_hip": (_I, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p), _I, _I,
                                     _P, _I, ctypes.c_char_p, _SZ, ctypes.POINTER(_SZ)]),
+    "sh_strictbinary_load": (_I, [_P, _SZ, _PP]),
+    "sh_strictbinary_free": (_I, [_P]),
+    "sh_strictbinary_type_count": (_I, [_P, ctypes.POINTER(_I)]),
+    "sh_strictbinary_type": (_I, [_P, _I, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_I),
+                                  ctypes.POINTER(_I)]),
+    "sh_strictbinary_member": (_I, [_P, _I, _I, _I, ctypes.POINTER(ctypes.c_char_p),
+                                    ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_I)]),
+    "sh_strictbinary_method": (_I, [_P, _I, _I, ctypes.POINTER(ctypes.c_char_p),
+                                    ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_char_p),
+                                    ctypes.POINTER(_I)]),
+    "sh_strictbinary_entry_point": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
+    "sh_strictbinary_find": (_I, [_P, ctypes.c_char_p, ctypes.c_char_p, _I, ctypes.c_char_p,
+                                  ctypes.POINTER(_I), ctypes.POINTER(_I)]),
+    "sh_strictbinary_instructions": (_I, [_P, _I, _I, _P, _I, ctypes.POINTER(_I)]),
+    "sh_strictbinary_constants": (_I, [_P, _I, _I, _P, _I, ctypes.POINTER(_I)]),
+    "sh_strictbinary_constant_values": (_I, [_P, _I, _I, _I, _P, _SZ]),
+    "sh_strictbinary_upload_f32": (_I, [_P, _P, _I, _I, _I, _P, _SZ]),
+    "sh_strictbinary_serialize": (_I, [_P, _P, _SZ, ctypes.POINTER(_SZ)]),
     "sh_module_load": (_I, [_P, _P, _SZ, _PP]),
     "sh_module_function": (_I, [_P, ctypes.c_char_p, _PP]),
     "sh_module_unload": (_I, [_P]),

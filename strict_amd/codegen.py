@@ -65,11 +65,12 @@ class Instruction:
 
     def __str__(self):  # as Strict's Instruction.ToString
         regs = " ".join(f"R{r}" for r in self.registers)
+        name = getattr(self.type, "name", str(self.type))  # a type outside the enum: its number
         if self.type == InstructionType.LoadVariableToRegister:
-            return f"{self.type.name} {self.identifier} {regs}"
+            return f"{name} {self.identifier} {regs}"
         if self.type == InstructionType.LoadConstantToRegister:
-            return f"{self.type.name} {regs} {self.number:g}"
-        return f"{self.type.name} {regs}"
+            return f"{name} {regs} {self.number:g}"
+        return f"{name} {regs}"
 
 
 def load_variable(register: int, identifier: str) -> Instruction:
@@ -296,9 +297,11 @@ class InstructionsToHip:
         return build_kernel(method.name, method.instructions, names,
                             self.needs_count_parameter(names))
 
-    def compile_binary(self, entry_point: Sequence[Instruction]) -> str:
-        """Compile(BinaryExecutable, Platform) (cs:14-15): entry point with no
-        parameters plus `count`."""
+    def compile_binary(self, binary) -> str:
+        """Compile(BinaryExecutable, Platform) (cs:14-15): the entry point's
+        instructions with no parameters plus `count`. `binary` is a loaded
+        strictbinary.BinaryExecutable, or the entry point's instructions."""
+        entry_point = binary.to_instructions() if hasattr(binary, "to_instructions") else binary
         return build_kernel(self.run_method, entry_point, [], True)
 
     @staticmethod
