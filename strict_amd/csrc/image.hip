@@ -101,6 +101,10 @@ __global__ __launch_bounds__(kBlock) void brightness_byte_kernel(const uint8_t *
 // ---------------------------------------------------------------------------
 
 constexpr int kStripPx = 256;  // 64 lanes x 4 pixels
+// threads per workgroup of the streaming blur (consecutive waves take
+// consecutive strips of a band; 512 and 1024, a whole band per workgroup,
+// measured the same)
+constexpr int kBlurBlock = 256;
 
 // SWAR brightness on packed RGBA words (direct kernel and byte paths).
 struct Brightness {
@@ -171,16 +175,6 @@ __device__ __forceinline__ uint32_t finish_pixel(uint32_t vl, uint32_t vh, uint3
 // row address is scalar and each lane adds its column offset. Lanes whose
 // chunk lies outside the image load a valid chunk nobody uses (the edge fix-up
 // in hsum supplies the clamped or zero taps instead).
-template <int kMode>
-__device__ __forceinline__ u32x4 load_row(const StreamArgs &a, int y, int lx) {
-  if (kMode == SH_BLUR_CONFIG) {
-    const int cy = min(max(y, 0), a.height - 1);
-    return *reinterpret_cast<const u32x4 *>(a.in + (size_t)cy * (size_t)a.width + lx);
-  } else {
-    if (y < 0 || y >= a.height) return u32x4{0, 0, 0, 0};
-    return *reinterpret_cast<const u32x4 *>(a.in + (size_t)y * (size_t)a.width + lx);
-  }
-}
 
 // This lane's 4 pixels of one input row as 16-bit lanes, brightened (kFuse);
 // reference mode: rows outside the image contribute nothing.
@@ -201,18 +195,25 @@ __device__ __forceinline__ void expand_row(const u32x4 v, int y, int height, uin
 }
 
 // Input rows y0 - 2 .. y0 + kR + 1 are loaded once per wave (kR + 4 loads
-// for kR output rows), each 5 steps before its use. The halo rows are shared
+// for kR output rows), each 5 steps before its use. Loads and stores sit
+// under no branch (clamped rows, buffer stores whose dropped lanes point
+// past the resource), so the compiler's waits count them exactly and keep
+// ~4 rows in flight; with branches around the halo loads and the stores it
+// waited for all but ~5 operations, about one row. The halo rows are shared
 // with the neighbouring bands through L2: odd bands sweep upwards, so two
 // neighbours reach their shared rows together (both at the start or both at
 // the end of the sweep; a band's bottom halo read at the end of a downward
 // sweep would be long evicted from L2 by the time the band below started).
 template <int kMode, int kFuse, int kR>
-__global__ __launch_bounds__(kBlock) void blur_rgba_rows_kernel(const StreamArgs a) {
-  constexpr int kQ = 10;
+__global__ __launch_bounds__(kBlurBlock) void blur_rgba_rows_kernel(const StreamArgs a) {
+  constexpr int kQ = 5;  // the window's rows
+  // rows requested ahead of their use (7 and 9 measured slower: their
+  // registers drop the kernel to 3 waves per SIMD)
+  constexpr int kL = 5;
   int b = blockIdx.x;
   if (a.xcd_blocks) b = (b & 7) * a.xcd_blocks + (b >> 3);
   const int lane = threadIdx.x & 63;
-  const int wi = b * (kBlock / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wi = b * (kBlurBlock / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (wi >= a.total_waves) return;
   const int sx = wi % a.strips_x, band = wi / a.strips_x;
   const int x0 = sx * kStripPx;
@@ -220,15 +221,30 @@ __global__ __launch_bounds__(kBlock) void blur_rgba_rows_kernel(const StreamArgs
   const int lx = min(cx, a.width - 4);
   const bool left_edge = cx == 0;
   const bool right_edge = cx + 4 == a.width;
-  const bool halo_lane = lane == 0 || lane == 63;
   // halo pixels: lane 0 the two left of the strip, lane 63 the two right of it
   const int hx = lane == 0 ? max(x0 - 2, 0) : min(x0 + kStripPx, a.width - 2);
   const int y0 = band * kR;
   // load j of the sweep reads row ys + dy * j
   const int dy = (band & 1) ? -1 : 1;
   const int ys = (band & 1) ? y0 + kR + 1 : y0 - 2;
+  // stores through a buffer resource over this band's output rows: lanes
+  // past the image's right edge and rows past its bottom get an offset
+  // beyond the resource, which the hardware drops, so no branch guards them
   const bool writer = cx < a.width;
   const int out_rows = min(kR, a.height - y0);
+  const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      a.out + (size_t)y0 * (size_t)a.width, 0, out_rows * a.width * 4, 0x00020000);
+  const int out_lane = writer ? cx * 4 : 0x7fffffff;  // per-lane part of a store's offset
+  // loads through a buffer resource over the rows this band reads (clamped
+  // into the image): the row's offset is a scalar, the lane's a constant,
+  // so a row costs no vector address arithmetic
+  const int yb = max(y0 - 2, 0), ye = min(y0 + kR + 2, a.height);
+  const __amdgpu_buffer_rsrc_t in_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t *>(a.in) + (size_t)yb * (size_t)a.width, 0, (ye - yb) * a.width * 4,
+      0x00020000);
+  // a wave that does not touch the image's left or right edge skips the
+  // edge rule (a wave-uniform branch around eight selects per row)
+  const bool edge_wave = x0 == 0 || x0 + kStripPx >= a.width;
 
   int cxk[4];
 #pragma unroll
@@ -243,13 +259,21 @@ __global__ __launch_bounds__(kBlock) void blur_rgba_rows_kernel(const StreamArgs
 #pragma unroll
   for (int k = 0; k < 4; k++) hs[k] = 0;
 
+  // every lane loads, so the loads' count is fixed (no branch); lanes 1..62
+  // read lane 0's two pixels (one address for the whole group: all 64 lanes
+  // at their own addresses measured 0.8 us slower)
+  const int hxl = lane == 63 ? hx : __builtin_amdgcn_readfirstlane(hx);
+  auto row_offset = [&](int y) -> int {
+    const int cy = min(max(y, 0), a.height - 1);
+    return __builtin_amdgcn_readfirstlane((cy - yb) * a.width * 4);
+  };
+  auto load_row = [&](int y) -> u32x4 {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(in_rsrc, lx * 4,
+                                                                           row_offset(y), 0));
+  };
   auto load_halo = [&](int y) -> u32x2 {
-    u32x2 v = {0u, 0u};
-    int cy = y;
-    if (kMode == SH_BLUR_CONFIG) cy = min(max(y, 0), a.height - 1);
-    else if (y < 0 || y >= a.height) return v;
-    if (halo_lane) v = *reinterpret_cast<const u32x2 *>(a.in + (size_t)cy * (size_t)a.width + hx);
-    return v;
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(in_rsrc, hxl * 4,
+                                                                          row_offset(y), 0));
   };
   auto expand_halo = [&](const u32x2 v, int y, uint32_t e[4]) {
     if (kMode == SH_BLUR_REFERENCE && (y < 0 || y >= a.height)) {
@@ -265,37 +289,38 @@ __global__ __launch_bounds__(kBlock) void blur_rgba_rows_kernel(const StreamArgs
     }
   };
 
-  u32x4 raw[kQ];
-  u32x2 hraw[kQ];
+  // raw[j % 5]: row j's load in flight (requested 5 steps before its use);
+  // ex[j % 5]: row j expanded to 16-bit lanes, kept until it leaves the
+  // window 5 steps later (re-expanding the leaving row cost ~20 of the ~140
+  // vector instructions per row, and the kernel is bound by them)
+  u32x4 raw[kL];
+  u32x2 hraw[kL];
+  uint32_t ex[kQ][8], exh[kQ][4];
 #pragma unroll
-  for (int i = 0; i < 5; i++) {
-    raw[i] = load_row<kMode>(a, ys + dy * i, lx);
+  for (int i = 0; i < kL && i < kR + 4; i++) {
+    raw[i] = load_row(ys + dy * i);
     hraw[i] = load_halo(ys + dy * i);
   }
 #pragma unroll
   for (int i = 0; i < kR + 4; i++) {
-    if (i >= 5) {
-      uint32_t e[8], eh[4];
-      expand_row<kMode, kFuse>(raw[(i - 5) % kQ], ys + dy * (i - 5), a.height, e, a.d_lo,
-                               a.d_hi);
-      expand_halo(hraw[(i - 5) % kQ], ys + dy * (i - 5), eh);
-#pragma unroll
-      for (int k = 0; k < 8; k++) vs[k] -= e[k];
-#pragma unroll
-      for (int k = 0; k < 4; k++) hs[k] -= eh[k];
+    uint32_t e[8], eh[4];
+    expand_row<kMode, kFuse>(raw[i % kL], ys + dy * i, a.height, e, a.d_lo, a.d_hi);
+    expand_halo(hraw[i % kL], ys + dy * i, eh);
+    if (i + kL < kR + 4) {  // the slot is free: request the row kL steps ahead
+      raw[i % kL] = load_row(ys + dy * (i + kL));
+      hraw[i % kL] = load_halo(ys + dy * (i + kL));
     }
-    if (i + 5 < kR + 4) {
-      raw[(i + 5) % kQ] = load_row<kMode>(a, ys + dy * (i + 5), lx);
-      hraw[(i + 5) % kQ] = load_halo(ys + dy * (i + 5));
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      vs[k] += e[k];
+      if (i >= kQ) vs[k] -= ex[i % kQ][k];
+      ex[i % kQ][k] = e[k];
     }
-    {
-      uint32_t e[8], eh[4];
-      expand_row<kMode, kFuse>(raw[i % kQ], ys + dy * i, a.height, e, a.d_lo, a.d_hi);
-      expand_halo(hraw[i % kQ], ys + dy * i, eh);
 #pragma unroll
-      for (int k = 0; k < 8; k++) vs[k] += e[k];
-#pragma unroll
-      for (int k = 0; k < 4; k++) hs[k] += eh[k];
+    for (int k = 0; k < 4; k++) {
+      hs[k] += eh[k];
+      if (i >= kQ) hs[k] -= exh[i % kQ][k];
+      exh[i % kQ][k] = eh[k];
     }
     if (i >= 4) {
       const int y = ys + dy * (i - 2), row = y - y0;  // the window's centre row
@@ -318,7 +343,8 @@ __global__ __launch_bounds__(kBlock) void blur_rgba_rows_kernel(const StreamArgs
       lo[7] = from_right(lo[3], hs[2]);
       hi[6] = from_right(hi[2], hs[1]);
       hi[7] = from_right(hi[3], hs[3]);
-      if (kMode == SH_BLUR_CONFIG) {
+      if (!edge_wave) {
+      } else if (kMode == SH_BLUR_CONFIG) {
         lo[0] = left_edge ? lo[2] : lo[0];
         lo[1] = left_edge ? lo[2] : lo[1];
         hi[0] = left_edge ? hi[2] : hi[0];
@@ -348,7 +374,7 @@ __global__ __launch_bounds__(kBlock) void blur_rgba_rows_kernel(const StreamArgs
         h[4 + part] = t + q[2] + q[6] + bias;
         h[6 + part] = t + q[6] + q[7] + bias;
       }
-      if (writer && row < out_rows) {
+      {
         const uint32_t ry = kMode == SH_BLUR_CONFIG
                                 ? 5u
                                 : (uint32_t)(min(y + 2, a.height - 1) - max(y - 2, 0) + 1);
@@ -357,8 +383,9 @@ __global__ __launch_bounds__(kBlock) void blur_rgba_rows_kernel(const StreamArgs
         o.y = finish_pixel<kMode>(h[2], h[3], ry * cxk[1]);
         o.z = finish_pixel<kMode>(h[4], h[5], ry * cxk[2]);
         o.w = finish_pixel<kMode>(h[6], h[7], ry * cxk[3]);
-        __builtin_nontemporal_store(
-            o, reinterpret_cast<u32x4 *>(a.out + (size_t)y * (size_t)a.width + cx));
+        // rows past the image's bottom land past the resource's end too
+        __builtin_amdgcn_raw_buffer_store_b128(
+            o, out_rsrc, out_lane, __builtin_amdgcn_readfirstlane(row * a.width * 4), 2);  // 2: nt
       }
     }
   }
@@ -453,11 +480,11 @@ template <int kMode, int kR>
 void launch_rows_fuse(hipStream_t s, const StreamArgs &a, int fuse) {
   const int blocks = a.xcd_blocks * 8;
   if (fuse == 1)
-    blur_rgba_rows_kernel<kMode, 1, kR><<<blocks, kBlock, 0, s>>>(a);
+    blur_rgba_rows_kernel<kMode, 1, kR><<<blocks, kBlurBlock, 0, s>>>(a);
   else if (fuse == 2)
-    blur_rgba_rows_kernel<kMode, 2, kR><<<blocks, kBlock, 0, s>>>(a);
+    blur_rgba_rows_kernel<kMode, 2, kR><<<blocks, kBlurBlock, 0, s>>>(a);
   else
-    blur_rgba_rows_kernel<kMode, 0, kR><<<blocks, kBlock, 0, s>>>(a);
+    blur_rgba_rows_kernel<kMode, 0, kR><<<blocks, kBlurBlock, 0, s>>>(a);
 }
 
 template <int kRowsPerWave>
@@ -473,7 +500,7 @@ void launch_blur_stream(hipStream_t s, const uint32_t *in, uint32_t *out, int wi
   a.total_waves = a.strips_x * bands;
   // padded to a multiple of 8 workgroups (the extra waves exit at once) so
   // that every XCD gets an equal contiguous range of bands
-  const int blocks = ((a.total_waves + kBlock / 64 - 1) / (kBlock / 64) + 7) / 8 * 8;
+  const int blocks = ((a.total_waves + kBlurBlock / 64 - 1) / (kBlurBlock / 64) + 7) / 8 * 8;
   a.xcd_blocks = blocks / 8;
   int f = 0;
   a.d_lo = a.d_hi = 0;
