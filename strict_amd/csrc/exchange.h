@@ -1,0 +1,145 @@
+// Exchange between the workgroups of a persistent kernel: values handed on
+// within a launch travel in 8-byte cells of device memory, payload in the
+// low word and the producing (step, layer) tag in the high word. A consumer
+// loads the cells it needs until each carries the tag it expects, so the data
+// is its own completion flag. Every cell access is a relaxed 64-bit
+// agent-scope atomic, which the memory model keeps coherent across the XCDs'
+// separate L2 caches. Every wait is bounded by a wall-clock limit; a timeout
+// sets the sticky error word, after which every other wait gives up at once,
+// so the grid always drains.
+//
+// The helpers take the kernel's argument struct, which must provide
+// `unsigned *err` and `unsigned long long spin_ticks`.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace sh {
+namespace xchg {
+
+#define SH_XGLOBAL __attribute__((address_space(1)))
+#define SH_XCONST __attribute__((address_space(4)))
+
+// Pointers cast to the global address space: loads through generic pointers
+// compile to flat instructions, which also count against the LDS wait
+// counter (every LDS wait would then wait for outstanding global requests).
+template <class T>
+__device__ __forceinline__ SH_XGLOBAL T *gbl(T *p) {
+  return (SH_XGLOBAL T *)p;
+}
+
+// Tables written before the launch and only read by it, through the constant
+// address space: uniform reads become scalar loads on their own counter.
+template <class T>
+__device__ __forceinline__ const SH_XCONST T *cnst(const T *p) {
+  return (const SH_XCONST T *)p;
+}
+
+// Tag of the values layer l of step `epoch` produces (epoch >= 1, l < 63,
+// so never 0, the value of never-written cells).
+__device__ __forceinline__ unsigned tag_of(unsigned epoch, int l) {
+  return epoch * 64u + (unsigned)l + 1u;
+}
+
+__device__ __forceinline__ uint64_t cld(const uint64_t *base, size_t cell) {
+  return __hip_atomic_load(base + cell, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void cst(uint64_t *base, size_t cell, uint32_t v, unsigned tag) {
+  __hip_atomic_store(base + cell, (uint64_t)v | ((uint64_t)tag << 32), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float cell_f32(uint64_t c) { return __builtin_bit_cast(float, (uint32_t)c); }
+__device__ __forceinline__ uint32_t bits_of(float f) { return __builtin_bit_cast(uint32_t, f); }
+
+template <class A>
+__device__ __forceinline__ unsigned ld_err(const A &a) {
+  return __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Loads base[at(k)], k < kN, until each one with bit k of mask set carries
+// `tag`; c[k] receives them. at(k) must name a valid cell for every k
+// (unused ones clamped onto used cells, so the loads need no branch). False
+// when the wait exceeded the limit or another wait has failed.
+template <int kN, class A, class At>
+__device__ __forceinline__ bool spin_cells(const A &a, const uint64_t *base, At at, uint64_t mask,
+                                           unsigned tag, uint64_t (&c)[kN]) {
+  unsigned long long t0 = 0;
+  for (int it = 0;; it++) {
+#pragma unroll
+    for (int k = 0; k < kN; k++) c[k] = cld(base, at(k));
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < kN; k++) ok = ok && ((mask >> k & 1) == 0 || (uint32_t)(c[k] >> 32) == tag);
+    if (ok) return true;
+    if (it == 0) {
+      t0 = wall_clock64();
+    } else if ((it & 7) == 0 && (ld_err(a) != 0 || wall_clock64() - t0 > a.spin_ticks)) {
+      return false;
+    }
+  }
+}
+
+// One cell already requested as `c`: polls it again until it carries `tag`.
+template <class A>
+__device__ __forceinline__ bool finish_cell(const A &a, const uint64_t *base, size_t cell,
+                                            unsigned tag, uint64_t &c) {
+  unsigned long long t0 = 0;
+  for (int it = 0; (uint32_t)(c >> 32) != tag; it++) {
+    if (it == 0) {
+      t0 = wall_clock64();
+    } else if ((it & 7) == 0 && (ld_err(a) != 0 || wall_clock64() - t0 > a.spin_ticks)) {
+      return false;
+    }
+    c = cld(base, cell);
+  }
+  return true;
+}
+
+// Workgroup barrier for LDS traffic only (vmcnt left alone): a
+// __syncthreads() fence would make each wave wait for every global store it
+// issued (cell stores) before the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Votes of block_any: two alternating sets, each wave's parity in its own
+// word (a wave that runs ahead writes the other set).
+struct Votes {
+  int vote[2][4];
+  int par[4];
+};
+
+// True in every thread when p holds in any thread (a barrier; 4 waves).
+__device__ __forceinline__ bool block_any(bool p, Votes *v) {
+  const int wave = threadIdx.x >> 6;
+  const int par = v->par[wave];
+  const bool any = __any(p ? 1 : 0) != 0;
+  if ((threadIdx.x & 63) == 0) {
+    v->vote[par][wave] = any ? 1 : 0;
+    v->par[wave] = par ^ 1;
+  }
+  lds_barrier();
+  const int *vt = v->vote[par];
+  return (vt[0] | vt[1] | vt[2] | vt[3]) != 0;
+}
+
+// Every thread's wait succeeded (workgroup-uniform); otherwise marks the
+// sticky error.
+template <class A>
+__device__ __forceinline__ bool waits_ok(const A &a, bool ok, Votes *v) {
+  if (block_any(!ok, v)) {
+    if (threadIdx.x == 0) atomicOr(a.err, 1u);
+    return false;
+  }
+  return true;
+}
+
+}  // namespace xchg
+}  // namespace sh

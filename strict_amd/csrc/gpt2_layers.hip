@@ -1,0 +1,568 @@
+// Persistent GPT-2 layers kernel: all decoder layers of one GPT-2 decode
+// step at batch 1 (fp16 weights, head_dim 64, LayerNorm, biases, GELU) in one
+// launch, one workgroup per CU, all resident together. It replaces the five
+// kernels per layer of the per-op path (LayerNorm + QKV GEMV, attention,
+// O GEMV + residual, LayerNorm + fc GEMV + GELU, proj GEMV + residual), each
+// ~3-6 us whatever its size, with exchanges between workgroups of ~1-1.5 us.
+//
+// Work per layer, as items spread over the workgroups:
+//   A  QKV   one 16-row tile of W_qkv each      (LayerNorm of x in every item)
+//   B  attn  one (head, split) each             (cache append, partial softmax)
+//   C  O     one 16-row tile of W_o each        (merges the splits of every
+//                                                head, x_mid = x + W_o attn + b)
+//   D  fc    one 16-row tile of W_fc each       (LayerNorm of x_mid, GELU)
+//   E  proj  one 16-row tile of W_proj each     (x = x_mid + W_proj act + b)
+// The final LayerNorm and the LM head run after the launch (the per-op
+// kernels), reading the last layer's x from the plain buffer x_in.
+//
+// Items: A on workgroups 0.., C and E on 0.., D after the C range, B on the
+// last workgroups; at most one item per workgroup and phase. Exchange:
+// exchange.h (tagged cells, bounded waits). Weights and K / V do not depend
+// on the step's activations: each workgroup requests the next layer's QKV
+// weights and K / V after its last item of a layer, and an item's other
+// weights when it starts, so they arrive while earlier phases run.
+//
+// Rounding points follow the per-op path and the oracle: LayerNorm
+// statistics in fp32 over the row, its output fp16 (the MFMA A operand);
+// q, k, v fp32 from the QKV GEMV, k and v stored fp16 in the cache; q scaled
+// by 1 / sqrt(64) in fp32; scores, softmax and the V sums in fp32, the
+// merged attention output fp16; residual stream fp32; GELU output fp16.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+#include "exchange.h"
+#include "llm.h"
+#include "llm_device.h"
+
+namespace sh {
+namespace {
+
+using namespace xchg;
+
+constexpr int kT = 256;     // threads per workgroup (4 waves)
+constexpr int kHd = 64;     // head dim
+constexpr int kMaxChunk = 256;  // positions per split (one per thread)
+constexpr int kVJ = kMaxChunk / 32;  // V rows per thread
+
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+struct LayerP {
+  const SH_XGLOBAL uint16_t *wqkv, *wo, *wfc, *wproj;
+  const SH_XGLOBAL float *bqkv, *bo, *bfc, *bproj;
+  const SH_XGLOBAL float *ln1_g, *ln1_b, *ln2_g, *ln2_b;
+  SH_XGLOBAL uint16_t *kcache, *vcache;
+};
+
+__device__ __forceinline__ LayerP layer_p(const Gpt2Args &a, int l) {
+  const SH_XCONST Gpt2LayerPtrs &p = cnst(a.layers)[l];
+  return LayerP{gbl(p.wqkv),  gbl(p.wo),    gbl(p.wfc),   gbl(p.wproj), gbl(p.bqkv),
+                gbl(p.bo),    gbl(p.bfc),   gbl(p.bproj), gbl(p.ln1_g), gbl(p.ln1_b),
+                gbl(p.ln2_g), gbl(p.ln2_b), gbl(p.kcache), gbl(p.vcache)};
+}
+
+// LDS of a workgroup (one batch row).
+struct Lds {
+  alignas(16) _Float16 xs[4096 + 8];  // the MFMA A operand row (fp16)
+  alignas(16) float red[3][64][4];    // waves 1..3's accumulators
+  float part[4];                      // per-wave partial sums
+  Votes votes;
+  // attention
+  alignas(16) float q[kHd];
+  alignas(16) _Float16 knew[kHd];
+  alignas(16) _Float16 vnew[kHd];
+  float p[kMaxChunk];
+  float wmax[4], wl[4];
+  alignas(16) float pv[4][kHd];
+};
+
+// ---- GEMV items ----------------------------------------------------------------
+
+// This wave's quarter of K for 16-row tile g of an fp16 tiled matrix with K
+// columns (1 KiB tiles of 16 rows x 32 K): kL 16-byte loads per lane.
+template <int kL>
+__device__ __forceinline__ void load_weights(u32x4 (&w)[kL], const SH_XGLOBAL uint16_t *W, int K, int g) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tiles = K >> 5;
+#pragma unroll
+  for (int u = 0; u < kL; u++) {
+    const size_t tile = (size_t)g * tiles + wave * kL + u;
+    w[u] = __builtin_nontemporal_load(reinterpret_cast<const SH_XGLOBAL u32x4 *>(
+        reinterpret_cast<const SH_XGLOBAL uint8_t *>(W) + tile * 1024 + (size_t)lane * 16));
+  }
+}
+
+// This wave's K quarter of row 0 of xs times the tile (lanes 0..15 of the
+// result's r = 0 hold the 16 columns; every A row reads row 0).
+template <int kL>
+__device__ __forceinline__ f32x4 mfma_weights(const u32x4 (&w)[kL], const _Float16 *xs) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const _Float16 *xrow = xs + wave * kL * 32 + 8 * (lane >> 4);
+  constexpr int kCh = kL < 4 ? kL : 4;  // independent accumulator chains
+  f32x4 part[kCh];
+#pragma unroll
+  for (int c = 0; c < kCh; c++) part[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < kL; u++) {
+    const f16x8 af = *reinterpret_cast<const f16x8 *>(xrow + u * 32);
+    part[u % kCh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, __builtin_bit_cast(f16x8, w[u]),
+                                                          part[u % kCh], 0, 0, 0);
+  }
+  f32x4 acc = part[0];
+#pragma unroll
+  for (int c = 1; c < kCh; c++) acc += part[c];
+  return acc;
+}
+
+// Sums the four waves' accumulators; the result is valid in wave 0.
+__device__ __forceinline__ f32x4 reduce_waves(f32x4 acc, Lds &S) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (wave > 0) *reinterpret_cast<f32x4 *>(S.red[wave - 1][lane]) = acc;
+  lds_barrier();
+  if (wave == 0) {
+    const f32x4 r1 = *reinterpret_cast<const f32x4 *>(S.red[0][lane]);
+    const f32x4 r2 = *reinterpret_cast<const f32x4 *>(S.red[1][lane]);
+    const f32x4 r3 = *reinterpret_cast<const f32x4 *>(S.red[2][lane]);
+    acc = (acc + r1) + (r2 + r3);
+  }
+  return acc;
+}
+
+// Sum of one value per thread over the workgroup (every thread gets it).
+__device__ __forceinline__ float block_sum(float v, Lds &S) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = wave_sum_rows(v);
+  if (lane == 0) S.part[wave] = v;
+  lds_barrier();
+  const float s = (S.part[0] + S.part[1]) + (S.part[2] + S.part[3]);
+  lds_barrier();  // part is reused by the next call
+  return s;
+}
+
+// LayerNorm of the fp32 row x (K values: cells tagged `tag`, or the plain
+// buffer xp) with gains g and biases b -> xs (fp16). Thread t holds the
+// 4-value chunks t + 256 j, j < kC.
+template <int kC>
+__device__ __forceinline__ bool stage_ln(const Gpt2Args &a, const uint64_t *xc, const float *xp,
+                                         unsigned tag, const SH_XGLOBAL float *g,
+                                         const SH_XGLOBAL float *bta, int K, Lds &S) {
+  const int t = threadIdx.x, c4 = K >> 2;
+  f32x4 gv[kC], bv[kC], v[kC];
+#pragma unroll
+  for (int j = 0; j < kC; j++) {
+    const int c = min(t + kT * j, c4 - 1);
+    gv[j] = *reinterpret_cast<const SH_XGLOBAL f32x4 *>(g + c * 4);
+    bv[j] = *reinterpret_cast<const SH_XGLOBAL f32x4 *>(bta + c * 4);
+  }
+  bool ok = true;
+  if (xp) {
+#pragma unroll
+    for (int j = 0; j < kC; j++)
+      v[j] = *reinterpret_cast<const SH_XGLOBAL f32x4 *>(gbl(xp) + min(t + kT * j, c4 - 1) * 4);
+  } else {
+    uint64_t cv[kC * 4];
+    uint64_t mask = 0;
+#pragma unroll
+    for (int j = 0; j < kC; j++)
+      if (t + kT * j < c4) mask |= 15ull << (j * 4);
+    ok = spin_cells(a, xc, [&](int k) { return (size_t)min(t + kT * (k >> 2), c4 - 1) * 4 + (k & 3); },
+                    mask, tag, cv);
+#pragma unroll
+    for (int j = 0; j < kC; j++)
+      v[j] = f32x4{cell_f32(cv[4 * j]), cell_f32(cv[4 * j + 1]), cell_f32(cv[4 * j + 2]),
+                   cell_f32(cv[4 * j + 3])};
+  }
+  if (!waits_ok(a, ok, &S.votes)) return false;
+  float sm = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kC; j++)
+    if (t + kT * j < c4) sm += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
+  const float mean = block_sum(sm, S) / (float)K;
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kC; j++)
+    if (t + kT * j < c4) {
+      const f32x4 d = v[j] - mean;
+      ss += (d[0] * d[0] + d[1] * d[1]) + (d[2] * d[2] + d[3] * d[3]);
+    }
+  const float inv = 1.0f / sqrtf(block_sum(ss, S) / (float)K + a.eps);
+#pragma unroll
+  for (int j = 0; j < kC; j++) {
+    const int c = t + kT * j;
+    if (c < c4) {
+      const f32x4 y = (v[j] - mean) * inv * gv[j] + bv[j];
+      *reinterpret_cast<f16x4 *>(S.xs + c * 4) =
+          f16x4{(_Float16)y[0], (_Float16)y[1], (_Float16)y[2], (_Float16)y[3]};
+    }
+  }
+  lds_barrier();
+  return true;
+}
+
+// fp16 row of K values packed two per cell (tagged `tag`) -> xs. Thread t
+// holds the two-cell chunks t + 256 j, j < kC.
+template <int kC>
+__device__ __forceinline__ bool stage_f16(const Gpt2Args &a, const uint64_t *cells, unsigned tag,
+                                          int K, Lds &S) {
+  const int t = threadIdx.x, c4 = K >> 2;
+  uint64_t cv[kC * 2];
+  uint64_t mask = 0;
+#pragma unroll
+  for (int j = 0; j < kC; j++)
+    if (t + kT * j < c4) mask |= 3ull << (j * 2);
+  const bool ok = spin_cells(a, cells, [&](int k) { return (size_t)min(t + kT * (k >> 1), c4 - 1) * 2 + (k & 1); },
+                             mask, tag, cv);
+  if (!waits_ok(a, ok, &S.votes)) return false;
+#pragma unroll
+  for (int j = 0; j < kC; j++) {
+    const int c = t + kT * j;
+    if (c < c4) *reinterpret_cast<u32x2 *>(S.xs + c * 4) = u32x2{(uint32_t)cv[2 * j], (uint32_t)cv[2 * j + 1]};
+  }
+  lds_barrier();
+  return true;
+}
+
+// A: qkv[16 i + c] = W_qkv LayerNorm(x) + b; w holds the item's weights
+template <int kLH>
+__device__ __forceinline__ bool qkv_item(const Gpt2Args &a, const LayerP &P, int l, int i, unsigned ep,
+                                         Lds &S, const u32x4 (&w)[kLH]) {
+  const int lane = threadIdx.x & 63, col = lane & 15;
+  const float bias = P.bqkv[i * 16 + col];
+  __builtin_amdgcn_sched_barrier(0);
+  if (!stage_ln<(kLH * 128 + 1023) / 1024>(a, a.x0c, l == 0 ? a.x_in : nullptr, tag_of(ep, l - 1),
+                                            P.ln1_g, P.ln1_b, a.H, S))
+    return false;
+  f32x4 acc = reduce_waves(mfma_weights<kLH>(w, S.xs), S);
+  if (threadIdx.x < 16) cst(a.qkvc, (size_t)i * 16 + col, bits_of(acc[0] + bias), tag_of(ep, l));
+  return true;
+}
+
+// K / V rows of attention item (head h, split s), requested ahead of the
+// item: thread t holds K[p0 + t][0..63] and, for dims 8 (t % 8) .., the V
+// rows p0 + t / 8 + 32 j. Positions are clamped to the cached ones (before
+// this step's token, which the item substitutes from its cells).
+struct AttnKV {
+  u32x4 k[8];
+  u32x4 v[kVJ];
+};
+
+__device__ __forceinline__ void attn_prefetch(const Gpt2Args &a, const LayerP &P, int item, int L,
+                                              AttnKV &kv) {
+  const int h = item / kGpt2Splits, s = item % kGpt2Splits, t = threadIdx.x;
+  const int p0 = s * a.chunk, last = max(min(L - 2, p0 + a.chunk - 1), 0);
+  const SH_XGLOBAL uint16_t *kb = P.kcache + (size_t)h * a.max_pos * kHd;
+  const SH_XGLOBAL uint16_t *vb = P.vcache + (size_t)h * a.max_pos * kHd;
+  const int pk = min(p0 + t, last);
+#pragma unroll
+  for (int e = 0; e < 8; e++)
+    kv.k[e] = *reinterpret_cast<const SH_XGLOBAL u32x4 *>(kb + (size_t)pk * kHd + 8 * e);
+  const int d8 = t & 7, pg = t >> 3;
+#pragma unroll
+  for (int j = 0; j < kVJ; j++) {
+    const int pv = min(p0 + pg + 32 * j, last);
+    kv.v[j] = *reinterpret_cast<const SH_XGLOBAL u32x4 *>(vb + (size_t)pv * kHd + 8 * d8);
+  }
+}
+
+__device__ __forceinline__ float dot8(const f16x8 k, const float *q) {
+  float s = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) s += q[e] * (float)k[e];
+  return s;
+}
+
+// B: item = (head h, split s): positions [p0, min(p0 + chunk, L)) of the
+// context. Appends the new token's k / v to the cache when the split holds
+// it, writes the partial (unnormalised V sum, max, sum) as cells. Splits past
+// the context write nothing.
+__device__ __forceinline__ bool attn_item(const Gpt2Args &a, const LayerP &P, int l, int item,
+                                          unsigned ep, int L, Lds &S, AttnKV &kv) {
+  const int h = item / kGpt2Splits, s = item % kGpt2Splits;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int p0 = s * a.chunk;
+  if (p0 >= L) return true;  // uniform
+  const int np = min(a.chunk, L - p0), pos = L - 1;
+  const bool holds_new = p0 + np == L;
+  const unsigned tag = tag_of(ep, l);
+  {  // q (threads 0..63), the new k (64..127), the new v (128..191)
+    const int part = min(t >> 6, 2), d = lane;
+    const size_t cell = (size_t)part * a.H + (size_t)h * kHd + d;
+    uint64_t cv[1];
+    const bool ok = spin_cells(a, a.qkvc, [&](int) { return cell; }, t < 192 ? 1ull : 0ull, tag, cv);
+    if (!waits_ok(a, ok, &S.votes)) return false;
+    const float v = cell_f32(cv[0]);
+    if (t < 64) {
+      S.q[d] = v * a.scale;
+    } else if (t < 192) {
+      const _Float16 hv = (_Float16)v;
+      if (t < 128) S.knew[d] = hv;
+      else S.vnew[d] = hv;
+      if (holds_new) {
+        SH_XGLOBAL uint16_t *c = (t < 128 ? P.kcache : P.vcache) + ((size_t)h * a.max_pos + pos) * kHd + d;
+        *c = __builtin_bit_cast(uint16_t, hv);
+      }
+    }
+  }
+  lds_barrier();
+  // scores: thread t scores position p0 + t
+  float sc = -INFINITY;
+  if (t < np) {
+    const bool fresh = p0 + t == pos;
+    float acc = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const f16x8 kr = fresh ? *reinterpret_cast<const f16x8 *>(&S.knew[8 * e])
+                             : __builtin_bit_cast(f16x8, kv.k[e]);
+      acc += dot8(kr, &S.q[8 * e]);
+    }
+    sc = acc;
+  }
+  float m = wave_max_rows(sc);
+  if (lane == 0) S.wmax[wave] = m;
+  lds_barrier();
+  m = fmaxf(fmaxf(S.wmax[0], S.wmax[1]), fmaxf(S.wmax[2], S.wmax[3]));
+  const float e = t < np ? expf(sc - m) : 0.0f;
+  S.p[t] = e;
+  const float ls = wave_sum_rows(e);
+  if (lane == 0) S.wl[wave] = ls;
+  lds_barrier();
+  const float lsum = (S.wl[0] + S.wl[1]) + (S.wl[2] + S.wl[3]);
+  // V sums: thread (d8 = t % 8, pg = t / 8) over positions pg + 32 j
+  const int d8 = t & 7, pg = t >> 3;
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < kVJ; j++) {
+    const int pi = pg + 32 * j;
+    if (pi < np) {
+      const float pw = S.p[pi];
+      const f16x8 vr = p0 + pi == pos ? *reinterpret_cast<const f16x8 *>(&S.vnew[8 * d8])
+                                      : __builtin_bit_cast(f16x8, kv.v[j]);
+#pragma unroll
+      for (int q = 0; q < 8; q++) o[q] += pw * (float)vr[q];
+    }
+  }
+  // sum over pg: lanes l, l ^ 8, l ^ 16, l ^ 32 share d8 within a wave
+#pragma unroll
+  for (int q = 0; q < 8; q++) {
+    o[q] += __shfl_xor(o[q], 8, 64);
+    o[q] += __shfl_xor(o[q], 16, 64);
+    o[q] += __shfl_xor(o[q], 32, 64);
+  }
+  if (lane < 8) {
+#pragma unroll
+    for (int q = 0; q < 8; q++) S.pv[wave][8 * lane + q] = o[q];
+  }
+  lds_barrier();
+  const size_t pp = ((size_t)h * kGpt2Splits + s) * kGpt2PStride;
+  if (t < kHd) {
+    const float v = (S.pv[0][t] + S.pv[1][t]) + (S.pv[2][t] + S.pv[3][t]);
+    cst(a.partc, pp + t, bits_of(v), tag);
+  } else if (t == kHd) {
+    cst(a.partc, pp + kHd, bits_of(m), tag);
+  } else if (t == kHd + 1) {
+    cst(a.partc, pp + kHd + 1, bits_of(lsum), tag);
+  }
+  return true;
+}
+
+// The attention output of every head (the splits merged, fp16) -> xs:
+// thread t computes values t + 256 j, j < kC, of the H = heads * 64.
+template <int kC>
+__device__ __forceinline__ bool stage_attn(const Gpt2Args &a, unsigned tag, int L, Lds &S) {
+  const int t = threadIdx.x, ns = (L + a.chunk - 1) / a.chunk;
+  constexpr int kN = kC * kGpt2Splits * 3;
+  uint64_t cv[kN];
+  uint64_t mask = 0;
+#pragma unroll
+  for (int j = 0; j < kC; j++)
+#pragma unroll
+    for (int s = 0; s < kGpt2Splits; s++)
+      if (s < ns && t + kT * j < a.H) mask |= 7ull << ((j * kGpt2Splits + s) * 3);
+  const bool ok = spin_cells(a, a.partc,
+                             [&](int k) {
+                               const int j = k / (kGpt2Splits * 3), s = (k / 3) % kGpt2Splits, f = k % 3;
+                               const int idx = min(t + kT * j, a.H - 1), h = idx >> 6, d = idx & 63;
+                               const size_t pp = ((size_t)h * kGpt2Splits + min(s, ns - 1)) * kGpt2PStride;
+                               return pp + (f == 0 ? d : kHd + f - 1);
+                             },
+                             mask, tag, cv);
+  if (!waits_ok(a, ok, &S.votes)) return false;
+#pragma unroll
+  for (int j = 0; j < kC; j++) {
+    const int idx = t + kT * j;
+    if (idx >= a.H) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < kGpt2Splits; s++)
+      if (s < ns) M = fmaxf(M, cell_f32(cv[(j * kGpt2Splits + s) * 3 + 1]));
+    float num = 0.0f, den = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kGpt2Splits; s++)
+      if (s < ns) {
+        const int k = (j * kGpt2Splits + s) * 3;
+        const float f = expf(cell_f32(cv[k + 1]) - M);
+        num += f * cell_f32(cv[k]);
+        den += f * cell_f32(cv[k + 2]);
+      }
+    S.xs[idx] = (_Float16)(num / den);
+  }
+  lds_barrier();
+  return true;
+}
+
+// C: x_mid[16 i + c] = x[.] + W_o attn + b
+template <int kLH>
+__device__ __forceinline__ bool o_item(const Gpt2Args &a, const LayerP &P, int l, int i, unsigned ep,
+                                       int L, Lds &S) {
+  const int lane = threadIdx.x & 63, col = lane & 15;
+  u32x4 w[kLH];
+  load_weights<kLH>(w, P.wo, a.H, i);
+  const float bias = P.bo[i * 16 + col];
+  const size_t cell = (size_t)i * 16 + col;
+  uint64_t rc = cld(a.x0c, cell);  // the residual (layer 0: the plain input)
+  const float x0 = l == 0 ? gbl(a.x_in)[cell] : 0.0f;
+  __builtin_amdgcn_sched_barrier(0);
+  if (!stage_attn<(kLH * 128 + 255) / 256>(a, tag_of(ep, l), L, S)) return false;
+  const f32x4 acc = reduce_waves(mfma_weights<kLH>(w, S.xs), S);
+  if (threadIdx.x < 16) {
+    float x = x0;
+    if (l > 0) {
+      if (!finish_cell(a, a.x0c, cell, tag_of(ep, l - 1), rc)) atomicOr(a.err, 1u);
+      x = cell_f32(rc);
+    }
+    cst(a.x1c, cell, bits_of(x + (acc[0] + bias)), tag_of(ep, l));
+  }
+  asm volatile("" ::"v"(rc));  // the residual load retires here in every thread
+  return true;
+}
+
+// D: act[16 i + c] = gelu(W_fc LayerNorm(x_mid) + b), fp16, two per cell
+template <int kLH>
+__device__ __forceinline__ bool fc_item(const Gpt2Args &a, const LayerP &P, int l, int i, unsigned ep,
+                                        Lds &S) {
+  const int lane = threadIdx.x & 63, col = lane & 15;
+  u32x4 w[kLH];
+  load_weights<kLH>(w, P.wfc, a.H, i);
+  const float bias = P.bfc[i * 16 + col];
+  __builtin_amdgcn_sched_barrier(0);
+  if (!stage_ln<(kLH * 128 + 1023) / 1024>(a, a.x1c, nullptr, tag_of(ep, l), P.ln2_g, P.ln2_b, a.H, S))
+    return false;
+  const f32x4 acc = reduce_waves(mfma_weights<kLH>(w, S.xs), S);
+  if (threadIdx.x < 64) {
+    const uint32_t hv = f32_to_f16_bits(gelu_tanh(acc[0] + bias));
+    const uint32_t nb = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hv, 0xB1, 0xf, 0xf, false);
+    if (threadIdx.x < 16 && (col & 1) == 0)
+      cst(a.actc, ((size_t)i * 16 + col) / 2, hv | (nb << 16), tag_of(ep, l));
+  }
+  return true;
+}
+
+// E: x[16 i + c] = x_mid[.] + W_proj act + b; the last layer also writes the
+// plain buffer the final LayerNorm reads
+template <int kLH, int kLI>
+__device__ __forceinline__ bool proj_item(const Gpt2Args &a, const LayerP &P, int l, int i, unsigned ep,
+                                          Lds &S) {
+  const int lane = threadIdx.x & 63, col = lane & 15;
+  u32x4 w[kLI];
+  load_weights<kLI>(w, P.wproj, a.inter, i);
+  const float bias = P.bproj[i * 16 + col];
+  const size_t cell = (size_t)i * 16 + col;
+  const unsigned tag = tag_of(ep, l);
+  uint64_t rc = cld(a.x1c, cell);
+  __builtin_amdgcn_sched_barrier(0);
+  if (!stage_f16<(kLI * 128 + 1023) / 1024>(a, a.actc, tag, a.inter, S)) return false;
+  const f32x4 acc = reduce_waves(mfma_weights<kLI>(w, S.xs), S);
+  if (threadIdx.x < 16) {
+    if (!finish_cell(a, a.x1c, cell, tag, rc)) atomicOr(a.err, 1u);
+    const float v = cell_f32(rc) + (acc[0] + bias);
+    if (l + 1 == a.n_layers) gbl(a.x_in)[cell] = v;
+    cst(a.x0c, cell, bits_of(v), tag);
+  }
+  asm volatile("" ::"v"(rc));
+  return true;
+}
+
+template <int kLH, int kLI>
+__global__ __launch_bounds__(kT, 1) void gpt2_layers_kernel(const Gpt2Args a) {
+  __shared__ Lds S;
+  if (threadIdx.x < 4) S.votes.par[threadIdx.x] = 0;
+  lds_barrier();
+  const unsigned ep = *cnst(a.epoch);
+  const int L = cnst(a.pos)[0] + 1;  // context including this step's token
+  const int G = gridDim.x, w = blockIdx.x;
+  const int nA = a.qkv_n / 16, nB = a.heads * kGpt2Splits, nC = a.H / 16, nD = a.inter / 16;
+  const int bi = w - (G - nB);  // this workgroup's attention item (when >= 0)
+  const bool hasD = w >= nC && w < nC + nD;
+  AttnKV kv;
+  u32x4 wa[kLH];
+  if (w < nA) load_weights<kLH>(wa, layer_p(a, 0).wqkv, a.H, w);
+  if (bi >= 0) attn_prefetch(a, layer_p(a, 0), bi, L, kv);
+  for (int l = 0; l < a.n_layers; l++) {
+    const LayerP P = layer_p(a, l);
+    const bool next = l + 1 < a.n_layers;
+    if (w < nA && !qkv_item<kLH>(a, P, l, w, ep, S, wa)) return;
+    if (bi >= 0) {
+      if (!attn_item(a, P, l, bi, ep, L, S, kv)) return;
+      if (next && !hasD) attn_prefetch(a, layer_p(a, l + 1), bi, L, kv);
+    }
+    if (w < nC && !o_item<kLH>(a, P, l, w, ep, L, S)) return;
+    if (hasD) {
+      if (!fc_item<kLH>(a, P, l, w - nC, ep, S)) return;
+      if (next) {
+        if (bi >= 0) attn_prefetch(a, layer_p(a, l + 1), bi, L, kv);
+        if (w < nA) load_weights<kLH>(wa, layer_p(a, l + 1).wqkv, a.H, w);
+      }
+    }
+    if (w < nC) {
+      if (!proj_item<kLH, kLI>(a, P, l, w, ep, S)) return;
+      if (next && w < nA) load_weights<kLH>(wa, layer_p(a, l + 1).wqkv, a.H, w);
+    }
+    if (next && w < nA && w >= nC + nD) load_weights<kLH>(wa, layer_p(a, l + 1).wqkv, a.H, w);
+  }
+}
+
+// (loads per lane for K = hidden, K = intermediate) per supported shape
+#define SH_GPT2_SHAPES(X) \
+  X(6, 24) /* GPT-2 small: hidden 768, intermediate 3072 */ \
+  X(2, 4)  /* hidden 256, intermediate 512 */
+
+const void *gpt2_kernel_for(int H, int inter) {
+#define SH_MATCH(LH, LI) \
+  if (H == LH * 128 && inter == LI * 128) return reinterpret_cast<const void *>(&gpt2_layers_kernel<LH, LI>);
+  SH_GPT2_SHAPES(SH_MATCH)
+#undef SH_MATCH
+  return nullptr;
+}
+
+}  // namespace
+
+bool gpt2_layers_supported(int layers, int H, int heads, int head_dim, int inter, int max_pos,
+                           int grid) {
+  if (layers < 1 || layers > kMaxDecodeLayers || head_dim != kHd || heads * kHd != H) return false;
+  if (!gpt2_kernel_for(H, inter)) return false;
+  if (max_pos < 1 || gpt2_layers_chunk(max_pos) > kMaxChunk) return false;
+  // at most one item per workgroup and phase; the attention items on the
+  // last workgroups
+  const int nA = 3 * H / 16, nB = heads * kGpt2Splits, nC = H / 16, nD = inter / 16;
+  return nA <= grid && nB <= grid && nC + nD <= grid;
+}
+
+int gpt2_layers_chunk(int max_pos) {
+  return ((max_pos + kGpt2Splits - 1) / kGpt2Splits + 15) / 16 * 16;
+}
+
+size_t gpt2_layers_partial_cells(int heads) { return (size_t)heads * kGpt2Splits * kGpt2PStride; }
+
+hipError_t gpt2_layers_occupancy(const Gpt2Args &a, int *blocks_per_cu) {
+  const void *k = gpt2_kernel_for(a.H, a.inter);
+  if (!k) return hipErrorInvalidValue;
+  return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, k, kT, 0);
+}
+
+hipError_t launch_gpt2_layers(hipStream_t s, const Gpt2Args &a, int grid) {
+  const void *k = gpt2_kernel_for(a.H, a.inter);
+  if (!k) return hipErrorInvalidValue;
+  void *args[] = {const_cast<Gpt2Args *>(&a)};
+  return hipLaunchKernel(k, dim3(grid), dim3(kT), args, 0, s);
+}
+
+}  // namespace sh

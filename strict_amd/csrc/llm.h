@@ -160,6 +160,43 @@ hipError_t decode_layers_trace(void *dst, size_t bytes);
 hipError_t launch_decode_layers(hipStream_t s, const LayersArgs &a, int grid, size_t lds,
                                 bool cooperative);
 
+// ---- persistent GPT-2 layers kernel (fp16 weights, head_dim 64, batch 1) ----
+
+// Device pointers of one GPT-2 layer, read by the kernel from a device array.
+struct Gpt2LayerPtrs {
+  const uint16_t *wqkv, *wo, *wfc, *wproj;  // fp16 tiled
+  const float *bqkv, *bo, *bfc, *bproj;     // biases
+  const float *ln1_g, *ln1_b, *ln2_g, *ln2_b;
+  uint16_t *kcache, *vcache;                // [max_batch][heads][max_pos][64] fp16 (row 0)
+};
+constexpr int kGpt2Splits = 4;    // attention splits per head
+constexpr int kGpt2PStride = 68;  // cells per attention partial: acc[64], max, sum, pad
+// Cell buffers (exchange.h): x0c [H] layer output, x1c [H] x_mid, qkvc [3 H],
+// partc [heads][4][68] attention partials, actc [inter / 2] GELU output (two
+// fp16 per cell).
+struct Gpt2Args {
+  const Gpt2LayerPtrs *layers = nullptr;  // [n_layers]
+  int n_layers = 0, H = 0, heads = 0, inter = 0, qkv_n = 0, max_pos = 0;
+  int chunk = 16;                    // positions per attention split
+  float eps = 1e-5f, scale = 0.125f;  // LayerNorm epsilon, attention 1 / sqrt(64)
+  const int *pos = nullptr;          // [1] this step's position (embed kernel)
+  const unsigned *epoch = nullptr;   // this step's number (embed kernel)
+  float *x_in = nullptr;             // [H] first layer's input, last layer's output
+  uint64_t *x0c = nullptr, *x1c = nullptr, *qkvc = nullptr, *partc = nullptr, *actc = nullptr;
+  unsigned *err = nullptr;           // set when a wait timed out (sticky)
+  unsigned long long spin_ticks = 0;  // wall-clock ticks a wait may take
+};
+// Shapes the kernel is built for (GPT-2 small and a reduced test shape),
+// max_pos <= 1024, and a grid of `grid` workgroups holding every phase's items.
+bool gpt2_layers_supported(int layers, int H, int heads, int head_dim, int inter, int max_pos,
+                           int grid);
+int gpt2_layers_chunk(int max_pos);
+size_t gpt2_layers_partial_cells(int heads);
+hipError_t gpt2_layers_occupancy(const Gpt2Args &a, int *blocks_per_cu);
+// Ordinary launch on stream s; needs its `grid` workgroups resident together
+// (one per CU), as the Qwen3 decode-layers kernel.
+hipError_t launch_gpt2_layers(hipStream_t s, const Gpt2Args &a, int grid);
+
 // Lets every GEMV instantiation use up to 160 KiB of dynamic LDS (current device).
 hipError_t prepare_gemv_kernels();
 hipError_t launch_gemv(hipStream_t s, const GemvArgs &a, int weight_type, int pro, int epi,

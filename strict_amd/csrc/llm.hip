@@ -92,6 +92,11 @@ struct sh_llm {
   int layers_grid = 0;
   size_t layers_lds = 0;
   unsigned *epoch = nullptr;
+  // persistent GPT-2 layers kernel (batch 1; other batches keep the per-op
+  // kernels, which share its cache layout)
+  bool gpt2_kernel = false;
+  Gpt2Args ga{};
+  int gpt2_grid = 0;
 };
 
 namespace {
@@ -179,16 +184,18 @@ int enqueue_step(sh_llm *m, bool logits) {
   e.inv_freq = m->inv_freq;
   e.rope = m->rope;
   e.half = d / 2;
-  float *x_final = m->x;  // the decode-layers kernel reads and writes m->x too
-  if (m->layers_kernel) e.epoch = m->epoch;
+  float *x_final = m->x;  // the layers kernels read and write m->x too
+  const bool gpt2_layers = m->gpt2_kernel && B == 1;
+  if (m->layers_kernel || gpt2_layers) e.epoch = m->epoch;
   SH_HIP_TRY(launch_embed(s, e, B));
 
   if (m->layers_kernel) {
     m->la.head_on = logits && m->head_in_layers ? 1 : 0;
     SH_HIP_TRY(launch_decode_layers(s, m->la, m->layers_grid, m->layers_lds, m->coop_layers));
   }
+  if (gpt2_layers) SH_HIP_TRY(launch_gpt2_layers(s, m->ga, m->gpt2_grid));
   for (Layer &L : m->layers) {
-    if (m->layers_kernel) break;  // every layer ran in the kernel above
+    if (m->layers_kernel || gpt2_layers) break;  // every layer ran in the kernel above
     GemvArgs g;
     g.w = L.qkv.w;
     g.scale = L.qkv.scale;
@@ -385,6 +392,66 @@ int setup_layers_kernel(sh_llm *m) {
   return SH_OK;
 }
 
+// Sets up the persistent GPT-2 layers kernel (batch 1) when the model's
+// shape and the device allow it; otherwise the per-op kernels stay in use.
+int setup_gpt2_kernel(sh_llm *m) {
+  const sh_llm_config &c = m->cfg;
+  const char *env = getenv("STRICT_HIP_LLM_LAYERS");
+  if (env && env[0] == '0') return SH_OK;
+  const int dev = device_of(m->ctx);
+  int cus = 0, clock_khz = 0;
+  SH_HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  SH_HIP_TRY(hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeWallClockRate, dev));
+  if (m->qwen || cus <= 0 || clock_khz <= 0 ||
+      !gpt2_layers_supported(c.layers, c.hidden, c.heads, c.head_dim, c.intermediate,
+                             c.max_positions, cus) ||
+      c.kv_heads != c.heads)
+    return SH_OK;
+  Gpt2Args &a = m->ga;
+  a.n_layers = c.layers;
+  a.H = c.hidden;
+  a.heads = c.heads;
+  a.inter = c.intermediate;
+  a.qkv_n = m->qkv_n;
+  a.max_pos = c.max_positions;
+  a.chunk = gpt2_layers_chunk(c.max_positions);
+  a.eps = c.norm_eps;
+  a.scale = 1.0f / std::sqrt((float)c.head_dim);
+  a.pos = m->pos;
+  a.spin_ticks = (unsigned long long)clock_khz * 50;  // 50 ms per wait
+  int per_cu = 0;
+  SH_HIP_TRY(gpt2_layers_occupancy(a, &per_cu));
+  if (per_cu < 1) return SH_OK;
+  int rc;
+  if ((rc = alloc_n(m, (size_t)c.hidden, &a.x0c)) || (rc = alloc_n(m, (size_t)c.hidden, &a.x1c)) ||
+      (rc = alloc_n(m, (size_t)m->qkv_n, &a.qkvc)) ||
+      (rc = alloc_n(m, gpt2_layers_partial_cells(c.heads), &a.partc)) ||
+      (rc = alloc_n(m, (size_t)c.intermediate / 2, &a.actc)) || (rc = alloc_n(m, 64, &a.err)) ||
+      (!m->epoch && (rc = alloc_n(m, 64, &m->epoch))))
+    return rc;
+  a.x_in = m->x;
+  a.epoch = m->epoch;
+  Gpt2LayerPtrs *dl = nullptr;
+  if ((rc = alloc_n(m, (size_t)c.layers, &dl))) return rc;
+  std::vector<Gpt2LayerPtrs> hl(c.layers);
+  for (int i = 0; i < c.layers; i++) {
+    const Layer &L = m->layers[i];
+    hl[i] = Gpt2LayerPtrs{reinterpret_cast<const uint16_t *>(L.qkv.w),
+                          reinterpret_cast<const uint16_t *>(L.o.w),
+                          reinterpret_cast<const uint16_t *>(L.up.w),
+                          reinterpret_cast<const uint16_t *>(L.down.w),
+                          L.qkv.bias, L.o.bias, L.up.bias, L.down.bias,
+                          L.norm1_g, L.norm1_b, L.norm2_g, L.norm2_b, L.kcache, L.vcache};
+  }
+  SH_HIP_TRY(hipMemcpyAsync(dl, hl.data(), hl.size() * sizeof(Gpt2LayerPtrs),
+                            hipMemcpyHostToDevice, stream_of(m->ctx)));
+  SH_HIP_TRY(hipStreamSynchronize(stream_of(m->ctx)));
+  a.layers = dl;
+  m->gpt2_grid = cus;
+  m->gpt2_kernel = true;
+  return SH_OK;
+}
+
 void drop_graphs(sh_llm *m) {
   for (int i = 0; i < 2; i++) {
     if (m->graph[i]) (void)hipGraphExecDestroy(m->graph[i]);
@@ -573,6 +640,7 @@ SH_API int sh_llm_create(sh_ctx *ctx, const sh_llm_config *config, sh_llm **out)
   if (e == hipSuccess) e = hipStreamSynchronize(stream_of(ctx));
   if (e != hipSuccess) return cleanup(hip_fail(e, "preparing the model"));
   if ((rc = setup_layers_kernel(m)) != SH_OK) return cleanup(rc);
+  if ((rc = setup_gpt2_kernel(m)) != SH_OK) return cleanup(rc);
   *out = m;
   return SH_OK;
 }
@@ -690,7 +758,8 @@ SH_API int sh_llm_tensor(sh_llm *m, const char *name, int layer, void **ptr, siz
   if (n == "wpe") return set(m->wpe, (size_t)c.max_positions * c.hidden * 2);
   if (n == "inv_freq") return set(m->inv_freq, (size_t)c.head_dim / 2 * 4);
   // present only when the decode-layers kernel runs the layers
-  if (n == "layers.err") return set(m->layers_kernel ? m->la.err : nullptr, 4);
+  if (n == "layers.err")
+    return set(m->layers_kernel ? m->la.err : m->gpt2_kernel ? m->ga.err : nullptr, 4);
   if (layer < 0 || layer >= c.layers)
     return fail(SH_ERR_NOT_FOUND, "tensor '%s' layer %d not found", name, layer);
   Layer &L = m->layers[layer];
@@ -737,6 +806,7 @@ SH_API int sh_llm_reset(sh_llm *m, int batch) {
     m->layers_lds = decode_layers_lds(batch, c.hidden, c.heads, c.intermediate, &a.lds_misc);
     SH_HIP_TRY(hipMemsetAsync(a.err, 0, 4, s));
   }
+  if (m->gpt2_kernel) SH_HIP_TRY(hipMemsetAsync(m->ga.err, 0, 4, s));
   return SH_OK;
 }
 
@@ -760,7 +830,7 @@ SH_API int sh_llm_step(sh_llm *m, const int32_t *tokens, int want_logits) {
     SH_HIP_TRY(hipStreamSynchronize(s));  // `keys` is a stack array
   }
   const int g = want_logits ? 1 : 0;
-  if (!m->use_graphs || m->layers_kernel) {
+  if (!m->use_graphs || m->layers_kernel || (m->gpt2_kernel && m->batch == 1)) {
     if ((rc = enqueue_step(m, want_logits != 0)) != SH_OK) return rc;
   } else if (m->graph_batch[g] != m->batch) {
     if (m->graph[g]) (void)hipGraphExecDestroy(m->graph[g]);
@@ -798,6 +868,8 @@ SH_API int sh_llm_next_tokens(sh_llm *m, int32_t *tokens) {
   unsigned err = 0;
   if (m->layers_kernel)
     SH_HIP_TRY(hipMemcpyAsync(&err, m->la.err, 4, hipMemcpyDeviceToHost, s));
+  else if (m->gpt2_kernel && m->batch == 1)
+    SH_HIP_TRY(hipMemcpyAsync(&err, m->ga.err, 4, hipMemcpyDeviceToHost, s));
   SH_HIP_TRY(hipStreamSynchronize(s));
   if (err)
     return fail(SH_ERR_HIP, "decode-layers kernel: a wait between workgroups timed out (step state lost; reset the model)");

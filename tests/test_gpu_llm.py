@@ -232,13 +232,15 @@ def test_per_op_path_without_graphs(ctx, monkeypatch, cfg):
     assert np.array_equal(runs[0][1], runs[1][1])
 
 
-def test_decode_layers_wait_failure_reported_and_reset_recovers(ctx):
-    # The bounded waits of the decode-layers kernel: the host sets the sticky
-    # error word before a step, so every wait between workgroups gives up
-    # after a few polls and the kernel ends normally; sh_llm_next_tokens
-    # reports the failed step, and sh_llm_reset clears the error.
-    prompt = np.random.default_rng(5).integers(0, QWEN_SMALL.vocab, 12)
-    with llm.Model(ctx, QWEN_SMALL) as m:
+@pytest.mark.parametrize("cfg", [QWEN_SMALL, GPT2_SMALL_TEST], ids=["qwen3", "gpt2"])
+def test_decode_layers_wait_failure_reported_and_reset_recovers(ctx, cfg):
+    # The bounded waits of the persistent layers kernels (Qwen3's decode-layers
+    # kernel, GPT-2's layers kernel): the host sets the sticky error word
+    # before a step, so every wait between workgroups gives up after a few
+    # polls and the kernel ends normally; sh_llm_next_tokens reports the
+    # failed step, and sh_llm_reset clears the error.
+    prompt = np.random.default_rng(5).integers(0, cfg.vocab, 12)
+    with llm.Model(ctx, cfg) as m:
         assert m.uses_layers_kernel
         m.init_random(seed=7, stddev=0.02)
         m.reset(1)
@@ -260,6 +262,7 @@ def test_decode_layers_wait_failure_reported_and_reset_recovers(ctx):
 
 def test_gpt2_small_shape_greedy_256(ctx):
     with llm.Model(ctx, GPT2_SMALL_TEST) as m:
+        assert m.uses_layers_kernel  # the persistent GPT-2 layers kernel at batch 1
         m.init_random(seed=8, stddev=0.02)
         _randomize_small_params(m, 2)
         prompt = np.random.default_rng(4).integers(0, GPT2_SMALL_TEST.vocab, 16)
@@ -271,6 +274,7 @@ def test_gpt2_config3_greedy_256(ctx):
     # 128-token prompt of seeded uniform ids, 256 greedy steps with KV cache
     cfg = llm.GPT2_SMALL
     with llm.Model(ctx, cfg) as m:
+        assert m.uses_layers_kernel
         m.init_random(seed=42, stddev=0.02)
         prompt = np.random.default_rng(42).integers(0, cfg.vocab, 128)
         _greedy_check(m, prompt, 256, "gpt2-config3")
