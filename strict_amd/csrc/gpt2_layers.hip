@@ -12,8 +12,9 @@
 //                                                head, x_mid = x + W_o attn + b)
 //   D  fc    one 16-row tile of W_fc each       (LayerNorm of x_mid, GELU)
 //   E  proj  one 16-row tile of W_proj each     (x = x_mid + W_proj act + b)
-// The final LayerNorm and the LM head run after the launch (the per-op
-// kernels), reading the last layer's x from the plain buffer x_in.
+// and, on steps with logits, after the last layer:
+//   H  head  16-row tiles of the LM head          (final LayerNorm, logits,
+//                                                  greedy argmax)
 //
 // Items: A on workgroups 0.., C and E on 0.., D after the C range, B on the
 // last workgroups; at most one item per workgroup and phase. Exchange:
@@ -481,6 +482,65 @@ __device__ __forceinline__ bool proj_item(const Gpt2Args &a, const LayerP &P, in
   return true;
 }
 
+// H (steps with logits): the final LayerNorm of x, then the LM head. Wave v
+// of workgroup w owns the 16-row tiles j = w + G v, w + G v + 4 G, ..; a
+// tile's 16 KiB x (H / 32) of weights stream through 4 H / 128 loads per
+// lane, the next tile's requested while the current one is multiplied. The
+// logits are written, and each wave folds its argmax keys into its slot.
+template <int kLH>
+__device__ __forceinline__ void head_load(u32x4 (&w)[4 * kLH], const Gpt2Args &a, int j) {
+  const int lane = threadIdx.x & 63, jj = min(j, a.head_tiles - 1);  // past the end: unused
+  const SH_XGLOBAL uint8_t *W = reinterpret_cast<const SH_XGLOBAL uint8_t *>(gbl(a.head_w));
+#pragma unroll
+  for (int u = 0; u < 4 * kLH; u++)
+    w[u] = __builtin_nontemporal_load(reinterpret_cast<const SH_XGLOBAL u32x4 *>(
+        W + ((size_t)jj * 4 * kLH + u) * 1024 + (size_t)lane * 16));
+}
+
+template <int kLH>
+__device__ __forceinline__ bool head_phase(const Gpt2Args &a, unsigned ep, Lds &S,
+                                           u32x4 (&wb)[2][4 * kLH]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, G = gridDim.x, w = blockIdx.x;
+  const int first = w + G * wave, step = 4 * G, nT = a.head_tiles;
+  if (!stage_ln<(kLH * 128 + 1023) / 1024>(a, a.x0c, nullptr, tag_of(ep, a.n_layers - 1),
+                                            gbl(a.final_g), gbl(a.final_b), a.H, S))
+    return false;
+  const _Float16 *xrow = S.xs + 8 * (lane >> 4);
+  unsigned long long best = 0;
+  auto tile = [&](const u32x4 (&wt)[4 * kLH], int j) {
+    f32x4 part[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) part[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 4 * kLH; u++)
+      part[u % 4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+          *reinterpret_cast<const f16x8 *>(xrow + u * 32), __builtin_bit_cast(f16x8, wt[u]), part[u % 4], 0, 0, 0);
+    const f32x4 acc = (part[0] + part[1]) + (part[2] + part[3]);
+    const int n = j * 16 + (lane & 15);
+    if (lane < 16 && n < a.n_valid) {
+      gbl(a.logits)[n] = acc[0];
+      const unsigned long long key = argmax_key(acc[0], n);
+      best = key > best ? key : best;
+    }
+  };
+  for (int j = first; j < nT; j += 2 * step) {
+    head_load<kLH>(wb[1], a, j + step);
+    tile(wb[0], j);
+    head_load<kLH>(wb[0], a, j + 2 * step);
+    if (j + step < nT) tile(wb[1], j + step);
+  }
+#pragma unroll
+  for (int off = 8; off >= 1; off >>= 1) {
+    const unsigned long long o = __shfl_xor(best, off, 64);
+    best = o > best ? o : best;
+  }
+  unsigned long long *slot = a.keys + ((w * 4 + wave) % kKeySlots) * kKeyStride;
+  if (lane == 0 && best != 0 &&
+      best > __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+    atomicMax(slot, best);
+  return true;
+}
+
 template <int kLH, int kLI>
 __global__ __launch_bounds__(kT, 1) void gpt2_layers_kernel(const Gpt2Args a) {
   __shared__ Lds S;
@@ -517,6 +577,11 @@ __global__ __launch_bounds__(kT, 1) void gpt2_layers_kernel(const Gpt2Args a) {
       if (next && w < nA) load_weights<kLH>(wa, layer_p(a, l + 1).wqkv, a.H, w);
     }
     if (next && w < nA && w >= nC + nD) load_weights<kLH>(wa, layer_p(a, l + 1).wqkv, a.H, w);
+  }
+  if (a.head_on) {
+    u32x4 wb[2][4 * kLH];
+    head_load<kLH>(wb[0], a, w + G * (threadIdx.x >> 6));  // before the final norm's wait
+    head_phase<kLH>(a, ep, S, wb);
   }
 }
 

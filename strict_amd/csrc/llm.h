@@ -185,6 +185,13 @@ struct Gpt2Args {
   uint64_t *x0c = nullptr, *x1c = nullptr, *qkvc = nullptr, *partc = nullptr, *actc = nullptr;
   unsigned *err = nullptr;           // set when a wait timed out (sticky)
   unsigned long long spin_ticks = 0;  // wall-clock ticks a wait may take
+  // final LayerNorm + LM head inside the kernel (steps with logits)
+  int head_on = 0;
+  const uint16_t *head_w = nullptr;  // fp16 tiled [head_tiles * 16][H] (tied embedding)
+  const float *final_g = nullptr, *final_b = nullptr;
+  int head_tiles = 0, n_valid = 0;   // 16-row tiles; columns that are real tokens
+  float *logits = nullptr;           // [logits_ld]
+  unsigned long long *keys = nullptr;  // [kKeySlots][kKeyStride] greedy argmax keys
 };
 // Shapes the kernel is built for (GPT-2 small and a reduced test shape),
 // max_pos <= 1024, and a grid of `grid` workgroups holding every phase's items.

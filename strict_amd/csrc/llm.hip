@@ -193,7 +193,10 @@ int enqueue_step(sh_llm *m, bool logits) {
     m->la.head_on = logits && m->head_in_layers ? 1 : 0;
     SH_HIP_TRY(launch_decode_layers(s, m->la, m->layers_grid, m->layers_lds, m->coop_layers));
   }
-  if (gpt2_layers) SH_HIP_TRY(launch_gpt2_layers(s, m->ga, m->gpt2_grid));
+  if (gpt2_layers) {
+    m->ga.head_on = logits ? 1 : 0;
+    SH_HIP_TRY(launch_gpt2_layers(s, m->ga, m->gpt2_grid));
+  }
   for (Layer &L : m->layers) {
     if (m->layers_kernel || gpt2_layers) break;  // every layer ran in the kernel above
     GemvArgs g;
@@ -277,7 +280,7 @@ int enqueue_step(sh_llm *m, bool logits) {
     SH_HIP_TRY(launch_gemv(s, dn, m->wtype, kProNone, kEpiResidual, 0));
   }
 
-  if (logits && !(m->layers_kernel && m->head_in_layers)) {
+  if (logits && !(m->layers_kernel && m->head_in_layers) && !gpt2_layers) {
     GemvArgs nrm;
     nrm.x = x_final;
     nrm.x_ld = H;
@@ -447,6 +450,13 @@ int setup_gpt2_kernel(sh_llm *m) {
                             hipMemcpyHostToDevice, stream_of(m->ctx)));
   SH_HIP_TRY(hipStreamSynchronize(stream_of(m->ctx)));
   a.layers = dl;
+  a.head_w = reinterpret_cast<const uint16_t *>(m->head.w);
+  a.final_g = m->final_g;
+  a.final_b = m->final_b;
+  a.head_tiles = m->head.N / 16;
+  a.n_valid = c.vocab;
+  a.logits = m->logits;
+  a.keys = m->keys;
   m->gpt2_grid = cus;
   m->gpt2_kernel = true;
   return SH_OK;
