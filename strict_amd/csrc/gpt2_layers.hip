@@ -366,21 +366,23 @@ __device__ __forceinline__ bool attn_item(const Gpt2Args &a, const LayerP &P, in
 }
 
 // The attention output of every head (the splits merged, fp16) -> xs:
-// thread t computes values t + 256 j, j < kC, of the H = heads * 64.
-template <int kC>
-__device__ __forceinline__ bool stage_attn(const Gpt2Args &a, unsigned tag, int L, Lds &S) {
-  const int t = threadIdx.x, ns = (L + a.chunk - 1) / a.chunk;
-  constexpr int kN = kC * kGpt2Splits * 3;
+// thread t computes values t + 256 j, j < kC, of the H = heads * 64, over
+// the first kNS splits (the active ones, ns <= kNS; the polls load only
+// those: every poll of a wait reloads all of its cells).
+template <int kC, int kNS>
+__device__ __forceinline__ bool stage_attn_n(const Gpt2Args &a, unsigned tag, int ns, Lds &S) {
+  const int t = threadIdx.x;
+  constexpr int kN = kC * kNS * 3;
   uint64_t cv[kN];
   uint64_t mask = 0;
 #pragma unroll
   for (int j = 0; j < kC; j++)
 #pragma unroll
-    for (int s = 0; s < kGpt2Splits; s++)
-      if (s < ns && t + kT * j < a.H) mask |= 7ull << ((j * kGpt2Splits + s) * 3);
+    for (int s = 0; s < kNS; s++)
+      if (s < ns && t + kT * j < a.H) mask |= 7ull << ((j * kNS + s) * 3);
   const bool ok = spin_cells(a, a.partc,
                              [&](int k) {
-                               const int j = k / (kGpt2Splits * 3), s = (k / 3) % kGpt2Splits, f = k % 3;
+                               const int j = k / (kNS * 3), s = (k / 3) % kNS, f = k % 3;
                                const int idx = min(t + kT * j, a.H - 1), h = idx >> 6, d = idx & 63;
                                const size_t pp = ((size_t)h * kGpt2Splits + min(s, ns - 1)) * kGpt2PStride;
                                return pp + (f == 0 ? d : kHd + f - 1);
@@ -393,13 +395,13 @@ __device__ __forceinline__ bool stage_attn(const Gpt2Args &a, unsigned tag, int 
     if (idx >= a.H) continue;
     float M = -INFINITY;
 #pragma unroll
-    for (int s = 0; s < kGpt2Splits; s++)
-      if (s < ns) M = fmaxf(M, cell_f32(cv[(j * kGpt2Splits + s) * 3 + 1]));
+    for (int s = 0; s < kNS; s++)
+      if (s < ns) M = fmaxf(M, cell_f32(cv[(j * kNS + s) * 3 + 1]));
     float num = 0.0f, den = 0.0f;
 #pragma unroll
-    for (int s = 0; s < kGpt2Splits; s++)
+    for (int s = 0; s < kNS; s++)
       if (s < ns) {
-        const int k = (j * kGpt2Splits + s) * 3;
+        const int k = (j * kNS + s) * 3;
         const float f = expf(cell_f32(cv[k + 1]) - M);
         num += f * cell_f32(cv[k]);
         den += f * cell_f32(cv[k + 2]);
@@ -408,6 +410,14 @@ __device__ __forceinline__ bool stage_attn(const Gpt2Args &a, unsigned tag, int 
   }
   lds_barrier();
   return true;
+}
+
+template <int kC>
+__device__ __forceinline__ bool stage_attn(const Gpt2Args &a, unsigned tag, int L, Lds &S) {
+  const int ns = (L + a.chunk - 1) / a.chunk;  // uniform
+  if (ns == 1) return stage_attn_n<kC, 1>(a, tag, ns, S);
+  if (ns == 2) return stage_attn_n<kC, 2>(a, tag, ns, S);
+  return stage_attn_n<kC, kGpt2Splits>(a, tag, ns, S);
 }
 
 // C: x_mid[16 i + c] = x[.] + W_o attn + b
