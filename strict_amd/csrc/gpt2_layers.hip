@@ -47,6 +47,21 @@ constexpr int kVJ = kMaxChunk / 32;  // V rows per thread
 
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
+#ifdef SH_GPT2_TRACE
+// Diagnostic builds only (-DSH_GPT2_TRACE): wall-clock marks per workgroup
+// and layer: slots 0..4 the ends of its A..E items, 5..9 the ends of their
+// waits, 10 the kernel's start (layer 0), 11 the head's end (layer 0).
+constexpr int kTrWgs = 256, kTrLayers = 16, kTrSlots = 12;
+__device__ unsigned long long g_gpt2_trace[kTrWgs][kTrLayers][kTrSlots];
+#define SH_G2MARK(l, slot)                                                              \
+  do {                                                                                   \
+    if (threadIdx.x == 0 && blockIdx.x < kTrWgs && (l) < kTrLayers)                     \
+      g_gpt2_trace[blockIdx.x][l][slot] = wall_clock64();                               \
+  } while (0)
+#else
+#define SH_G2MARK(l, slot) ((void)0)
+#endif
+
 struct LayerP {
   const SH_XGLOBAL uint16_t *wqkv, *wo, *wfc, *wproj;
   const SH_XGLOBAL float *bqkv, *bo, *bfc, *bproj;
@@ -232,8 +247,10 @@ __device__ __forceinline__ bool qkv_item(const Gpt2Args &a, const LayerP &P, int
   if (!stage_ln<(kLH * 128 + 1023) / 1024>(a, a.x0c, l == 0 ? a.x_in : nullptr, tag_of(ep, l - 1),
                                             P.ln1_g, P.ln1_b, a.H, S))
     return false;
+  SH_G2MARK(l, 5);
   f32x4 acc = reduce_waves(mfma_weights<kLH>(w, S.xs), S);
   if (threadIdx.x < 16) cst(a.qkvc, (size_t)i * 16 + col, bits_of(acc[0] + bias), tag_of(ep, l));
+  SH_G2MARK(l, 0);
   return true;
 }
 
@@ -290,6 +307,7 @@ __device__ __forceinline__ bool attn_item(const Gpt2Args &a, const LayerP &P, in
     uint64_t cv[1];
     const bool ok = spin_cells(a, a.qkvc, [&](int) { return cell; }, t < 192 ? 1ull : 0ull, tag, cv);
     if (!waits_ok(a, ok, &S.votes)) return false;
+    SH_G2MARK(l, 6);
     const float v = cell_f32(cv[0]);
     if (t < 64) {
       S.q[d] = v * a.scale;
@@ -362,6 +380,7 @@ __device__ __forceinline__ bool attn_item(const Gpt2Args &a, const LayerP &P, in
   } else if (t == kHd + 1) {
     cst(a.partc, pp + kHd + 1, bits_of(lsum), tag);
   }
+  SH_G2MARK(l, 1);
   return true;
 }
 
@@ -433,6 +452,7 @@ __device__ __forceinline__ bool o_item(const Gpt2Args &a, const LayerP &P, int l
   const float x0 = l == 0 ? gbl(a.x_in)[cell] : 0.0f;
   __builtin_amdgcn_sched_barrier(0);
   if (!stage_attn<(kLH * 128 + 255) / 256>(a, tag_of(ep, l), L, S)) return false;
+  SH_G2MARK(l, 7);
   const f32x4 acc = reduce_waves(mfma_weights<kLH>(w, S.xs), S);
   if (threadIdx.x < 16) {
     float x = x0;
@@ -443,6 +463,7 @@ __device__ __forceinline__ bool o_item(const Gpt2Args &a, const LayerP &P, int l
     cst(a.x1c, cell, bits_of(x + (acc[0] + bias)), tag_of(ep, l));
   }
   asm volatile("" ::"v"(rc));  // the residual load retires here in every thread
+  SH_G2MARK(l, 2);
   return true;
 }
 
@@ -457,6 +478,7 @@ __device__ __forceinline__ bool fc_item(const Gpt2Args &a, const LayerP &P, int 
   __builtin_amdgcn_sched_barrier(0);
   if (!stage_ln<(kLH * 128 + 1023) / 1024>(a, a.x1c, nullptr, tag_of(ep, l), P.ln2_g, P.ln2_b, a.H, S))
     return false;
+  SH_G2MARK(l, 8);
   const f32x4 acc = reduce_waves(mfma_weights<kLH>(w, S.xs), S);
   if (threadIdx.x < 64) {
     const uint32_t hv = f32_to_f16_bits(gelu_tanh(acc[0] + bias));
@@ -464,6 +486,7 @@ __device__ __forceinline__ bool fc_item(const Gpt2Args &a, const LayerP &P, int 
     if (threadIdx.x < 16 && (col & 1) == 0)
       cst(a.actc, ((size_t)i * 16 + col) / 2, hv | (nb << 16), tag_of(ep, l));
   }
+  SH_G2MARK(l, 3);
   return true;
 }
 
@@ -481,6 +504,7 @@ __device__ __forceinline__ bool proj_item(const Gpt2Args &a, const LayerP &P, in
   uint64_t rc = cld(a.x1c, cell);
   __builtin_amdgcn_sched_barrier(0);
   if (!stage_f16<(kLI * 128 + 1023) / 1024>(a, a.actc, tag, a.inter, S)) return false;
+  SH_G2MARK(l, 9);
   const f32x4 acc = reduce_waves(mfma_weights<kLI>(w, S.xs), S);
   if (threadIdx.x < 16) {
     if (!finish_cell(a, a.x1c, cell, tag, rc)) atomicOr(a.err, 1u);
@@ -489,6 +513,7 @@ __device__ __forceinline__ bool proj_item(const Gpt2Args &a, const LayerP &P, in
     cst(a.x0c, cell, bits_of(v), tag);
   }
   asm volatile("" ::"v"(rc));
+  SH_G2MARK(l, 4);
   return true;
 }
 
@@ -556,6 +581,7 @@ __global__ __launch_bounds__(kT, 1) void gpt2_layers_kernel(const Gpt2Args a) {
   __shared__ Lds S;
   if (threadIdx.x < 4) S.votes.par[threadIdx.x] = 0;
   lds_barrier();
+  SH_G2MARK(0, 10);
   const unsigned ep = *cnst(a.epoch);
   const int L = cnst(a.pos)[0] + 1;  // context including this step's token
   const int G = gridDim.x, w = blockIdx.x;
@@ -592,6 +618,7 @@ __global__ __launch_bounds__(kT, 1) void gpt2_layers_kernel(const Gpt2Args a) {
     u32x4 wb[2][4 * kLH];
     head_load<kLH>(wb[0], a, w + G * (threadIdx.x >> 6));  // before the final norm's wait
     head_phase<kLH>(a, ep, S, wb);
+    SH_G2MARK(0, 11);
   }
 }
 
@@ -632,6 +659,13 @@ hipError_t gpt2_layers_occupancy(const Gpt2Args &a, int *blocks_per_cu) {
   if (!k) return hipErrorInvalidValue;
   return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, k, kT, 0);
 }
+
+#ifdef SH_GPT2_TRACE
+hipError_t gpt2_layers_trace(void *dst, size_t bytes) {
+  if (bytes > sizeof(g_gpt2_trace)) bytes = sizeof(g_gpt2_trace);
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_gpt2_trace), bytes, 0, hipMemcpyDeviceToHost);
+}
+#endif
 
 hipError_t launch_gpt2_layers(hipStream_t s, const Gpt2Args &a, int grid) {
   const void *k = gpt2_kernel_for(a.H, a.inter);

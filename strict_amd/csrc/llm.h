@@ -203,6 +203,10 @@ hipError_t gpt2_layers_occupancy(const Gpt2Args &a, int *blocks_per_cu);
 // Ordinary launch on stream s; needs its `grid` workgroups resident together
 // (one per CU), as the Qwen3 decode-layers kernel.
 hipError_t launch_gpt2_layers(hipStream_t s, const Gpt2Args &a, int grid);
+#ifdef SH_GPT2_TRACE
+// Diagnostic builds: the last step's marks, [256][16][12] wall-clock ticks.
+hipError_t gpt2_layers_trace(void *dst, size_t bytes);
+#endif
 
 // Lets every GEMV instantiation use up to 160 KiB of dynamic LDS (current device).
 hipError_t prepare_gemv_kernels();

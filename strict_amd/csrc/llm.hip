@@ -655,6 +655,15 @@ SH_API int sh_llm_create(sh_ctx *ctx, const sh_llm_config *config, sh_llm **out)
   return SH_OK;
 }
 
+#ifdef SH_GPT2_TRACE
+// Diagnostic builds only (-DSH_GPT2_TRACE): the GPT-2 layers kernel's marks
+// of the last step, [256][16][12] wall-clock ticks.
+SH_API int sh_debug_gpt2_trace(void *dst, size_t bytes) {
+  SH_HIP_TRY(gpt2_layers_trace(dst, bytes));
+  return SH_OK;
+}
+#endif
+
 #ifdef SH_DECODE_TRACE
 // Diagnostic builds only (-DSH_DECODE_TRACE): the decode-layers kernel's
 // per-workgroup phase timeline of the last step, [256][32][16] wall-clock ticks.
