@@ -31,6 +31,49 @@
 #include <hip/hip_runtime.h>
 
 #include "common.h"
+
+#ifdef SH_GPT2_TRACE
+// Diagnostic builds only (-DSH_GPT2_TRACE): wall-clock marks per workgroup
+// and layer: slots 0..4 the ends of its A..E items, 5..9 the ends of their
+// waits, 10 the kernel's start (layer 0), 11 the head's end (layer 0),
+// 12 + 3 p .. 14 + 3 p the entry, the first failed poll and the number of
+// polls of phase p's wait, 27 + p when phase p's cell stores were acked.
+constexpr int kTrWgs = 256, kTrLayers = 16, kTrSlots = 32;
+__device__ unsigned long long g_gpt2_trace[kTrWgs][kTrLayers][kTrSlots];
+__device__ unsigned long long g_gpt2_xt[kTrWgs][3];
+#define SH_XCHG_TRACE(t_enter, t_first, polls)                                        \
+  do {                                                                                 \
+    if (threadIdx.x == 0 && blockIdx.x < kTrWgs) {                                    \
+      g_gpt2_xt[blockIdx.x][0] = t_enter;                                             \
+      g_gpt2_xt[blockIdx.x][1] = t_first;                                             \
+      g_gpt2_xt[blockIdx.x][2] = (unsigned long long)(polls);                         \
+    }                                                                                  \
+  } while (0)
+#define SH_G2MARK(l, slot)                                                              \
+  do {                                                                                   \
+    if (threadIdx.x == 0 && blockIdx.x < kTrWgs && (l) < kTrLayers)                     \
+      g_gpt2_trace[blockIdx.x][l][slot] = wall_clock64();                               \
+  } while (0)
+#define SH_G2WAIT(l, p)                                                                 \
+  do {                                                                                   \
+    if (threadIdx.x == 0 && blockIdx.x < kTrWgs && (l) < kTrLayers) {                   \
+      g_gpt2_trace[blockIdx.x][l][5 + (p)] = wall_clock64();                            \
+      for (int q_ = 0; q_ < 3; q_++)                                                    \
+        g_gpt2_trace[blockIdx.x][l][12 + 3 * (p) + q_] = g_gpt2_xt[blockIdx.x][q_];     \
+    }                                                                                    \
+  } while (0)
+// after a phase's cell stores: waits for their acknowledgement (every thread)
+#define SH_G2ACK(l, p)                                                                  \
+  do {                                                                                   \
+    __builtin_amdgcn_s_waitcnt(0x0F70);                                                 \
+    SH_G2MARK(l, 27 + (p));                                                             \
+  } while (0)
+#else
+#define SH_G2MARK(l, slot) ((void)0)
+#define SH_G2WAIT(l, p) ((void)0)
+#define SH_G2ACK(l, p) ((void)0)
+#endif
+
 #include "exchange.h"
 #include "llm.h"
 #include "llm_device.h"
@@ -47,20 +90,6 @@ constexpr int kVJ = kMaxChunk / 32;  // V rows per thread
 
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
-#ifdef SH_GPT2_TRACE
-// Diagnostic builds only (-DSH_GPT2_TRACE): wall-clock marks per workgroup
-// and layer: slots 0..4 the ends of its A..E items, 5..9 the ends of their
-// waits, 10 the kernel's start (layer 0), 11 the head's end (layer 0).
-constexpr int kTrWgs = 256, kTrLayers = 16, kTrSlots = 12;
-__device__ unsigned long long g_gpt2_trace[kTrWgs][kTrLayers][kTrSlots];
-#define SH_G2MARK(l, slot)                                                              \
-  do {                                                                                   \
-    if (threadIdx.x == 0 && blockIdx.x < kTrWgs && (l) < kTrLayers)                     \
-      g_gpt2_trace[blockIdx.x][l][slot] = wall_clock64();                               \
-  } while (0)
-#else
-#define SH_G2MARK(l, slot) ((void)0)
-#endif
 
 struct LayerP {
   const SH_XGLOBAL uint16_t *wqkv, *wo, *wfc, *wproj;
@@ -247,10 +276,11 @@ __device__ __forceinline__ bool qkv_item(const Gpt2Args &a, const LayerP &P, int
   if (!stage_ln<(kLH * 128 + 1023) / 1024>(a, a.x0c, l == 0 ? a.x_in : nullptr, tag_of(ep, l - 1),
                                             P.ln1_g, P.ln1_b, a.H, S))
     return false;
-  SH_G2MARK(l, 5);
+  SH_G2WAIT(l, 0);
   f32x4 acc = reduce_waves(mfma_weights<kLH>(w, S.xs), S);
   if (threadIdx.x < 16) cst(a.qkvc, (size_t)i * 16 + col, bits_of(acc[0] + bias), tag_of(ep, l));
   SH_G2MARK(l, 0);
+  SH_G2ACK(l, 0);
   return true;
 }
 
@@ -307,7 +337,7 @@ __device__ __forceinline__ bool attn_item(const Gpt2Args &a, const LayerP &P, in
     uint64_t cv[1];
     const bool ok = spin_cells(a, a.qkvc, [&](int) { return cell; }, t < 192 ? 1ull : 0ull, tag, cv);
     if (!waits_ok(a, ok, &S.votes)) return false;
-    SH_G2MARK(l, 6);
+    SH_G2WAIT(l, 1);
     const float v = cell_f32(cv[0]);
     if (t < 64) {
       S.q[d] = v * a.scale;
@@ -381,6 +411,7 @@ __device__ __forceinline__ bool attn_item(const Gpt2Args &a, const LayerP &P, in
     cst(a.partc, pp + kHd + 1, bits_of(lsum), tag);
   }
   SH_G2MARK(l, 1);
+  SH_G2ACK(l, 1);
   return true;
 }
 
@@ -452,7 +483,7 @@ __device__ __forceinline__ bool o_item(const Gpt2Args &a, const LayerP &P, int l
   const float x0 = l == 0 ? gbl(a.x_in)[cell] : 0.0f;
   __builtin_amdgcn_sched_barrier(0);
   if (!stage_attn<(kLH * 128 + 255) / 256>(a, tag_of(ep, l), L, S)) return false;
-  SH_G2MARK(l, 7);
+  SH_G2WAIT(l, 2);
   const f32x4 acc = reduce_waves(mfma_weights<kLH>(w, S.xs), S);
   if (threadIdx.x < 16) {
     float x = x0;
@@ -464,6 +495,7 @@ __device__ __forceinline__ bool o_item(const Gpt2Args &a, const LayerP &P, int l
   }
   asm volatile("" ::"v"(rc));  // the residual load retires here in every thread
   SH_G2MARK(l, 2);
+  SH_G2ACK(l, 2);
   return true;
 }
 
@@ -478,7 +510,7 @@ __device__ __forceinline__ bool fc_item(const Gpt2Args &a, const LayerP &P, int 
   __builtin_amdgcn_sched_barrier(0);
   if (!stage_ln<(kLH * 128 + 1023) / 1024>(a, a.x1c, nullptr, tag_of(ep, l), P.ln2_g, P.ln2_b, a.H, S))
     return false;
-  SH_G2MARK(l, 8);
+  SH_G2WAIT(l, 3);
   const f32x4 acc = reduce_waves(mfma_weights<kLH>(w, S.xs), S);
   if (threadIdx.x < 64) {
     const uint32_t hv = f32_to_f16_bits(gelu_tanh(acc[0] + bias));
@@ -487,6 +519,7 @@ __device__ __forceinline__ bool fc_item(const Gpt2Args &a, const LayerP &P, int 
       cst(a.actc, ((size_t)i * 16 + col) / 2, hv | (nb << 16), tag_of(ep, l));
   }
   SH_G2MARK(l, 3);
+  SH_G2ACK(l, 3);
   return true;
 }
 
@@ -504,7 +537,7 @@ __device__ __forceinline__ bool proj_item(const Gpt2Args &a, const LayerP &P, in
   uint64_t rc = cld(a.x1c, cell);
   __builtin_amdgcn_sched_barrier(0);
   if (!stage_f16<(kLI * 128 + 1023) / 1024>(a, a.actc, tag, a.inter, S)) return false;
-  SH_G2MARK(l, 9);
+  SH_G2WAIT(l, 4);
   const f32x4 acc = reduce_waves(mfma_weights<kLI>(w, S.xs), S);
   if (threadIdx.x < 16) {
     if (!finish_cell(a, a.x1c, cell, tag, rc)) atomicOr(a.err, 1u);
@@ -514,6 +547,7 @@ __device__ __forceinline__ bool proj_item(const Gpt2Args &a, const LayerP &P, in
   }
   asm volatile("" ::"v"(rc));
   SH_G2MARK(l, 4);
+  SH_G2ACK(l, 4);
   return true;
 }
 

@@ -95,9 +95,10 @@ __global__ __launch_bounds__(kBlock) void brightness_byte_kernel(const uint8_t *
 // into 16-bit lanes (R|B and G|A words) and added to the 5-row column sums
 // (the halo pixels' sums alongside), the row leaving the window is
 // subtracted, and the 5-pixel horizontal sum of the column sums is the
-// 25-tap box sum of the output row two rows up. Raw rows sit in a 10-slot
-// register ring (the window, the current row and the next four in flight);
-// the loop is unrolled so the slots are static.
+// 25-tap box sum of the output row two rows up. Rows are requested five
+// steps ahead into a 5-slot ring of raw loads and kept, expanded, in a
+// 5-slot ring of the window's rows; the loop is unrolled so the slots are
+// static.
 // ---------------------------------------------------------------------------
 
 constexpr int kStripPx = 256;  // 64 lanes x 4 pixels
