@@ -342,13 +342,27 @@ __device__ __forceinline__ void reduce_waves(f32x4 (&acc)[kNT], float *red) {
   }
 }
 
+// The 4-value chunks of a K-value row a thread stages: wave w holds the
+// chunks of its K quarter, [w K / 16, (w + 1) K / 16), lane l the chunks
+// w K / 16 + l + 64 j. That is the quarter of xs the wave's MFMAs read
+// (mfma_weights), so a GEMV item needs no workgroup barrier between staging
+// and its MFMAs: a wave's LDS reads follow its own writes in order.
+__device__ __forceinline__ int stage_chunk(int K, int j) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  return wave * (K >> 4) + lane + 64 * j;
+}
+__device__ __forceinline__ bool stage_chunk_ok(int K, int j) {
+  return (threadIdx.x & 63) + 64 * j < (K >> 4);
+}
+
 // Rows [B][K] of fp32 x -> RMSNorm with gains g -> xs (fp16, row stride
 // K + 8), kRows rows per pass. The rows come from cells xc tagged `tag` or,
 // for the first layer, from the plain buffer xp the embedding kernel wrote
-// before this launch. Each thread keeps its 4-value chunks in registers;
-// the per-row sums of squares are combined across the four waves through
-// LDS. kChunks >= K / 4 / 256.
-template <int kChunks, int kRows>
+// before this launch. Each thread keeps its 4-value chunks (stage_chunk) in
+// registers; the per-row sums of squares are combined across the four
+// waves through LDS. kChunks >= K / 1024. kLocal: the caller's waves read
+// only their own K quarter of xs, so no barrier follows the stores.
+template <int kChunks, int kRows, bool kLocal>
 __device__ __forceinline__ bool stage_rms(const LayersArgs &a, const uint64_t *xc, const float *xp, unsigned tag,
                           const SH_GLOBAL float *g, int K, _Float16 *xs, Misc *misc) {
   typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
@@ -358,7 +372,7 @@ __device__ __forceinline__ bool stage_rms(const LayersArgs &a, const uint64_t *x
   f32x4 gv[kChunks];
 #pragma unroll
   for (int j = 0; j < kChunks; j++)
-    gv[j] = *reinterpret_cast<const SH_GLOBAL f32x4 *>(g + min(t + kT * j, c4 - 1) * 4);
+    gv[j] = *reinterpret_cast<const SH_GLOBAL f32x4 *>(g + min(stage_chunk(K, j), c4 - 1) * 4);
   for (int b0 = 0; b0 < B; b0 += kRows) {
     f32x4 v[kRows][kChunks];
     bool ok = true;
@@ -367,23 +381,24 @@ __device__ __forceinline__ bool stage_rms(const LayersArgs &a, const uint64_t *x
       for (int r = 0; r < kRows; r++)
 #pragma unroll
         for (int j = 0; j < kChunks; j++) {
-          const int c = min(t + kT * j, c4 - 1), b = min(b0 + r, B - 1);
+          const int c = min(stage_chunk(K, j), c4 - 1), b = min(b0 + r, B - 1);
           v[r][j] = *reinterpret_cast<const f32x4 *>(xp + (size_t)b * K + c * 4);
         }
     } else {
-      // cells of chunk (r, j): row b0 + r, values 4 c .. 4 c + 3, c = t + 256 j
-      // (rows past B and chunks past the row re-read the last ones)
+      // cells of chunk (r, j): row b0 + r, values 4 c .. 4 c + 3, c =
+      // stage_chunk(K, j) (rows past B and chunks past the wave's quarter
+      // re-read valid ones)
       uint64_t cv[kN];
       uint64_t mask = 0;
 #pragma unroll
       for (int r = 0; r < kRows; r++)
 #pragma unroll
         for (int j = 0; j < kChunks; j++)
-          if (b0 + r < B && t + kT * j < c4) mask |= 15ull << ((r * kChunks + j) * 4);
+          if (b0 + r < B && stage_chunk_ok(K, j)) mask |= 15ull << ((r * kChunks + j) * 4);
       ok = spin_cells(a, xc,
                       [&](int k) {
                         const int r = k / (kChunks * 4), j = (k / 4) % kChunks, e = k % 4;
-                        return (size_t)min(b0 + r, B - 1) * K + min(t + kT * j, c4 - 1) * 4 + e;
+                        return (size_t)min(b0 + r, B - 1) * K + min(stage_chunk(K, j), c4 - 1) * 4 + e;
                       },
                       mask, tag, cv);
 #pragma unroll
@@ -400,7 +415,7 @@ __device__ __forceinline__ bool stage_rms(const LayersArgs &a, const uint64_t *x
       float ss = 0.0f;
 #pragma unroll
       for (int j = 0; j < kChunks; j++)
-        if (t + kT * j < c4)
+        if (stage_chunk_ok(K, j))
           ss += (v[r][j][0] * v[r][j][0] + v[r][j][1] * v[r][j][1]) +
                 (v[r][j][2] * v[r][j][2] + v[r][j][3] * v[r][j][3]);
       ss = wave_sum_rows(ss);
@@ -415,42 +430,45 @@ __device__ __forceinline__ bool stage_rms(const LayersArgs &a, const uint64_t *x
       const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
 #pragma unroll
       for (int j = 0; j < kChunks; j++) {
-        const int c = t + kT * j;
-        if (c < c4) {
+        const int c = stage_chunk(K, j);
+        if (stage_chunk_ok(K, j)) {
           const f32x4 y = v[r][j] * inv * gv[j];
           *reinterpret_cast<f16x4 *>(xs + b * (K + 8) + c * 4) =
               f16x4{(_Float16)y[0], (_Float16)y[1], (_Float16)y[2], (_Float16)y[3]};
         }
       }
     }
-    lds_barrier();
+    // the next pass's sums reuse misc->part; with kLocal, the MFMAs read
+    // only this wave's stores
+    if (!kLocal || b0 + kRows < B) lds_barrier();
   }
   return true;
 }
 
 // Rows [B][K] of fp16 values packed two per cell (K / 2 cells per row,
-// tagged `tag`) -> xs (row stride K + 8), kRows rows per pass. kChunks >=
-// K / 4 / 256 two-cell chunks per thread and row.
-template <int kChunks, int kRows>
+// tagged `tag`) -> xs (row stride K + 8), kRows rows per pass. A thread
+// stages the two-cell chunks stage_chunk(K, j), j < kChunks (kChunks >=
+// K / 1024). kLocal as for stage_rms.
+template <int kChunks, int kRows, bool kLocal>
 __device__ __forceinline__ bool stage_f16(const LayersArgs &a, const uint64_t *cells, unsigned tag, int K,
                           _Float16 *xs, Misc *misc) {
   constexpr int kN = kRows * kChunks * 2;
   static_assert(kN <= 64, "cells per thread");
-  const int B = kRows == 1 ? 1 : a.B, c4 = K >> 2, t = threadIdx.x, row_cells = K >> 1;
+  const int B = kRows == 1 ? 1 : a.B, c4 = K >> 2, row_cells = K >> 1;
   for (int b0 = 0; b0 < B; b0 += kRows) {
-    // cells of chunk (r, j): row b0 + r, cells 2 c, 2 c + 1, c = t + 256 j
+    // cells of chunk (r, j): row b0 + r, cells 2 c, 2 c + 1, c = stage_chunk(K, j)
     uint64_t cv[kN];
     uint64_t mask = 0;
 #pragma unroll
     for (int r = 0; r < kRows; r++)
 #pragma unroll
       for (int j = 0; j < kChunks; j++)
-        if (b0 + r < B && t + kT * j < c4) mask |= 3ull << ((r * kChunks + j) * 2);
+        if (b0 + r < B && stage_chunk_ok(K, j)) mask |= 3ull << ((r * kChunks + j) * 2);
     const bool ok = spin_cells(a, cells,
                                [&](int k) {
                                  const int r = k / (kChunks * 2), j = (k / 2) % kChunks, e = k % 2;
                                  return (size_t)min(b0 + r, B - 1) * row_cells +
-                                        min(t + kT * j, c4 - 1) * 2 + e;
+                                        min(stage_chunk(K, j), c4 - 1) * 2 + e;
                                },
                                mask, tag, cv);
     if (!waits_ok(a, ok, misc)) return false;
@@ -458,12 +476,12 @@ __device__ __forceinline__ bool stage_f16(const LayersArgs &a, const uint64_t *c
     for (int r = 0; r < kRows; r++)
 #pragma unroll
       for (int j = 0; j < kChunks; j++) {
-        const int b = b0 + r, c = t + kT * j, k = (r * kChunks + j) * 2;
-        if (b < B && c < c4)
+        const int b = b0 + r, c = stage_chunk(K, j), k = (r * kChunks + j) * 2;
+        if (b < B && stage_chunk_ok(K, j))
           *reinterpret_cast<u32x2 *>(xs + b * (K + 8) + c * 4) = u32x2{(uint32_t)cv[k], (uint32_t)cv[k + 1]};
       }
   }
-  lds_barrier();
+  if (!kLocal) lds_barrier();
   return true;
 }
 
@@ -538,7 +556,7 @@ __device__ __forceinline__ bool qkv_item(const LayersArgs &a, const LayerG &P, i
   const int lane = threadIdx.x & 63, col = lane & 15;
   const float sc = P.sqkv[i * 16 + col];
   __builtin_amdgcn_sched_barrier(0);
-  if (!stage_rms<(kL + 3) / 4, kRows>(a, a.x0c, l == 0 ? a.x_in : nullptr, tag_of(ep, l - 1), P.norm1,
+  if (!stage_rms<(kL + 3) / 4, kRows, true>(a, a.x0c, l == 0 ? a.x_in : nullptr, tag_of(ep, l - 1), P.norm1,
                                a.H, s.xs, s.misc))
     return false;
   SH_MARK(s.misc, l, 0);
@@ -571,7 +589,7 @@ __device__ __forceinline__ bool o_item(const LayersArgs &a, const LayerG &P, int
   uint64_t rc[4];
   request_residual<kOutRows<kRows>>(a, a.x0c, l == 0 ? a.x_in : nullptr, i * 16 + col, rv, rc);
   __builtin_amdgcn_sched_barrier(0);
-  if (!stage_f16<(kL + 3) / 4, kRows>(a, a.attnc, tag_of(ep, l), K, s.xs, s.misc)) return false;
+  if (!stage_f16<(kL + 3) / 4, kRows, true>(a, a.attnc, tag_of(ep, l), K, s.xs, s.misc)) return false;
   f32x4 acc[1];
   mfma_weights<kL, 1>(w, s.xs, K + 8, kRows == 1 ? 1 : a.B, acc);
   reduce_waves<1>(acc, s.red);
@@ -599,7 +617,7 @@ __device__ __forceinline__ bool up_item(const LayersArgs &a, const LayerG &P, in
   const int ng = 2 * p * 16 + col;  // tiled rows of the gate and up tiles of pair p
   const float sg = P.sup[ng], su = P.sup[ng + 16];
   __builtin_amdgcn_sched_barrier(0);
-  if (!stage_rms<(kL + 3) / 4, kRows>(a, a.x1c, nullptr, tag_of(ep, l), P.norm2, a.H, s.xs, s.misc))
+  if (!stage_rms<(kL + 3) / 4, kRows, true>(a, a.x1c, nullptr, tag_of(ep, l), P.norm2, a.H, s.xs, s.misc))
     return false;
   f32x4 acc[2];
   mfma_weights<kL, 2>(w, s.xs, a.H + 8, kRows == 1 ? 1 : a.B, acc);
@@ -632,7 +650,7 @@ __device__ __forceinline__ bool down_item(const LayersArgs &a, const LayerG &P, 
   uint64_t rc[4];
   request_residual<kOutRows<kRows>>(a, a.x1c, nullptr, i * 16 + col, rv, rc);
   __builtin_amdgcn_sched_barrier(0);
-  if (!stage_f16<(kL + 3) / 4, kRows>(a, a.actc, tag, K, s.xs, s.misc)) return false;
+  if (!stage_f16<(kL + 3) / 4, kRows, true>(a, a.actc, tag, K, s.xs, s.misc)) return false;
   SH_MARK(s.misc, l, 4);
   f32x4 acc[1];
   mfma_weights<kL, 1>(w, s.xs, K + 8, kRows == 1 ? 1 : a.B, acc);
@@ -682,6 +700,7 @@ struct AttnLds {
   float scores[kG][kMaxSplitChunk];
   alignas(16) _Float16 p[kG][kMaxSplitChunk + kBlk];  // probabilities, zero up to whole blocks
   float wmax[4][kG], wl[4][kG];
+  float sdump[4][kG][64];  // where the score stores of lanes without a score go
 };
 
 // LDS of a merge item.
@@ -768,7 +787,10 @@ __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, 
   AttnLds<kG> &S = *reinterpret_cast<AttnLds<kG> *>(smem);
   const int splits = a.splits, kvn = a.kv_heads;
   const int s = item % splits, kvh = (item / splits) % kvn, b = item / (splits * kvn);
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, r = lane & 15, grp = lane >> 4;
+  // wave through readfirstlane: the compiler then treats conditions on it
+  // as uniform (scalar branches, no exec masks between MFMA chains)
+  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), r = lane & 15,
+            grp = lane >> 4;
   const int chunk = a.chunk, p0 = s * chunk;
   const int cap = min(chunk, a.max_pos - p0);  // <= 0 for splits past the cache
   const size_t kv_row = (size_t)b * kvn + kvh;
@@ -861,31 +883,52 @@ __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, 
   const int nblk = (np + kBlk - 1) / kBlk;
 
   // scores: lanes 0..15 of a tile's result hold heads 0..3 of its 16
-  // positions; each lane keeps the max of the scores it stores
+  // positions; each lane keeps the max of the scores it stores. The new
+  // token's K replaces the cache copy in its lane's registers before a
+  // block's MFMAs (a fix-up between the tiles' MFMAs split them into basic
+  // blocks, and the tiles' chains ran one after another), the tiles have
+  // their own accumulators, and lanes without a score store it to a dump
+  // area (no branch around the stores).
   float M[kG], lsum[kG];
 #pragma unroll
   for (int g = 0; g < kG; g++) M[g] = -INFINITY;
   for (int bb = 0; bb < nblk; bb++) {
     const int pb = p0 + bb * kBlk;
     if (bb > 0) attn_load_k(kb, pb, split_end_k(a, s), kv);
+    const int pn = pos - pb;  // the new token's index in this block
+    if (holds_new && pn >= 0 && pn < kBlk) {  // uniform
+      const bool mine = r == (pn & 15);
+#pragma unroll
+      for (int tt = 0; tt < kKT; tt++)
+        if ((pn >> 4) == wave + 4 * tt) {  // uniform
+#pragma unroll
+          for (int kk = 0; kk < 4; kk++) {
+            const f16x8 kn = *reinterpret_cast<const f16x8 *>(&S.knew[32 * kk + 8 * grp]);
+            kv.k[tt][kk] = mine ? kn : kv.k[tt][kk];
+          }
+        }
+    }
+    // every wave runs kKT tiles; a tile past the block (waves 2 and 3's
+    // last) scores clamped rows that nothing stores or counts
+    // (the tiles' chains interleaved: each MFMA waits for its chain's last)
+    f32x4 acc[kKT];
+#pragma unroll
+    for (int tt = 0; tt < kKT; tt++) acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+      for (int tt = 0; tt < kKT; tt++)
+        acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[kk], kv.k[tt][kk], acc[tt], 0, 0, 0);
 #pragma unroll
     for (int tt = 0; tt < kKT; tt++) {
       const int tile = wave + 4 * tt;
-      if (tile >= kBlk / 16) continue;  // uniform
-      if (holds_new && pb + 16 * tile + r == pos) {  // the new token's K (not in the requested copy)
-#pragma unroll
-        for (int kk = 0; kk < 4; kk++) kv.k[tt][kk] = *reinterpret_cast<const f16x8 *>(&S.knew[32 * kk + 8 * grp]);
-      }
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < 4; kk++) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[kk], kv.k[tt][kk], acc, 0, 0, 0);
       const int pi = bb * kBlk + 16 * tile + lane;
-      if (lane < 16 && pi < np) {
+      const bool valid = tile < kBlk / 16 && lane < 16 && pi < np;
 #pragma unroll
-        for (int g = 0; g < kG; g++) {
-          S.scores[g][pi] = acc[g];
-          M[g] = fmaxf(M[g], acc[g]);
-        }
+      for (int g = 0; g < kG; g++) {
+        float *dst = valid ? &S.scores[g][pi] : &S.sdump[wave][g][lane];
+        *dst = acc[tt][g];
+        M[g] = fmaxf(M[g], valid ? acc[tt][g] : -INFINITY);
       }
     }
   }
@@ -1091,7 +1134,7 @@ __device__ __forceinline__ bool head_phase(const LayersArgs &a, unsigned ep, con
   };
   if (first < nT) load_tile(wb[0], sc[0], first);
   __builtin_amdgcn_sched_barrier(0);
-  if (!stage_rms<(kLA + 3) / 4, kRows>(a, a.x0c, nullptr, tag_of(ep, a.n_layers - 1), gbl(a.final_g),
+  if (!stage_rms<(kLA + 3) / 4, kRows, false>(a, a.x0c, nullptr, tag_of(ep, a.n_layers - 1), gbl(a.final_g),
                                        H, s.xs, s.misc))
     return false;
   const int arow = lane & 15, acol = 8 * (lane >> 4);
@@ -1226,8 +1269,14 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
           return true;
         }))
       return;
-    // workgroups with an O item: the next layer's K / V while the gate/up
-    // items run; the others after their gate/up item, with the next QKV weights
+    // Workgroups with an O item: the next layer's K / V while the gate/up
+    // items run; the others after their gate/up item, with the next QKV
+    // weights. Loads complete in issue order, and a wave also stalls at
+    // issuing a bulk request while the memory pipeline is backed up: both
+    // belong where the workgroup waits at least an exchange anyway. (Right
+    // after the attention item, the K / V delayed the O items' polls;
+    // between the down item's wait and its MFMAs, their issue stalled the
+    // down item by ~2 us.)
     if (hasC && next && w < nB) attn_prefetch(a, layer_g(a, l + 1), w, kv);
     if (!for_items<kOne>(d0, nD, G, [&](int i) {
           if (i == d0) SH_TRACE(misc, l, 6);
