@@ -638,12 +638,11 @@ __device__ __forceinline__ bool up_item(const LayersArgs &a, const LayerG &P, in
 
 // E: x[b][16 i + c] = x_mid[b][.] + scale * (W_down act); the last layer
 // writes the plain buffer the final norm reads
+// w holds the item's weights (requested by the caller).
 template <int kL, int kRows>
 __device__ __forceinline__ bool down_item(const LayersArgs &a, const LayerG &P, int l, int i, unsigned ep,
-                          const Lds &s) {
+                          const Lds &s, const u32x4 (&w)[kL][1]) {
   const int lane = threadIdx.x & 63, col = lane & 15, K = a.inter;
-  u32x4 w[kL][1];
-  load_weights<kL, 1>(w, P.wdown, K, i);
   const float sc = P.sdown[i * 16 + col];
   const unsigned tag = tag_of(ep, l);
   float rv[4];
@@ -1262,6 +1261,12 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
       return;
     // O, gate/up and down items request their weights when they start: at
     // batch 1 each workgroup's previous item is then a phase or more behind
+    // Workgroups with an O item request their down item's weights before
+    // it, so the windows before the O item's and the down item's polls
+    // carry 80 and 64 KiB of requests (with the down weights after the O
+    // item: 32 and 112 KiB, and the down items' polls came last).
+    u32x4 wd[kLE][1];
+    if (w < nE) load_weights<kLE, 1>(wd, P.wdown, a.inter, w);
     if (!for_items<kOne>(w, nC, G, [&](int i) {
           if (i == w) SH_TRACE(misc, l, 4);
           if (!o_item<kLC, kRows>(a, P, l, i, ep, lds)) return false;
@@ -1269,15 +1274,19 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
           return true;
         }))
       return;
-    // Workgroups with an O item: the next layer's K / V while the gate/up
-    // items run; the others after their gate/up item, with the next QKV
-    // weights. Loads complete in issue order, and a wave also stalls at
-    // issuing a bulk request while the memory pipeline is backed up: both
-    // belong where the workgroup waits at least an exchange anyway. (Right
-    // after the attention item, the K / V delayed the O items' polls;
-    // between the down item's wait and its MFMAs, their issue stalled the
-    // down item by ~2 us.)
-    if (hasC && next && w < nB) attn_prefetch(a, layer_g(a, l + 1), w, kv);
+    // The next layer's K / V and QKV weights: on workgroups with an O item
+    // while the gate/up items run, on the others after their gate/up item.
+    // Loads complete in issue order, and a wave also stalls at issuing a
+    // bulk request while the memory pipeline is backed up: both belong
+    // where the workgroup waits at least an exchange anyway. (Right after
+    // the attention item, the K / V delayed the O items' polls; between the
+    // down item's wait and its MFMAs, their issue stalled the down item by
+    // ~2 us; on the workgroups with only a gate/up item, right after the
+    // attention item, the burst slowed the merge and O items' polls.)
+    if (hasC && next) {
+      if (w < nB) attn_prefetch(a, layer_g(a, l + 1), w, kv);
+      if (w < nA) load_weights<kLA, 1>(wa, layer_g(a, l + 1).wqkv, H, w);
+    }
     if (!for_items<kOne>(d0, nD, G, [&](int i) {
           if (i == d0) SH_TRACE(misc, l, 6);
           if (!up_item<kLD, kRows>(a, P, l, i, ep, lds)) return false;
@@ -1291,12 +1300,12 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
     }
     if (!for_items<kOne>(w, nE, G, [&](int i) {
           if (i == w) SH_TRACE(misc, l, 8);
-          if (!down_item<kLE, kRows>(a, P, l, i, ep, lds)) return false;
+          if (i != w) load_weights<kLE, 1>(wd, P.wdown, a.inter, i);
+          if (!down_item<kLE, kRows>(a, P, l, i, ep, lds, wd)) return false;
           if (i == w) { SH_TRACE(misc, l, 9); SH_TRACE_WAIT(l, 4, misc); }
           return true;
         }))
       return;
-    if (hasC && next && w < nA) load_weights<kLA, 1>(wa, layer_g(a, l + 1).wqkv, H, w);
   }
   if (a.head_on && !head_phase<kLA, kRows>(a, ep, lds)) return;
 #ifdef SH_DECODE_TRACE
