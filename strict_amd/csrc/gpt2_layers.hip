@@ -109,7 +109,7 @@ __device__ __forceinline__ LayerP layer_p(const Gpt2Args &a, int l) {
 struct Lds {
   alignas(16) _Float16 xs[4096 + 8];  // the MFMA A operand row (fp16)
   alignas(16) float red[3][64][4];    // waves 1..3's accumulators
-  float part[4];                      // per-wave partial sums
+  float part[2][4];                   // per-wave partial sums (LayerNorm's two)
   Votes votes;
   // attention
   alignas(16) float q[kHd];
@@ -172,29 +172,42 @@ __device__ __forceinline__ f32x4 reduce_waves(f32x4 acc, Lds &S) {
   return acc;
 }
 
-// Sum of one value per thread over the workgroup (every thread gets it).
-__device__ __forceinline__ float block_sum(float v, Lds &S) {
+// Sum of one value per thread over the workgroup (every thread gets it),
+// through partial-sum slot k (a slot is written again only after the
+// workgroup's next barrier).
+__device__ __forceinline__ float block_sum(float v, int k, Lds &S) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   v = wave_sum_rows(v);
-  if (lane == 0) S.part[wave] = v;
+  if (lane == 0) S.part[k][wave] = v;
   lds_barrier();
-  const float s = (S.part[0] + S.part[1]) + (S.part[2] + S.part[3]);
-  lds_barrier();  // part is reused by the next call
-  return s;
+  return (S.part[k][0] + S.part[k][1]) + (S.part[k][2] + S.part[k][3]);
+}
+
+// The 4-value chunks of a K-value row a thread stages: wave w holds those of
+// its K quarter, [w K / 16, (w + 1) K / 16), lane l the chunks w K / 16 + l +
+// 64 j. That is the quarter of xs the wave's MFMAs read (mfma_weights), so a
+// GEMV item needs no workgroup barrier between staging and its MFMAs: a
+// wave's LDS reads follow its own writes in order.
+__device__ __forceinline__ int stage_chunk(int K, int j) {
+  return (threadIdx.x >> 6) * (K >> 4) + (threadIdx.x & 63) + 64 * j;
+}
+__device__ __forceinline__ bool stage_chunk_ok(int K, int j) {
+  return (threadIdx.x & 63) + 64 * j < (K >> 4);
 }
 
 // LayerNorm of the fp32 row x (K values: cells tagged `tag`, or the plain
-// buffer xp) with gains g and biases b -> xs (fp16). Thread t holds the
-// 4-value chunks t + 256 j, j < kC.
-template <int kC>
+// buffer xp) with gains g and biases b -> xs (fp16). A thread holds the
+// 4-value chunks stage_chunk(K, j), j < kC. kLocal: the caller's waves read
+// only their own K quarter of xs, so no barrier follows the stores.
+template <int kC, bool kLocal>
 __device__ __forceinline__ bool stage_ln(const Gpt2Args &a, const uint64_t *xc, const float *xp,
                                          unsigned tag, const SH_XGLOBAL float *g,
                                          const SH_XGLOBAL float *bta, int K, Lds &S) {
-  const int t = threadIdx.x, c4 = K >> 2;
+  const int c4 = K >> 2;
   f32x4 gv[kC], bv[kC], v[kC];
 #pragma unroll
   for (int j = 0; j < kC; j++) {
-    const int c = min(t + kT * j, c4 - 1);
+    const int c = min(stage_chunk(K, j), c4 - 1);
     gv[j] = *reinterpret_cast<const SH_XGLOBAL f32x4 *>(g + c * 4);
     bv[j] = *reinterpret_cast<const SH_XGLOBAL f32x4 *>(bta + c * 4);
   }
@@ -202,14 +215,14 @@ __device__ __forceinline__ bool stage_ln(const Gpt2Args &a, const uint64_t *xc, 
   if (xp) {
 #pragma unroll
     for (int j = 0; j < kC; j++)
-      v[j] = *reinterpret_cast<const SH_XGLOBAL f32x4 *>(gbl(xp) + min(t + kT * j, c4 - 1) * 4);
+      v[j] = *reinterpret_cast<const SH_XGLOBAL f32x4 *>(gbl(xp) + min(stage_chunk(K, j), c4 - 1) * 4);
   } else {
     uint64_t cv[kC * 4];
     uint64_t mask = 0;
 #pragma unroll
     for (int j = 0; j < kC; j++)
-      if (t + kT * j < c4) mask |= 15ull << (j * 4);
-    ok = spin_cells(a, xc, [&](int k) { return (size_t)min(t + kT * (k >> 2), c4 - 1) * 4 + (k & 3); },
+      if (stage_chunk_ok(K, j)) mask |= 15ull << (j * 4);
+    ok = spin_cells(a, xc, [&](int k) { return (size_t)min(stage_chunk(K, k >> 2), c4 - 1) * 4 + (k & 3); },
                     mask, tag, cv);
 #pragma unroll
     for (int j = 0; j < kC; j++)
@@ -220,49 +233,50 @@ __device__ __forceinline__ bool stage_ln(const Gpt2Args &a, const uint64_t *xc, 
   float sm = 0.0f;
 #pragma unroll
   for (int j = 0; j < kC; j++)
-    if (t + kT * j < c4) sm += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
-  const float mean = block_sum(sm, S) / (float)K;
+    if (stage_chunk_ok(K, j)) sm += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
+  const float mean = block_sum(sm, 0, S) / (float)K;
   float ss = 0.0f;
 #pragma unroll
   for (int j = 0; j < kC; j++)
-    if (t + kT * j < c4) {
+    if (stage_chunk_ok(K, j)) {
       const f32x4 d = v[j] - mean;
       ss += (d[0] * d[0] + d[1] * d[1]) + (d[2] * d[2] + d[3] * d[3]);
     }
-  const float inv = 1.0f / sqrtf(block_sum(ss, S) / (float)K + a.eps);
+  const float inv = 1.0f / sqrtf(block_sum(ss, 1, S) / (float)K + a.eps);
 #pragma unroll
   for (int j = 0; j < kC; j++) {
-    const int c = t + kT * j;
-    if (c < c4) {
+    const int c = stage_chunk(K, j);
+    if (stage_chunk_ok(K, j)) {
       const f32x4 y = (v[j] - mean) * inv * gv[j] + bv[j];
       *reinterpret_cast<f16x4 *>(S.xs + c * 4) =
           f16x4{(_Float16)y[0], (_Float16)y[1], (_Float16)y[2], (_Float16)y[3]};
     }
   }
-  lds_barrier();
+  if (!kLocal) lds_barrier();
   return true;
 }
 
-// fp16 row of K values packed two per cell (tagged `tag`) -> xs. Thread t
-// holds the two-cell chunks t + 256 j, j < kC.
+// fp16 row of K values packed two per cell (tagged `tag`) -> xs. A thread
+// holds the two-cell chunks stage_chunk(K, j), j < kC; the caller's waves
+// read only their own K quarter of xs.
 template <int kC>
 __device__ __forceinline__ bool stage_f16(const Gpt2Args &a, const uint64_t *cells, unsigned tag,
                                           int K, Lds &S) {
-  const int t = threadIdx.x, c4 = K >> 2;
+  const int c4 = K >> 2;
   uint64_t cv[kC * 2];
   uint64_t mask = 0;
 #pragma unroll
   for (int j = 0; j < kC; j++)
-    if (t + kT * j < c4) mask |= 3ull << (j * 2);
-  const bool ok = spin_cells(a, cells, [&](int k) { return (size_t)min(t + kT * (k >> 1), c4 - 1) * 2 + (k & 1); },
-                             mask, tag, cv);
+    if (stage_chunk_ok(K, j)) mask |= 3ull << (j * 2);
+  const bool ok = spin_cells(
+      a, cells, [&](int k) { return (size_t)min(stage_chunk(K, k >> 1), c4 - 1) * 2 + (k & 1); }, mask, tag, cv);
   if (!waits_ok(a, ok, &S.votes)) return false;
 #pragma unroll
   for (int j = 0; j < kC; j++) {
-    const int c = t + kT * j;
-    if (c < c4) *reinterpret_cast<u32x2 *>(S.xs + c * 4) = u32x2{(uint32_t)cv[2 * j], (uint32_t)cv[2 * j + 1]};
+    const int c = stage_chunk(K, j);
+    if (stage_chunk_ok(K, j))
+      *reinterpret_cast<u32x2 *>(S.xs + c * 4) = u32x2{(uint32_t)cv[2 * j], (uint32_t)cv[2 * j + 1]};
   }
-  lds_barrier();
   return true;
 }
 
@@ -273,7 +287,7 @@ __device__ __forceinline__ bool qkv_item(const Gpt2Args &a, const LayerP &P, int
   const int lane = threadIdx.x & 63, col = lane & 15;
   const float bias = P.bqkv[i * 16 + col];
   __builtin_amdgcn_sched_barrier(0);
-  if (!stage_ln<(kLH * 128 + 1023) / 1024>(a, a.x0c, l == 0 ? a.x_in : nullptr, tag_of(ep, l - 1),
+  if (!stage_ln<(kLH * 128 + 1023) / 1024, true>(a, a.x0c, l == 0 ? a.x_in : nullptr, tag_of(ep, l - 1),
                                             P.ln1_g, P.ln1_b, a.H, S))
     return false;
   SH_G2WAIT(l, 0);
@@ -415,13 +429,14 @@ __device__ __forceinline__ bool attn_item(const Gpt2Args &a, const LayerP &P, in
   return true;
 }
 
-// The attention output of every head (the splits merged, fp16) -> xs:
-// thread t computes values t + 256 j, j < kC, of the H = heads * 64, over
-// the first kNS splits (the active ones, ns <= kNS; the polls load only
-// those: every poll of a wait reloads all of its cells).
+// The attention output of every head (the splits merged, fp16) -> xs: a
+// thread computes values wave H / 4 + lane + 64 j, j < kC, of the H =
+// heads * 64 (the wave's K quarter of the O item's MFMAs, so no barrier
+// follows), over the first kNS splits (the active ones, ns <= kNS; the polls
+// load only those: every poll of a wait reloads all of its cells).
 template <int kC, int kNS>
 __device__ __forceinline__ bool stage_attn_n(const Gpt2Args &a, unsigned tag, int ns, Lds &S) {
-  const int t = threadIdx.x;
+  const int lane = threadIdx.x & 63, q4 = a.H >> 2, base = (threadIdx.x >> 6) * q4;
   constexpr int kN = kC * kNS * 3;
   uint64_t cv[kN];
   uint64_t mask = 0;
@@ -429,11 +444,11 @@ __device__ __forceinline__ bool stage_attn_n(const Gpt2Args &a, unsigned tag, in
   for (int j = 0; j < kC; j++)
 #pragma unroll
     for (int s = 0; s < kNS; s++)
-      if (s < ns && t + kT * j < a.H) mask |= 7ull << ((j * kNS + s) * 3);
+      if (s < ns && lane + 64 * j < q4) mask |= 7ull << ((j * kNS + s) * 3);
   const bool ok = spin_cells(a, a.partc,
                              [&](int k) {
                                const int j = k / (kNS * 3), s = (k / 3) % kNS, f = k % 3;
-                               const int idx = min(t + kT * j, a.H - 1), h = idx >> 6, d = idx & 63;
+                               const int idx = base + min(lane + 64 * j, q4 - 1), h = idx >> 6, d = idx & 63;
                                const size_t pp = ((size_t)h * kGpt2Splits + min(s, ns - 1)) * kGpt2PStride;
                                return pp + (f == 0 ? d : kHd + f - 1);
                              },
@@ -441,8 +456,8 @@ __device__ __forceinline__ bool stage_attn_n(const Gpt2Args &a, unsigned tag, in
   if (!waits_ok(a, ok, &S.votes)) return false;
 #pragma unroll
   for (int j = 0; j < kC; j++) {
-    const int idx = t + kT * j;
-    if (idx >= a.H) continue;
+    if (lane + 64 * j >= q4) continue;
+    const int idx = base + lane + 64 * j;
     float M = -INFINITY;
 #pragma unroll
     for (int s = 0; s < kNS; s++)
@@ -458,7 +473,6 @@ __device__ __forceinline__ bool stage_attn_n(const Gpt2Args &a, unsigned tag, in
       }
     S.xs[idx] = (_Float16)(num / den);
   }
-  lds_barrier();
   return true;
 }
 
@@ -508,7 +522,7 @@ __device__ __forceinline__ bool fc_item(const Gpt2Args &a, const LayerP &P, int 
   load_weights<kLH>(w, P.wfc, a.H, i);
   const float bias = P.bfc[i * 16 + col];
   __builtin_amdgcn_sched_barrier(0);
-  if (!stage_ln<(kLH * 128 + 1023) / 1024>(a, a.x1c, nullptr, tag_of(ep, l), P.ln2_g, P.ln2_b, a.H, S))
+  if (!stage_ln<(kLH * 128 + 1023) / 1024, true>(a, a.x1c, nullptr, tag_of(ep, l), P.ln2_g, P.ln2_b, a.H, S))
     return false;
   SH_G2WAIT(l, 3);
   const f32x4 acc = reduce_waves(mfma_weights<kLH>(w, S.xs), S);
@@ -523,14 +537,13 @@ __device__ __forceinline__ bool fc_item(const Gpt2Args &a, const LayerP &P, int 
   return true;
 }
 
-// E: x[16 i + c] = x_mid[.] + W_proj act + b; the last layer also writes the
-// plain buffer the final LayerNorm reads
+// E: x[16 i + c] = x_mid[.] + W_proj act + b (w: the item's weights, requested
+// by the caller); the last layer also writes the plain buffer the final
+// LayerNorm reads
 template <int kLH, int kLI>
 __device__ __forceinline__ bool proj_item(const Gpt2Args &a, const LayerP &P, int l, int i, unsigned ep,
-                                          Lds &S) {
+                                          Lds &S, const u32x4 (&w)[kLI]) {
   const int lane = threadIdx.x & 63, col = lane & 15;
-  u32x4 w[kLI];
-  load_weights<kLI>(w, P.wproj, a.inter, i);
   const float bias = P.bproj[i * 16 + col];
   const size_t cell = (size_t)i * 16 + col;
   const unsigned tag = tag_of(ep, l);
@@ -571,7 +584,7 @@ __device__ __forceinline__ bool head_phase(const Gpt2Args &a, unsigned ep, Lds &
                                            u32x4 (&wb)[2][4 * kLH]) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, G = gridDim.x, w = blockIdx.x;
   const int first = w + G * wave, step = 4 * G, nT = a.head_tiles;
-  if (!stage_ln<(kLH * 128 + 1023) / 1024>(a, a.x0c, nullptr, tag_of(ep, a.n_layers - 1),
+  if (!stage_ln<(kLH * 128 + 1023) / 1024, false>(a, a.x0c, nullptr, tag_of(ep, a.n_layers - 1),
                                             gbl(a.final_g), gbl(a.final_b), a.H, S))
     return false;
   const _Float16 *xrow = S.xs + 8 * (lane >> 4);
@@ -634,7 +647,14 @@ __global__ __launch_bounds__(kT, 1) void gpt2_layers_kernel(const Gpt2Args a) {
       if (!attn_item(a, P, l, bi, ep, L, S, kv)) return;
       if (next && !hasD) attn_prefetch(a, layer_p(a, l + 1), bi, L, kv);
     }
+    // Workgroups with O and proj items request the proj weights (96 KiB at
+    // GPT-2 small) before the O item and the next QKV weights after it: the
+    // windows before the O, proj and next QKV polls then carry 120, 24 and
+    // 0 KiB of requests (loads complete in issue order; before: 24, 96, 24).
+    u32x4 wp[kLI];
+    if (w < nC) load_weights<kLI>(wp, P.wproj, a.inter, w);
     if (w < nC && !o_item<kLH>(a, P, l, w, ep, L, S)) return;
+    if (w < nC && next && w < nA) load_weights<kLH>(wa, layer_p(a, l + 1).wqkv, a.H, w);
     if (hasD) {
       if (!fc_item<kLH>(a, P, l, w - nC, ep, S)) return;
       if (next) {
@@ -643,8 +663,7 @@ __global__ __launch_bounds__(kT, 1) void gpt2_layers_kernel(const Gpt2Args a) {
       }
     }
     if (w < nC) {
-      if (!proj_item<kLH, kLI>(a, P, l, w, ep, S)) return;
-      if (next && w < nA) load_weights<kLH>(wa, layer_p(a, l + 1).wqkv, a.H, w);
+      if (!proj_item<kLH, kLI>(a, P, l, w, ep, S, wp)) return;
     }
     if (next && w < nA && w >= nC + nD) load_weights<kLH>(wa, layer_p(a, l + 1).wqkv, a.H, w);
   }
