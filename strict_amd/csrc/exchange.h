@@ -19,15 +19,6 @@
 namespace sh {
 namespace xchg {
 
-// Diagnostic hook: a file may define SH_XCHG_TRACE(t_enter, t_first, polls)
-// before including this header to see each finished wait of spin_cells.
-#ifndef SH_XCHG_TRACE
-#define SH_XCHG_TRACE(t_enter, t_first, polls) ((void)0)
-#define SH_XCHG_TRACE_ENTER 0ull
-#else
-#define SH_XCHG_TRACE_ENTER wall_clock64()
-#endif
-
 #define SH_XGLOBAL __attribute__((address_space(1)))
 #define SH_XCONST __attribute__((address_space(4)))
 
@@ -77,18 +68,13 @@ template <int kN, class A, class At>
 __device__ __forceinline__ bool spin_cells(const A &a, const uint64_t *base, At at, uint64_t mask,
                                            unsigned tag, uint64_t (&c)[kN]) {
   unsigned long long t0 = 0;
-  const unsigned long long t_enter = SH_XCHG_TRACE_ENTER;
-  (void)t_enter;
   for (int it = 0;; it++) {
 #pragma unroll
     for (int k = 0; k < kN; k++) c[k] = cld(base, at(k));
     bool ok = true;
 #pragma unroll
     for (int k = 0; k < kN; k++) ok = ok && ((mask >> k & 1) == 0 || (uint32_t)(c[k] >> 32) == tag);
-    if (ok) {
-      SH_XCHG_TRACE(t_enter, t0, it);
-      return true;
-    }
+    if (ok) return true;
     if (it == 0) {
       t0 = wall_clock64();
     } else if ((it & 7) == 0 && (ld_err(a) != 0 || wall_clock64() - t0 > a.spin_ticks)) {

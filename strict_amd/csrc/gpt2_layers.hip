@@ -35,44 +35,18 @@
 #ifdef SH_GPT2_TRACE
 // Diagnostic builds only (-DSH_GPT2_TRACE): wall-clock marks per workgroup
 // and layer: slots 0..4 the ends of its A..E items, 5..9 the ends of their
-// waits, 10 the kernel's start (layer 0), 11 the head's end (layer 0),
-// 12 + 3 p .. 14 + 3 p the entry, the first failed poll and the number of
-// polls of phase p's wait, 27 + p when phase p's cell stores were acked.
-constexpr int kTrWgs = 256, kTrLayers = 16, kTrSlots = 32;
+// waits, 10 the kernel's start (layer 0), 11 the head's end (layer 0).
+constexpr int kTrWgs = 256, kTrLayers = 16, kTrSlots = 12;
 __device__ unsigned long long g_gpt2_trace[kTrWgs][kTrLayers][kTrSlots];
-__device__ unsigned long long g_gpt2_xt[kTrWgs][3];
-#define SH_XCHG_TRACE(t_enter, t_first, polls)                                        \
-  do {                                                                                 \
-    if (threadIdx.x == 0 && blockIdx.x < kTrWgs) {                                    \
-      g_gpt2_xt[blockIdx.x][0] = t_enter;                                             \
-      g_gpt2_xt[blockIdx.x][1] = t_first;                                             \
-      g_gpt2_xt[blockIdx.x][2] = (unsigned long long)(polls);                         \
-    }                                                                                  \
-  } while (0)
 #define SH_G2MARK(l, slot)                                                              \
   do {                                                                                   \
     if (threadIdx.x == 0 && blockIdx.x < kTrWgs && (l) < kTrLayers)                     \
       g_gpt2_trace[blockIdx.x][l][slot] = wall_clock64();                               \
   } while (0)
-#define SH_G2WAIT(l, p)                                                                 \
-  do {                                                                                   \
-    if (threadIdx.x == 0 && blockIdx.x < kTrWgs && (l) < kTrLayers) {                   \
-      g_gpt2_trace[blockIdx.x][l][5 + (p)] = wall_clock64();                            \
-      for (int q_ = 0; q_ < 3; q_++)                                                    \
-        g_gpt2_trace[blockIdx.x][l][12 + 3 * (p) + q_] = g_gpt2_xt[blockIdx.x][q_];     \
-    }                                                                                    \
-  } while (0)
-// after a phase's cell stores: waits for their acknowledgement (every thread)
-#define SH_G2ACK(l, p)                                                                  \
-  do {                                                                                   \
-    __builtin_amdgcn_s_waitcnt(0x0F70);                                                 \
-    SH_G2MARK(l, 27 + (p));                                                             \
-  } while (0)
 #else
 #define SH_G2MARK(l, slot) ((void)0)
-#define SH_G2WAIT(l, p) ((void)0)
-#define SH_G2ACK(l, p) ((void)0)
 #endif
+#define SH_G2WAIT(l, p) SH_G2MARK(l, 5 + (p))
 
 #include "exchange.h"
 #include "llm.h"
@@ -123,13 +97,14 @@ struct Lds {
 // ---- GEMV items ----------------------------------------------------------------
 
 // This wave's quarter of K for 16-row tile g of an fp16 tiled matrix with K
-// columns (1 KiB tiles of 16 rows x 32 K): kL 16-byte loads per lane.
-template <int kL>
+// columns (1 KiB tiles of 16 rows x 32 K): kL 16-byte loads per lane (those
+// of u in [kU0, kU1)).
+template <int kL, int kU0 = 0, int kU1 = kL>
 __device__ __forceinline__ void load_weights(u32x4 (&w)[kL], const SH_XGLOBAL uint16_t *W, int K, int g) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int tiles = K >> 5;
 #pragma unroll
-  for (int u = 0; u < kL; u++) {
+  for (int u = kU0; u < kU1; u++) {
     const size_t tile = (size_t)g * tiles + wave * kL + u;
     w[u] = __builtin_nontemporal_load(reinterpret_cast<const SH_XGLOBAL u32x4 *>(
         reinterpret_cast<const SH_XGLOBAL uint8_t *>(W) + tile * 1024 + (size_t)lane * 16));
@@ -294,7 +269,6 @@ __device__ __forceinline__ bool qkv_item(const Gpt2Args &a, const LayerP &P, int
   f32x4 acc = reduce_waves(mfma_weights<kLH>(w, S.xs), S);
   if (threadIdx.x < 16) cst(a.qkvc, (size_t)i * 16 + col, bits_of(acc[0] + bias), tag_of(ep, l));
   SH_G2MARK(l, 0);
-  SH_G2ACK(l, 0);
   return true;
 }
 
@@ -425,7 +399,6 @@ __device__ __forceinline__ bool attn_item(const Gpt2Args &a, const LayerP &P, in
     cst(a.partc, pp + kHd + 1, bits_of(lsum), tag);
   }
   SH_G2MARK(l, 1);
-  SH_G2ACK(l, 1);
   return true;
 }
 
@@ -509,7 +482,6 @@ __device__ __forceinline__ bool o_item(const Gpt2Args &a, const LayerP &P, int l
   }
   asm volatile("" ::"v"(rc));  // the residual load retires here in every thread
   SH_G2MARK(l, 2);
-  SH_G2ACK(l, 2);
   return true;
 }
 
@@ -533,7 +505,6 @@ __device__ __forceinline__ bool fc_item(const Gpt2Args &a, const LayerP &P, int 
       cst(a.actc, ((size_t)i * 16 + col) / 2, hv | (nb << 16), tag_of(ep, l));
   }
   SH_G2MARK(l, 3);
-  SH_G2ACK(l, 3);
   return true;
 }
 
@@ -560,7 +531,6 @@ __device__ __forceinline__ bool proj_item(const Gpt2Args &a, const LayerP &P, in
   }
   asm volatile("" ::"v"(rc));
   SH_G2MARK(l, 4);
-  SH_G2ACK(l, 4);
   return true;
 }
 
@@ -648,13 +618,17 @@ __global__ __launch_bounds__(kT, 1) void gpt2_layers_kernel(const Gpt2Args a) {
       if (next && !hasD) attn_prefetch(a, layer_p(a, l + 1), bi, L, kv);
     }
     // Workgroups with O and proj items request the proj weights (96 KiB at
-    // GPT-2 small) before the O item and the next QKV weights after it: the
-    // windows before the O, proj and next QKV polls then carry 120, 24 and
-    // 0 KiB of requests (loads complete in issue order; before: 24, 96, 24).
+    // GPT-2 small) and the next QKV weights before the O item: nothing then
+    // stands between the proj and next QKV items' polls and their data
+    // (loads complete in issue order). Measured: 24 / 96 / 24 KiB before the
+    // O / proj / next QKV polls (proj weights at the proj item) 5,014
+    // tok/s; 120 / 24 / 0 KiB 5,173; 72 / 72 / 0 KiB 5,095.
     u32x4 wp[kLI];
-    if (w < nC) load_weights<kLI>(wp, P.wproj, a.inter, w);
+    if (w < nC) {
+      load_weights<kLI>(wp, P.wproj, a.inter, w);
+      if (next && w < nA) load_weights<kLH>(wa, layer_p(a, l + 1).wqkv, a.H, w);
+    }
     if (w < nC && !o_item<kLH>(a, P, l, w, ep, L, S)) return;
-    if (w < nC && next && w < nA) load_weights<kLH>(wa, layer_p(a, l + 1).wqkv, a.H, w);
     if (hasD) {
       if (!fc_item<kLH>(a, P, l, w - nC, ep, S)) return;
       if (next) {
