@@ -35,8 +35,10 @@
 #ifdef SH_GPT2_TRACE
 // Diagnostic builds only (-DSH_GPT2_TRACE): wall-clock marks per workgroup
 // and layer: slots 0..4 the ends of its A..E items, 5..9 the ends of their
-// waits, 10 the kernel's start (layer 0), 11 the head's end (layer 0).
-constexpr int kTrWgs = 256, kTrLayers = 16, kTrSlots = 12;
+// waits, 10 the kernel's start (layer 0), 11 the head's end (layer 0),
+// 12..15 the ends of the attention item's q / k / v staging, scores,
+// softmax and V sums.
+constexpr int kTrWgs = 256, kTrLayers = 16, kTrSlots = 16;
 __device__ unsigned long long g_gpt2_trace[kTrWgs][kTrLayers][kTrSlots];
 #define SH_G2MARK(l, slot)                                                              \
   do {                                                                                   \
@@ -273,9 +275,11 @@ __device__ __forceinline__ bool qkv_item(const Gpt2Args &a, const LayerP &P, int
 }
 
 // K / V rows of attention item (head h, split s), requested ahead of the
-// item: thread t holds K[p0 + t][0..63] and, for dims 8 (t % 8) .., the V
-// rows p0 + t / 8 + 32 j. Positions are clamped to the cached ones (before
-// this step's token, which the item substitutes from its cells).
+// item. Thread t = 4 g + q holds dims 16 q .. 16 q + 15 of the K rows p0 + g
+// + 64 m, m < 4 (k[2 m], k[2 m + 1]: a quarter of each dot product, the
+// four quarters summed across the lane quad), and, for dims 8 (t % 8) ..,
+// the V rows p0 + t / 8 + 32 j. Positions are clamped to the cached ones
+// (before this step's token, which the item substitutes from its cells).
 struct AttnKV {
   u32x4 k[8];
   u32x4 v[kVJ];
@@ -287,10 +291,14 @@ __device__ __forceinline__ void attn_prefetch(const Gpt2Args &a, const LayerP &P
   const int p0 = s * a.chunk, last = max(min(L - 2, p0 + a.chunk - 1), 0);
   const SH_XGLOBAL uint16_t *kb = P.kcache + (size_t)h * a.max_pos * kHd;
   const SH_XGLOBAL uint16_t *vb = P.vcache + (size_t)h * a.max_pos * kHd;
-  const int pk = min(p0 + t, last);
+  const int kq = t & 3, kg = t >> 2;
 #pragma unroll
-  for (int e = 0; e < 8; e++)
-    kv.k[e] = *reinterpret_cast<const SH_XGLOBAL u32x4 *>(kb + (size_t)pk * kHd + 8 * e);
+  for (int m = 0; m < 4; m++) {
+    const int pk = min(p0 + kg + 64 * m, last);
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++)
+      kv.k[2 * m + hh] = *reinterpret_cast<const SH_XGLOBAL u32x4 *>(kb + (size_t)pk * kHd + 16 * kq + 8 * hh);
+  }
   const int d8 = t & 7, pg = t >> 3;
 #pragma unroll
   for (int j = 0; j < kVJ; j++) {
@@ -299,11 +307,21 @@ __device__ __forceinline__ void attn_prefetch(const Gpt2Args &a, const LayerP &P
   }
 }
 
-__device__ __forceinline__ float dot8(const f16x8 k, const float *q) {
-  float s = 0.0f;
-#pragma unroll
-  for (int e = 0; e < 8; e++) s += q[e] * (float)k[e];
-  return s;
+
+// x + x of lane l ^ kX (kX 16 or 32) in every lane: v_permlane16_swap /
+// v_permlane32_swap exchange the odd and even 16-lane rows / the halves of
+// two registers, so on two copies of x their sum is the pair sum. Inline
+// asm with two read-write operands: through the compiler's builtins, the
+// two results of a swap of one value were folded into one (x' + x'). The
+// s_nop covers the wait states between the copy and the swap.
+template <int kX>
+__device__ __forceinline__ float add_lane_swap(float x) {
+  unsigned u = __builtin_bit_cast(unsigned, x), v = u;
+  if (kX == 16)
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(u), "+v"(v));
+  else
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(u), "+v"(v));
+  return __builtin_bit_cast(float, u) + __builtin_bit_cast(float, v);
 }
 
 // B: item = (head h, split s): positions [p0, min(p0 + chunk, L)) of the
@@ -340,55 +358,88 @@ __device__ __forceinline__ bool attn_item(const Gpt2Args &a, const LayerP &P, in
     }
   }
   lds_barrier();
-  // scores: thread t scores position p0 + t
-  float sc = -INFINITY;
-  if (t < np) {
-    const bool fresh = p0 + t == pos;
+  SH_G2MARK(l, 12);
+  // scores: thread t = 4 g + q sums dims 16 q .. 16 q + 15 of positions
+  // g + 64 m, m < 4 (four independent chains, q read from LDS once); the
+  // quad's lanes then add their quarters (DPP), and thread t keeps the
+  // score of position g + 64 q. The new token's K first replaces the cache
+  // copy in the registers of the quad that holds it.
+  const int kq = t & 3, kg = t >> 2;
+  f32x4 qr[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) qr[i] = *reinterpret_cast<const f32x4 *>(&S.q[16 * kq + 4 * i]);
+  const int pn = pos - p0;  // the new token's index in the split (when holds_new)
+  if (holds_new) {          // uniform
+    // selects on every m (a branch per m became a dynamic register index,
+    // which put kv in scratch memory)
+    const u32x4 kn[2] = {*reinterpret_cast<const u32x4 *>(&S.knew[16 * kq]),
+                         *reinterpret_cast<const u32x4 *>(&S.knew[16 * kq + 8])};
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+      const bool hit = kg + 64 * m == pn;
+#pragma unroll
+      for (int hh = 0; hh < 2; hh++) kv.k[2 * m + hh] = hit ? kn[hh] : kv.k[2 * m + hh];
+    }
+  }
+  float s4[4];
+#pragma unroll
+  for (int m = 0; m < 4; m++) {
     float acc = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-      const f16x8 kr = fresh ? *reinterpret_cast<const f16x8 *>(&S.knew[8 * e])
-                             : __builtin_bit_cast(f16x8, kv.k[e]);
-      acc += dot8(kr, &S.q[8 * e]);
+    for (int hh = 0; hh < 2; hh++) {
+      const f16x8 kr = __builtin_bit_cast(f16x8, kv.k[2 * m + hh]);
+#pragma unroll
+      for (int e = 0; e < 8; e++) acc += qr[2 * hh + e / 4][e % 4] * (float)kr[e];
     }
-    sc = acc;
+    s4[m] = acc;
   }
+#pragma unroll
+  for (int m = 0; m < 4; m++) {
+    s4[m] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s4[m]), 0xB1, 0xf, 0xf, false));
+    s4[m] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s4[m]), 0x4E, 0xf, 0xf, false));
+  }
+  const int pi_own = kg + 64 * kq;  // this thread's position in the split
+  float sc = kq == 0 ? s4[0] : kq == 1 ? s4[1] : kq == 2 ? s4[2] : s4[3];
+  sc = pi_own < np ? sc : -INFINITY;
   float m = wave_max_rows(sc);
   if (lane == 0) S.wmax[wave] = m;
   lds_barrier();
+  SH_G2MARK(l, 13);
   m = fmaxf(fmaxf(S.wmax[0], S.wmax[1]), fmaxf(S.wmax[2], S.wmax[3]));
-  const float e = t < np ? expf(sc - m) : 0.0f;
-  S.p[t] = e;
+  const float e = pi_own < np ? expf(sc - m) : 0.0f;
+  S.p[pi_own] = e;
   const float ls = wave_sum_rows(e);
   if (lane == 0) S.wl[wave] = ls;
   lds_barrier();
+  SH_G2MARK(l, 14);
   const float lsum = (S.wl[0] + S.wl[1]) + (S.wl[2] + S.wl[3]);
   // V sums: thread (d8 = t % 8, pg = t / 8) over positions pg + 32 j
+  // (p = 0 past the split's end); the new token's V from LDS
   const int d8 = t & 7, pg = t >> 3;
+  const u32x4 vnw = *reinterpret_cast<const u32x4 *>(&S.vnew[8 * d8]);
   float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int j = 0; j < kVJ; j++) {
     const int pi = pg + 32 * j;
-    if (pi < np) {
-      const float pw = S.p[pi];
-      const f16x8 vr = p0 + pi == pos ? *reinterpret_cast<const f16x8 *>(&S.vnew[8 * d8])
-                                      : __builtin_bit_cast(f16x8, kv.v[j]);
+    const float pw = S.p[pi];
+    const f16x8 vr = __builtin_bit_cast(f16x8, p0 + pi == pos ? vnw : kv.v[j]);
 #pragma unroll
-      for (int q = 0; q < 8; q++) o[q] += pw * (float)vr[q];
-    }
+    for (int q = 0; q < 8; q++) o[q] += pw * (float)vr[q];
   }
   // sum over pg: lanes l, l ^ 8, l ^ 16, l ^ 32 share d8 within a wave
+  // (DPP row_ror:8 within 16-lane rows, then the gfx950 row / half swaps)
 #pragma unroll
   for (int q = 0; q < 8; q++) {
-    o[q] += __shfl_xor(o[q], 8, 64);
-    o[q] += __shfl_xor(o[q], 16, 64);
-    o[q] += __shfl_xor(o[q], 32, 64);
+    o[q] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, o[q]), 0x128, 0xf, 0xf, false));
+    o[q] = add_lane_swap<16>(o[q]);
+    o[q] = add_lane_swap<32>(o[q]);
   }
   if (lane < 8) {
 #pragma unroll
     for (int q = 0; q < 8; q++) S.pv[wave][8 * lane + q] = o[q];
   }
   lds_barrier();
+  SH_G2MARK(l, 15);
   const size_t pp = ((size_t)h * kGpt2Splits + s) * kGpt2PStride;
   if (t < kHd) {
     const float v = (S.pv[0][t] + S.pv[1][t]) + (S.pv[2][t] + S.pv[3][t]);
