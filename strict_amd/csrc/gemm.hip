@@ -2,28 +2,19 @@
 // bf16 output, all row-major. The reference only holds an unused cuBLAS
 // handle for this (Kernel.cs:10-11, :16); the workload is BASELINE configs[2].
 //
-// MFMA kernel (M % 256 == 0, N % 256 == 0, K % 64 == 0, leading dimensions
+// MFMA kernel (M % 256 == 0, N % 256 == 0, K % 32 == 0, leading dimensions
 // multiples of 8 elements, 16-byte aligned operands):
 //  - one 256-thread workgroup per 256 x 256 tile of C; its 4 waves own
 //    128 x 128 quadrants, each a 4 x 4 grid of v_mfma_f32_32x32x16_bf16
 //    accumulators (256 fp32 per lane, held in AGPRs at one wave per SIMD);
-//  - K advances in 64-wide slabs staged in LDS, double buffered (2 x 64 KiB),
-//    software-pipelined: within a slab the fragments of k-step s + 1 are read
-//    while the MFMAs of step s run; the next slab goes out to the other buffer
-//    during steps 2 (A rows) and 3 (B columns), and each half's global loads
-//    for the slab after that are issued as soon as its staging registers are
-//    written out, so they have four k-steps to arrive; one barrier per slab,
-//    before the last four MFMAs, whose shadow covers the next slab's first
-//    fragment reads; scheduling barriers fix the instruction order (one
-//    MFMA, then the memory operations that go with it);
-//  - operands are read with buffer loads: one 32-bit lane offset per operand,
-//    the row and slab steps in the scalar offset (the tile's A rows and all of
-//    B's rows must span < 2 GiB);
-//  - A rows and B columns are stored K-contiguous in LDS (128 B per row), the
-//    16-byte chunk index XOR-swizzled by (row / 2) % 8 so that the 16-lane
-//    phases of ds_read_b128 / ds_write_b128 touch 16 distinct bank groups;
-//  - B arrives row-major (N contiguous): each thread loads an 8(k) x 8(n)
-//    block and transposes it in registers with v_perm before the LDS store;
+//  - the operands go global -> LDS directly (buffer loads with the LDS
+//    destination), in 32-wide K stages, four in flight; within a stage the
+//    fragments of k-step 1 are read under the MFMAs of k-step 0, and the
+//    next stage's first fragments under the last MFMAs, after its
+//    readiness wait and one barrier (details at the kernel);
+//  - A rows are stored K-contiguous in LDS, B as it arrives (N contiguous)
+//    and read through the transposing ds_read_b64_tr_b16; both XOR-swizzled
+//    so that the fragment reads' lane phases touch distinct banks;
 //  - the MFMA is issued as Bt x A so that each lane ends up holding one row
 //    of C with runs of 4 consecutive columns (8-byte bf16 stores);
 //  - tiles are numbered so that each of the 8 XCDs (workgroups are dealt to
@@ -40,13 +31,8 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kBM = 256, kBN = 256, kBK = 64;
+constexpr int kBM = 256, kBN = 256;
 constexpr int kThreads = 256;
-constexpr int kLdsRow = kBK * 2;          // bytes per staged row (64 bf16)
-constexpr int kLdsTile = 256 * kLdsRow;   // 32 KiB per operand slab
-constexpr int kLdsBytes = 4 * kLdsTile;   // 2 buffers x (A, Bt)
-
-__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   uint32_t u = __builtin_bit_cast(uint32_t, f);
@@ -55,10 +41,39 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   return u >> 16;
 }
 
+// ---- MFMA kernel -----------------------------------------------------------
+// The operands go global -> LDS by buffer loads with the LDS destination (no
+// staging registers, no LDS stores): K advances in 32-wide stages, four in
+// flight (128 KiB), each wave issuing 8 of a stage's 32 one-KiB loads. The compiler
+// does not count these loads' LDS writes against later LDS reads, so every
+// stage's readiness is an explicit s_waitcnt vmcnt (this wave's loads of
+// the stage done, the two later stages still in flight) plus s_barrier (the
+// other waves' too), never a full vmcnt(0).
+//  - A stage: 256 rows x 64 B, the 16-byte chunk c of row r stored at
+//    position c ^ ((r / 4) % 4) (16-lane phases of the fragment reads hit
+//    distinct banks); a load's lane l writes position l % 4 of row l / 4
+//    of its 16-row block, so it fetches chunk (l % 4) ^ swizzle.
+//  - B stage: 32 k rows x 512 B (N contiguous, as B is stored), chunk c of
+//    k row r at position c ^ (4 (r % 4)); the MFMA's B fragments (8
+//    consecutive k of one column per lane) come from pairs of transposing
+//    reads (ds_read_b64_tr_b16: within 16 lanes, lane 4 i + q addresses k
+//    row kb + i at column cb + 4 q, and lane j receives column cb + j at
+//    rows kb .. kb + 3), whose 4-row groups the swizzle spreads over the
+//    banks.
+constexpr int kDK = 32;                      // K per stage
+constexpr int kDStages = 4;                  // stages in flight
+constexpr int kDBar = 8;                     // k-step 1 MFMAs before the stage barrier
+constexpr int kDA = kBM * kDK * 2;           // A stage bytes (16 KiB)
+constexpr int kDStage = kDA + kDK * kBN * 2;  // + B (16 KiB)
+constexpr int kDLdsBytes = kDStages * kDStage;
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+#define SH_LDS_AS __attribute__((address_space(3)))
+
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_bf16_mfma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
-                           uint16_t *__restrict__ C, int K, int lda, int ldb, int ldc,
-                           int tiles_m, int tiles_n, int grouped) {
+                          uint16_t *__restrict__ C, int K, int lda, int ldb, int ldc, int tiles_m,
+                          int tiles_n, int grouped) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
   const int ntiles = tiles_m * tiles_n;
@@ -75,64 +90,71 @@ void gemm_bf16_mfma_kernel(const uint16_t *__restrict__ A, const uint16_t *__res
     tn = tile % tiles_n;
   }
 
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
-  // A: rows t/8 + 32i (i < 8), 16-byte chunk t%8 of the 64-wide slab;
-  // B: an 8 x 8 block, k rows 8*(t%8) .. +7, n columns 8*(t/8) .. +7
-  const int a_row = t >> 3, a_chunk = t & 7;
-  const int b_kc = t & 7, b_nc = t >> 3;
-
-  const __amdgpu_buffer_rsrc_t a_rs = __builtin_amdgcn_make_buffer_rsrc(
-      (void *)(A + (size_t)tm * kBM * lda), (short)0, (255 * lda + K) * 2, 0x00020000);
-  const __amdgpu_buffer_rsrc_t b_rs = __builtin_amdgcn_make_buffer_rsrc(
-      (void *)(B + tn * kBN), (short)0, ((K - 1) * ldb + kBN) * 2, 0x00020000);
-  const int a_voff = (a_row * lda + a_chunk * 8) * 2, b_voff = (8 * b_kc * ldb + 8 * b_nc) * 2;
-  u32x4 ra[8], rb[8];
-  auto load_a = [&](int kt, int i) {
-    ra[i] = __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_voff, (32 * i * lda + kt * kBK) * 2, 0);
-  };
-  auto load_b = [&](int kt, int i) {
-    rb[i] = __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff, (kt * kBK + i) * ldb * 2, 0);
-  };
-  auto store_a = [&](uint8_t *buf, int i) {
-    const int r = a_row + 32 * i;
-    *reinterpret_cast<u32x4 *>(buf + r * kLdsRow + swz(r, a_chunk) * 16) = ra[i];
-  };
-  // B's 8 x 8 block transposed: every output column needs all eight staged
-  // rows, so the whole block is permuted before any of its registers is
-  // reloaded
-  u32x4 bt[8];
-  auto transpose_b = [&]() {
+  // this lane's source offsets for the wave's 4 A and 4 B loads of a stage
+  int a_vo[4], b_vo[4];
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const int jj = j ^ (b_nc & 1);
-      const uint32_t sel = (jj & 1) ? 0x07060302u : 0x05040100u;
-      bt[j].x = __builtin_amdgcn_perm(rb[1][jj >> 1], rb[0][jj >> 1], sel);
-      bt[j].y = __builtin_amdgcn_perm(rb[3][jj >> 1], rb[2][jj >> 1], sel);
-      bt[j].z = __builtin_amdgcn_perm(rb[5][jj >> 1], rb[4][jj >> 1], sel);
-      bt[j].w = __builtin_amdgcn_perm(rb[7][jj >> 1], rb[6][jj >> 1], sel);
+  for (int u = 0; u < 4; u++) {
+    const int r = (wave * 4 + u) * 16 + (lane >> 2);
+    a_vo[u] = (r * lda + (((lane & 3) ^ ((r >> 2) & 3)) * 8)) * 2;
+    const int kr = (wave * 4 + u) * 2 + (lane >> 5);
+    b_vo[u] = (kr * ldb + (((lane & 31) ^ (4 * (kr & 3))) * 8)) * 2;
+  }
+  SH_LDS_AS uint8_t *lds3 = (SH_LDS_AS uint8_t *)lds;
+  // the same resources as 4-dword descriptors for the asm (base, stride 0,
+  // size in bytes, the flags make_buffer_rsrc gets above)
+  auto desc = [](const void *base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    return u32x4{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, bytes, 0x00020000u};
+  };
+  const u32x4 a_d = desc(A + (size_t)tm * kBM * lda, (uint32_t)((255 * lda + K) * 2));
+  const u32x4 b_d = desc(B + tn * kBN, (uint32_t)(((K - 1) * ldb + kBN) * 2));
+  const uint32_t lds_base = (uint32_t)(uintptr_t)lds3;
+  // load u (< 8) of stage kt. Inline asm: through the compiler's builtin,
+  // every later LDS read that it could not tell apart from the loads' LDS
+  // writes got a full vmcnt(0) wait, which emptied the pipeline; here the
+  // explicit per-stage waits below are the only ones.
+  auto dma = [&](int kt, int u) {
+    const uint32_t m0 = lds_base + (kt % kDStages) * kDStage + (u < 4 ? 0 : kDA) + (wave * 4 + (u & 3)) * 1024;
+    if (u < 4)
+      asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+                   :: "v"(a_vo[u]), "s"(a_d), "s"(kt * kDK * 2), "{m0}"(m0) : "memory");
+    else
+      asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+                   :: "v"(b_vo[u - 4]), "s"(b_d), "s"(kt * kDK * ldb * 2), "{m0}"(m0) : "memory");
+  };
+
+  // fragments: A q (< 4): rows wm 128 + 32 q + lane % 32, 8 k at chunk
+  // 2 s + lane / 32 of k-step s (16 k); B j (< 4): columns wn 128 + 32 j +
+  // lane % 32, 8 k (two transposing reads of 4)
+  const int fr = lane & 31, fh = lane >> 5;
+  const int a_base = (wm * 128 + fr) * (kDK * 2), a_sw = (fr >> 2) & 3;
+  const int G = lane >> 4, ti = (lane >> 2) & 3, tq = lane & 3;
+  int b_base[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+    b_base[j] = kDA + (8 * (G >> 1) + ti) * (kBN * 2) +
+                (16 * wn + 4 * (j ^ ti) + 2 * (G & 1) + (tq >> 1)) * 16 + (tq & 1) * 8;
+  bf16x8 f[2][8];
+  s16x4 bh[2][4][2];
+  auto read_frag = [&](int fs, const SH_LDS_AS uint8_t *st, int s, int r) {
+    // read r (< 12) of k-step s in the order the MFMAs need them:
+    // A0, B0 (2), B1 (2), B2 (2), B3 (2), A1, A2, A3
+    if (r == 0 || r >= 9) {
+      const int q = r == 0 ? 0 : r - 8;
+      f[fs][q] = *reinterpret_cast<const SH_LDS_AS bf16x8 *>(
+          st + a_base + q * 32 * (kDK * 2) + (((2 * s + fh) ^ a_sw) * 16));
+    } else {
+      const int j = (r - 1) >> 1, h = (r - 1) & 1;
+      bh[fs][j][h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (SH_LDS_AS s16x4 *)(st + b_base[j] + (16 * s + 4 * h) * (kBN * 2)));
     }
   };
-  auto store_b = [&](uint8_t *buf, int j) {
-    const int n = 8 * b_nc + (j ^ (b_nc & 1));
-    *reinterpret_cast<u32x4 *>(buf + kLdsTile + n * kLdsRow + swz(n, b_kc) * 16) = bt[j];
+  auto b_frag = [&](int fs, int j) {
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(bh[fs][j][0], bh[fs][j][1], 0, 1, 2, 3, 4, 5, 6, 7));
   };
-
-  // Fragment q of k-step s: q < 4 is A rows wm*128 + 32 q + (lane % 32), q >= 4
-  // B columns wn*128 + 32 (q - 4) + (lane % 32); 8 k values each, k chunk
-  // 2 s + lane / 32. The row swizzle (row / 2) % 8 only depends on lane % 32.
-  const int frag_row = lane & 31, frag_half = lane >> 5, fsw = (frag_row >> 1) & 7;
-  const int a_off = (wm * 128 + frag_row) * kLdsRow, b_off = kLdsTile + (wn * 128 + frag_row) * kLdsRow;
-  bf16x8 f[2][8];
-  auto read_frag = [&](bf16x8 (&fr)[8], const uint8_t *buf, int s, int q) {
-    const int chunk = ((2 * s + frag_half) ^ fsw) * 16;
-    const int off = q < 4 ? a_off + q * 32 * kLdsRow : b_off + (q - 4) * 32 * kLdsRow;
-    fr[q] = *reinterpret_cast<const bf16x8 *>(buf + off + chunk);
-  };
-  // fragments are read A0, B0, B1, B2, B3, A1, A2, A3: the order the MFMAs
-  // (row-major over the 4 x 4 accumulators) first need them
-  constexpr int kReadOrder[8] = {0, 4, 5, 6, 7, 1, 2, 3};
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -141,91 +163,69 @@ void gemm_bf16_mfma_kernel(const uint16_t *__restrict__ A, const uint16_t *__res
     for (int j = 0; j < 4; j++)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
-  auto mfma = [&](const bf16x8 (&fr)[8], int k) {
+  auto mfma = [&](int fs, int k) {
     const int i = k >> 2, j = k & 3;
-    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr[4 + j], fr[i], acc[i][j], 0, 0, 0);
+    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b_frag(fs, j), f[fs][i], acc[i][j], 0, 0, 0);
   };
 
-  const int ktiles = K / kBK;
-  // prologue: slab 0 into buffer 0, slab 1 requested, step 0 fragments read
+  // this wave's loads of the oldest stage in flight done (8 loads per
+  // stage; the kDStages - 2 later stages may still be in flight)
+  static_assert(kDStages == 4, "stage_wait's count");
+  auto stage_wait = [] { asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); };
+  const int ktiles = K / kDK;
+  // prologue: stages 0 .. kDStages - 2 requested, stage 0 waited for, its first fragments read
 #pragma unroll
-  for (int i = 0; i < 8; i++) load_a(0, i);
+  for (int p = 0; p < kDStages - 1; p++)
 #pragma unroll
-  for (int i = 0; i < 8; i++) load_b(0, i);
+    for (int u = 0; u < 8; u++) dma(min(p, ktiles - 1), u);
+  stage_wait();
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int i = 0; i < 8; i++) store_a(lds, i);
-  transpose_b();
-#pragma unroll
-  for (int j = 0; j < 8; j++) store_b(lds, j);
-  const int k1 = min(1, ktiles - 1);
-#pragma unroll
-  for (int i = 0; i < 8; i++) load_a(k1, i);
-#pragma unroll
-  for (int i = 0; i < 8; i++) load_b(k1, i);
-  __syncthreads();
-#pragma unroll
-  for (int q = 0; q < 8; q++) read_frag(f[0], lds, 0, kReadOrder[q]);
+  for (int r = 0; r < 12; r++) read_frag(0, lds3, 0, r);
 
   for (int kt = 0; kt < ktiles; kt++) {
-    const uint8_t *cur = lds + (kt & 1) * 2 * kLdsTile;
-    uint8_t *nxt = lds + ((kt & 1) ^ 1) * 2 * kLdsTile;
-    // slab after the next one (re-reads the last slab at the end; those
-    // values are never used)
-    const int k2 = min(kt + 2, ktiles - 1);
-    // steps 0 and 1: MFMAs of step s, reads of step s + 1
-#pragma unroll
-    for (int s = 0; s < 2; s++) {
-#pragma unroll
-      for (int k = 0; k < 16; k++) {
-        mfma(f[s & 1], k);
-        if (k < 8) read_frag(f[(s + 1) & 1], cur, s + 1, kReadOrder[k]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    // step 2: reads of step 3, then the A half of the next slab out to LDS
-    // and the A half of the slab after it requested
+    const SH_LDS_AS uint8_t *cur = lds3 + (kt % kDStages) * kDStage;
+    const SH_LDS_AS uint8_t *nxt = lds3 + ((kt + 1) % kDStages) * kDStage;
+    // the stage three ahead goes to the buffer read during the previous
+    // stage (re-reads the last K slab at the end; never read)
+    const int kq = min(kt + kDStages - 1, ktiles - 1);
+    // k-step 0: its MFMAs, the stage's requests and k-step 1's reads
 #pragma unroll
     for (int k = 0; k < 16; k++) {
-      mfma(f[0], k);
-      if (k < 8) {
-        read_frag(f[1], cur, 3, kReadOrder[k]);
-      } else {
-        store_a(nxt, k - 8);
-        load_a(k2, k - 8);
-      }
+      mfma(0, k);
+      if (k < 12) read_frag(1, cur, 1, k);
+      if (k >= 8) dma(kq, k - 8);
       __builtin_amdgcn_sched_barrier(0);
     }
-    // step 3: the B half likewise, then the barrier, then the next slab's
-    // step 0 fragments under the last four MFMAs
-    transpose_b();
+    // k-step 1: kDBar MFMAs, the next stage's readiness, then its first
+    // reads spread over the remaining ones
 #pragma unroll
-    for (int k = 0; k < 12; k++) {
-      mfma(f[1], k);
-      if (k < 8) {
-        store_b(nxt, k);
-        load_b(k2, k);
-      }
+    for (int k = 0; k < kDBar; k++) {
+      mfma(1, k);
       __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes done
+    stage_wait();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int k = 12; k < 16; k++) {
-      mfma(f[1], k);
-      read_frag(f[0], nxt, 0, kReadOrder[2 * (k - 12)]);
-      read_frag(f[0], nxt, 0, kReadOrder[2 * (k - 12) + 1]);
+    for (int k = kDBar; k < 16; k++) {
+      mfma(1, k);
+      constexpr int kPer = (12 + 16 - kDBar - 1) / (16 - kDBar);
+#pragma unroll
+      for (int r = kPer * (k - kDBar); r < kPer * (k - kDBar + 1) && r < 12; r++) read_frag(0, nxt, 0, r);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS write in flight past the end
 
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    const int m = tm * kBM + wm * 128 + i * 32 + frag_row;
+    const int m = tm * kBM + wm * 128 + i * 32 + fr;
     uint16_t *crow = C + (size_t)m * ldc;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const int n0 = tn * kBN + wn * 128 + j * 32 + 4 * frag_half;
+      const int n0 = tn * kBN + wn * 128 + j * 32 + 4 * fh;
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         const uint32_t p0 = f32_to_bf16_bits(acc[i][j][4 * q + 0]) |
@@ -297,7 +297,7 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 bool gemm_bf16_uses_mfma(int M, int N, int K, int lda, int ldb, int ldc, const void *A,
                          const void *B, const void *C) {
-  return M % kBM == 0 && N % kBN == 0 && K % kBK == 0 && K > 0 && lda % 8 == 0 &&
+  return M % kBM == 0 && N % kBN == 0 && K % kDK == 0 && K > 0 && lda % 8 == 0 &&
          ldb % 8 == 0 && ldc % 4 == 0 && aligned16(A) && aligned16(B) &&
          (reinterpret_cast<uintptr_t>(C) & 7) == 0 && (int64_t)kBM * lda * 2 < (1ll << 31) &&
          (int64_t)K * ldb * 2 < (1ll << 31);
@@ -306,14 +306,17 @@ bool gemm_bf16_uses_mfma(int M, int N, int K, int lda, int ldb, int ldc, const v
 hipError_t launch_gemm_bf16(hipStream_t s, const uint16_t *A, const uint16_t *B, uint16_t *C,
                             int M, int N, int K, int lda, int ldb, int ldc) {
   if (gemm_bf16_uses_mfma(M, N, K, lda, ldb, ldc, A, B, C)) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_bf16_mfma_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    const void *kfn = reinterpret_cast<const void *>(&gemm_bf16_mfma_kernel);
+    const int lds_bytes = kDLdsBytes;
+    hipError_t e = hipFuncSetAttribute(kfn, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
     if (e != hipSuccess) return e;
     const int tiles_m = M / kBM, tiles_n = N / kBN;
     const int ntiles = tiles_m * tiles_n;
     const int grouped = (ntiles % 256 == 0 && tiles_m % 4 == 0 && tiles_n % 8 == 0) ? 1 : 0;
-    gemm_bf16_mfma_kernel<<<ntiles, kThreads, kLdsBytes, s>>>(A, B, C, K, lda, ldb, ldc, tiles_m,
-                                                             tiles_n, grouped);
+    void *args[] = {(void *)&A, (void *)&B, (void *)&C, (void *)&K, (void *)&lda, (void *)&ldb, (void *)&ldc,
+                    (void *)&tiles_m, (void *)&tiles_n, (void *)&grouped};
+    e = hipLaunchKernel(kfn, dim3(ntiles), dim3(kThreads), args, lds_bytes, s);
+    if (e != hipSuccess) return e;
   } else {
     dim3 grid((N + kGT - 1) / kGT, (M + kGT - 1) / kGT);
     gemm_bf16_generic_kernel<<<grid, 256, 0, s>>>(A, B, C, M, N, K, lda, ldb, ldc);
