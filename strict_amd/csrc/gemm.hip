@@ -92,6 +92,11 @@ void gemm_bf16_mfma_kernel(const uint16_t *__restrict__ A, const uint16_t *__res
 
   const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int wm = wave >> 1, wn = wave & 1;
+  // C's pointer is used here, so its scalar load completes before the loop:
+  // left pending until the epilogue, it made every wait on the LDS counter
+  // at the loop's top a full lgkmcnt(0) (scalar and LDS results return out
+  // of order), including the fragments the first MFMAs do not need
+  asm volatile("" ::"s"(C));
 
   // this lane's source offsets for the wave's 4 A and 4 B loads of a stage
   int a_vo[4], b_vo[4];
@@ -181,8 +186,14 @@ void gemm_bf16_mfma_kernel(const uint16_t *__restrict__ A, const uint16_t *__res
   stage_wait();
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
+  // in the loop's order (A0 first): the loop's top waits for what both
+  // paths into it have pending, so with A0 read last here, every iteration
+  // began with a full lgkmcnt(0)
 #pragma unroll
-  for (int r = 0; r < 12; r++) read_frag(0, lds3, 0, r);
+  for (int r = 0; r < 12; r++) {
+    read_frag(0, lds3, 0, r);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   for (int kt = 0; kt < ktiles; kt++) {
     const SH_LDS_AS uint8_t *cur = lds3 + (kt % kDStages) * kDStage;

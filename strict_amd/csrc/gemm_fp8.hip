@@ -79,8 +79,13 @@ void gemm_fp8_mfma_kernel(const uint8_t *__restrict__ A, const float *__restrict
     tn = tile % tiles_n;
   }
 
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int wm = wave >> 1, wn = wave & 1;
+  // the epilogue's pointers are used here, so their scalar loads complete
+  // before the loop: left pending, they made every wait on the LDS counter
+  // at the loop's top a full lgkmcnt(0) (scalar and LDS results return out
+  // of order)
+  asm volatile("" ::"s"(sa), "s"(sb), "s"(C));
 
   // rows t/8 + 32i (i < 8), 16-byte chunk t%8 of the slab
   const int g_row = t >> 3, g_chunk = t & 7;
@@ -151,8 +156,14 @@ void gemm_fp8_mfma_kernel(const uint8_t *__restrict__ A, const float *__restrict
 #pragma unroll
   for (int i = 0; i < 8; i++) load_b(k1, i);
   __syncthreads();
+  // in the loop's order: the loop's top waits for what both paths into it
+  // have pending, so reads issued here in another order made every
+  // iteration begin with a full lgkmcnt(0)
 #pragma unroll
-  for (int q = 0; q < 16; q++) read_half(f[0], lds, 0, kReadOrder[q >> 1], q & 1);
+  for (int q = 0; q < 16; q++) {
+    read_half(f[0], lds, 0, kReadOrder[q >> 1], q & 1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   for (int kt = 0; kt < ktiles; kt++) {
     const uint8_t *cur = lds + (kt & 1) * 2 * kLdsTile;
