@@ -5,23 +5,25 @@
 // MFMA kernel (M % 256 == 0, N % 256 == 0, K % 32 == 0, leading dimensions
 // multiples of 8 elements, 16-byte aligned operands):
 //  - one 256-thread workgroup per 256 x 256 tile of C; its 4 waves own
-//    128 x 128 quadrants, each a 4 x 4 grid of v_mfma_f32_32x32x16_bf16
+//    128 x 128 quadrants, each an 8 x 8 grid of v_mfma_f32_16x16x32_bf16
 //    accumulators (256 fp32 per lane, held in AGPRs at one wave per SIMD);
 //  - the operands go global -> LDS directly (buffer loads with the LDS
-//    destination), in 32-wide K stages, four in flight; within a stage the
-//    fragments of k-step 1 are read under the MFMAs of k-step 0, and the
-//    next stage's first fragments under the last MFMAs, after its
+//    destination), in 32-wide K stages, four in flight; the next stage's
+//    fragments are read under a stage's MFMAs, after the next stage's
 //    readiness wait and one barrier (details at the kernel);
 //  - A rows are stored K-contiguous in LDS, B as it arrives (N contiguous)
 //    and read through the transposing ds_read_b64_tr_b16; both XOR-swizzled
 //    so that the fragment reads' lane phases touch distinct banks;
 //  - the MFMA is issued as Bt x A so that each lane ends up holding one row
-//    of C with runs of 4 consecutive columns (8-byte bf16 stores);
+//    of C with runs of 4 consecutive columns (8-byte bf16 stores; 16 lanes
+//    write 32 contiguous bytes of each row);
 //  - tiles are numbered so that each of the 8 XCDs (workgroups are dealt to
 //    XCDs round-robin) computes a 4 x 8 block of tiles, whose A and B slabs
 //    its L2 then shares.
 // Every other shape takes a bounds-checked LDS-tiled fp32 FMA kernel.
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 
 #include "common.h"
 
@@ -60,14 +62,39 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
 //    row kb + i at column cb + 4 q, and lane j receives column cb + j at
 //    rows kb .. kb + 3), whose 4-row groups the swizzle spreads over the
 //    banks.
+//  - A stage is one k-step of v_mfma_f32_16x16x32_bf16: each wave reads 8 A
+//    fragments (16 rows x 32 k, one 16-byte read each) and 8 B fragments
+//    (16 columns x 32 k, two transposing reads each) and issues 8 x 8
+//    MFMAs of 16 cycles. Sustained on every SIMD, this MFMA delivers ~13 %
+//    more flops than v_mfma_f32_32x32x16_bf16 under the power limit (~2.34
+//    against ~2.07 PFLOP/s in register-only loops), and the kernel, which
+//    was power-limited, took ~112 us against ~121-129 us with the 32x32x16
+//    tiles of the same stages (launches interleaved in one process), same
+//    results bit for bit; the clock it then runs at is no longer below
+//    hipBLASLt's.
+//  - Per stage: its 8 loads of the stage three ahead, one every kDGap
+//    MFMAs from the first (issued back to back they measured ~5 % slower:
+//    112 against 115-118 us), the next stage's readiness after MFMA kDBar,
+//    then the next stage's 24 fragment reads one per MFMA (into the other
+//    fragment set; two per MFMA measured ~9 % slower). Five stages in
+//    flight (all 160 KiB of LDS) measured slower than four.
+//  - The MFMAs are inline asm with AGPR accumulator operands: through the
+//    builtin, the 64 four-register accumulators were shuttled between
+//    AGPRs and VGPRs (~180 moves each way per stage pair) and spilled. The
+//    compiler does not see these as MFMAs, so: each accumulator is rewritten
+//    only 63 MFMAs after its previous write (no dependent-MFMA wait needed),
+//    fragment registers are waited for by the load counters like any asm
+//    input, and explicit wait states precede the epilogue's accumulator reads.
 constexpr int kDK = 32;                      // K per stage
 constexpr int kDStages = 4;                  // stages in flight
-constexpr int kDBar = 8;                     // k-step 1 MFMAs before the stage barrier
 constexpr int kDA = kBM * kDK * 2;           // A stage bytes (16 KiB)
 constexpr int kDStage = kDA + kDK * kBN * 2;  // + B (16 KiB)
 constexpr int kDLdsBytes = kDStages * kDStage;
+constexpr int kDBar = 39;                    // MFMAs of a stage before the next stage's readiness wait
+constexpr int kDGap = 4;                     // MFMAs between a stage's loads
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
 #define SH_LDS_AS __attribute__((address_space(3)))
 
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -131,54 +158,57 @@ void gemm_bf16_mfma_kernel(const uint16_t *__restrict__ A, const uint16_t *__res
                    :: "v"(b_vo[u - 4]), "s"(b_d), "s"(kt * kDK * ldb * 2), "{m0}"(m0) : "memory");
   };
 
-  // fragments: A q (< 4): rows wm 128 + 32 q + lane % 32, 8 k at chunk
-  // 2 s + lane / 32 of k-step s (16 k); B j (< 4): columns wn 128 + 32 j +
-  // lane % 32, 8 k (two transposing reads of 4)
-  const int fr = lane & 31, fh = lane >> 5;
-  const int a_base = (wm * 128 + fr) * (kDK * 2), a_sw = (fr >> 2) & 3;
+  // A fragment i (< 8): rows wm 128 + 16 i + lane % 16, k 8 (lane / 16) .. + 7
+  // (chunk lane / 16 of the row, swizzled by the row's (r / 4) % 4 =
+  // (lane % 16) / 4)
+  const int a_base = (wm * 128 + (lane & 15)) * (kDK * 2) + (((lane >> 4) ^ ((lane & 15) >> 2)) * 16);
+  // B fragment j (< 8): columns wn 128 + 16 j + lane % 16, k 8 (lane / 16)
+  // .. + 7 from two transposing reads (k rows + 4 h); lane 4 ti + tq of
+  // 16-lane group G addresses k row 8 G + ti (+ 4 h), columns + 4 tq
   const int G = lane >> 4, ti = (lane >> 2) & 3, tq = lane & 3;
-  int b_base[4];
+  int b_base[8];
 #pragma unroll
-  for (int j = 0; j < 4; j++)
-    b_base[j] = kDA + (8 * (G >> 1) + ti) * (kBN * 2) +
-                (16 * wn + 4 * (j ^ ti) + 2 * (G & 1) + (tq >> 1)) * 16 + (tq & 1) * 8;
-  bf16x8 f[2][8];
-  s16x4 bh[2][4][2];
-  auto read_frag = [&](int fs, const SH_LDS_AS uint8_t *st, int s, int r) {
-    // read r (< 12) of k-step s in the order the MFMAs need them:
-    // A0, B0 (2), B1 (2), B2 (2), B3 (2), A1, A2, A3
-    if (r == 0 || r >= 9) {
-      const int q = r == 0 ? 0 : r - 8;
-      f[fs][q] = *reinterpret_cast<const SH_LDS_AS bf16x8 *>(
-          st + a_base + q * 32 * (kDK * 2) + (((2 * s + fh) ^ a_sw) * 16));
+  for (int j = 0; j < 8; j++)
+    b_base[j] = kDA + (8 * G + ti) * (kBN * 2) + ((16 * wn + 2 * j + (tq >> 1)) ^ (4 * ti)) * 16 + (tq & 1) * 8;
+  bf16x8 fa[2][8];
+  s16x4 fb[2][8][2];
+  auto read_frag = [&](int fs, const SH_LDS_AS uint8_t *st, int r) {
+    // read r (< 24) of a stage in the order the MFMAs need them: A0, B0
+    // (2), B1 (2), .. B7 (2), A1 .. A7
+    if (r == 0 || r >= 17) {
+      const int i = r == 0 ? 0 : r - 16;
+      fa[fs][i] = *reinterpret_cast<const SH_LDS_AS bf16x8 *>(st + a_base + i * 16 * (kDK * 2));
     } else {
       const int j = (r - 1) >> 1, h = (r - 1) & 1;
-      bh[fs][j][h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (SH_LDS_AS s16x4 *)(st + b_base[j] + (16 * s + 4 * h) * (kBN * 2)));
+      fb[fs][j][h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (SH_LDS_AS s16x4 *)(st + b_base[j] + 4 * h * (kBN * 2)));
     }
   };
-  auto b_frag = [&](int fs, int j) {
-    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(bh[fs][j][0], bh[fs][j][1], 0, 1, 2, 3, 4, 5, 6, 7));
-  };
 
-  f32x16 acc[4][4];
+  f32x4v acc[8][8];
 #pragma unroll
-  for (int i = 0; i < 4; i++)
+  for (int i = 0; i < 8; i++)
 #pragma unroll
-    for (int j = 0; j < 4; j++)
+    for (int j = 0; j < 8; j++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+      for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0f;
+  // MFMA k (< 64) of a stage: accumulator (k / 8, k % 8), issued as Bt x A
+  // so that each lane ends up holding row lane % 16 of the 16 x 16 block,
+  // columns 4 (lane / 16) .. + 3 (8-byte bf16 stores)
   auto mfma = [&](int fs, int k) {
-    const int i = k >> 2, j = k & 3;
-    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b_frag(fs, j), f[fs][i], acc[i][j], 0, 0, 0);
+    const int i = k >> 3, j = k & 7;
+    const bf16x8 b = __builtin_bit_cast(
+        bf16x8, __builtin_shufflevector(fb[fs][j][0], fb[fs][j][1], 0, 1, 2, 3, 4, 5, 6, 7));
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc[i][j]) : "v"(b), "v"(fa[fs][i]));
   };
 
   // this wave's loads of the oldest stage in flight done (8 loads per
   // stage; the kDStages - 2 later stages may still be in flight)
   static_assert(kDStages == 4, "stage_wait's count");
+  static_assert(7 * kDGap < kDBar && 24 <= 63 - kDBar, "a stage's loads precede the wait; all reads fit");
   auto stage_wait = [] { asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); };
   const int ktiles = K / kDK;
-  // prologue: stages 0 .. kDStages - 2 requested, stage 0 waited for, its first fragments read
+  // prologue: stages 0 .. kDStages - 2 requested, stage 0 waited for, its fragments read
 #pragma unroll
   for (int p = 0; p < kDStages - 1; p++)
 #pragma unroll
@@ -187,64 +217,55 @@ void gemm_bf16_mfma_kernel(const uint16_t *__restrict__ A, const uint16_t *__res
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
   // in the loop's order (A0 first): the loop's top waits for what both
-  // paths into it have pending, so with A0 read last here, every iteration
-  // began with a full lgkmcnt(0)
+  // paths into it have pending, so reads issued here in another order
+  // made every iteration begin with a full wait
 #pragma unroll
-  for (int r = 0; r < 12; r++) {
-    read_frag(0, lds3, 0, r);
+  for (int r = 0; r < 24; r++) {
+    read_frag(0, lds3, r);
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  for (int kt = 0; kt < ktiles; kt++) {
-    const SH_LDS_AS uint8_t *cur = lds3 + (kt % kDStages) * kDStage;
+  // stage kt on fragment set kCur: its MFMAs; the loads of stage kt + 3
+  // into the buffer stage kt - 1 used (every wave has read that one: each
+  // is past the previous stage's barrier); after MFMA kDBar, stage kt + 1's
+  // readiness, then its fragments into the other set (re-reads the last
+  // stage past the end; never used)
+  auto stage = [&](auto cur_c, int kt) {
+    constexpr int kCur = decltype(cur_c)::value;
     const SH_LDS_AS uint8_t *nxt = lds3 + ((kt + 1) % kDStages) * kDStage;
-    // the stage three ahead goes to the buffer read during the previous
-    // stage (re-reads the last K slab at the end; never read)
     const int kq = min(kt + kDStages - 1, ktiles - 1);
-    // k-step 0: its MFMAs, the stage's requests and k-step 1's reads
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
-      mfma(0, k);
-      if (k < 12) read_frag(1, cur, 1, k);
-      if (k >= 8) dma(kq, k - 8);
+    for (int k = 0; k < 64; k++) {
+      mfma(kCur, k);
+      if (k % kDGap == 0 && k / kDGap < 8) dma(kq, k / kDGap);
+      if (k == kDBar) {
+        stage_wait();
+        __builtin_amdgcn_s_barrier();
+      }
+      if (k > kDBar && k - kDBar - 1 < 24) read_frag(kCur ^ 1, nxt, k - kDBar - 1);
       __builtin_amdgcn_sched_barrier(0);
     }
-    // k-step 1: kDBar MFMAs, the next stage's readiness, then its first
-    // reads spread over the remaining ones
-#pragma unroll
-    for (int k = 0; k < kDBar; k++) {
-      mfma(1, k);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    stage_wait();
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int k = kDBar; k < 16; k++) {
-      mfma(1, k);
-      constexpr int kPer = (12 + 16 - kDBar - 1) / (16 - kDBar);
-#pragma unroll
-      for (int r = kPer * (k - kDBar); r < kPer * (k - kDBar + 1) && r < 12; r++) read_frag(0, nxt, 0, r);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+  };
+  int kt = 0;
+  for (; kt + 1 < ktiles; kt += 2) {
+    stage(std::integral_constant<int, 0>{}, kt);
+    stage(std::integral_constant<int, 1>{}, kt + 1);
   }
+  if (kt < ktiles) stage(std::integral_constant<int, 0>{}, kt);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS write in flight past the end
+  // the MFMAs are asm: the wait states before the accumulators are read
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int m = tm * kBM + wm * 128 + i * 32 + fr;
+  for (int i = 0; i < 8; i++) {
+    const int m = tm * kBM + wm * 128 + i * 16 + (lane & 15);
     uint16_t *crow = C + (size_t)m * ldc;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int n0 = tn * kBN + wn * 128 + j * 32 + 4 * fh;
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const uint32_t p0 = f32_to_bf16_bits(acc[i][j][4 * q + 0]) |
-                            (f32_to_bf16_bits(acc[i][j][4 * q + 1]) << 16);
-        const uint32_t p1 = f32_to_bf16_bits(acc[i][j][4 * q + 2]) |
-                            (f32_to_bf16_bits(acc[i][j][4 * q + 3]) << 16);
-        *reinterpret_cast<u32x2 *>(crow + n0 + 8 * q) = u32x2{p0, p1};
-      }
+    for (int j = 0; j < 8; j++) {
+      const int n0 = tn * kBN + wn * 128 + j * 16 + 4 * (lane >> 4);
+      const uint32_t p0 = f32_to_bf16_bits(acc[i][j][0]) | (f32_to_bf16_bits(acc[i][j][1]) << 16);
+      const uint32_t p1 = f32_to_bf16_bits(acc[i][j][2]) | (f32_to_bf16_bits(acc[i][j][3]) << 16);
+      *reinterpret_cast<u32x2 *>(crow + n0) = u32x2{p0, p1};
     }
   }
 }

@@ -60,7 +60,8 @@ def test_gemm_4096_config(ctx):
 
 
 @pytest.mark.parametrize("m,n,k", [(256, 256, 64), (512, 768, 320), (768, 512, 4096),
-                                   (1024, 2048, 128)])
+                                   (1024, 2048, 128), (256, 512, 32), (512, 256, 96),
+                                   (256, 256, 160)])
 def test_gemm_mfma_shapes(ctx, m, n, k):
     a, b = _bf16_operands(m, n, k, seed=m + n + k)
     c = _run(ctx, a, b, m, n, k)
