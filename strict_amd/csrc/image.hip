@@ -102,10 +102,15 @@ __global__ __launch_bounds__(kBlock) void brightness_byte_kernel(const uint8_t *
 // ---------------------------------------------------------------------------
 
 constexpr int kStripPx = 256;  // 64 lanes x 4 pixels
-// threads per workgroup of the streaming blur (consecutive waves take
-// consecutive strips of a band; 512 and 1024, a whole band per workgroup,
-// measured the same)
-constexpr int kBlurBlock = 256;
+// threads per workgroup of the streaming blur: consecutive waves take
+// consecutive strips of a band, so 8 waves on one CU sweep half of a band's
+// 16 KiB rows together. Against 256 threads, launches interleaved in one
+// process over 1 GiB of rotating buffers: 26.05 against 26.6 us (fused 26.4
+// against 26.9); 1024 (a whole band per CU) 27.2, 64 and 128 27.2-27.5. A
+// copy with the same rows, bands and sweep directions and no arithmetic
+// took 24.7 (512) and 26.2 us (256), a flat copy of the same bytes 22.5 us:
+// the gap to the copy is this access pattern, not the arithmetic.
+constexpr int kBlurBlock = 512;
 
 // SWAR brightness on packed RGBA words (direct kernel and byte paths).
 struct Brightness {
