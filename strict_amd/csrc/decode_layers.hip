@@ -172,7 +172,7 @@ __device__ __forceinline__ bool finish_cell(const LayersArgs &a, const uint64_t 
 }
 
 #ifdef SH_DECODE_TRACE
-constexpr int kTraceWgs = 256, kTraceLayers = 32, kTraceSlots = 16;
+constexpr int kTraceWgs = 256, kTraceLayers = 32, kTraceSlots = 24;
 #endif
 
 // Small LDS words after the phase areas.
@@ -236,7 +236,10 @@ __device__ __forceinline__ bool waits_ok(const LayersArgs &a, bool ok, Misc *mis
 // end (odd slots), the end of its wait (10..14) and the merge end (15); tr[1]
 // holds marks inside items: QKV 0..3 (staged, MFMA, reduced, stored), down
 // 4..7, attention 8..13 (q/k/v polled, RoPE, scores, softmax, V sums,
-// stored), merge 14..15 (polled, stored).
+// stored), merge 14..15 (polled, stored), and the end of each phase's items
+// on this workgroup (all of them, not only the first): 16 QKV, 17
+// attention, 18 merge, 19 O, 20 gate/up, 21 down; 22 an attention item's
+// start (with 8..13, the workgroup's last item's).
 __device__ unsigned long long g_decode_trace[2][kTraceWgs][kTraceLayers][kTraceSlots];
 __device__ __forceinline__ void trace_mark(Misc *misc, int set, int l, int slot) {
   if (threadIdx.x == 0 && l < kTraceLayers) misc->tr[set][l][slot] = wall_clock64();
@@ -784,6 +787,7 @@ __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, 
   static_assert((kG + 2) * kD / 2 <= kT, "one pair of q / k / v cells per thread");
   static_assert(kG <= 4, "MFMA rows 0..3 of lanes 0..15 hold the heads");
   AttnLds<kG> &S = *reinterpret_cast<AttnLds<kG> *>(smem);
+  SH_MARK(misc, l, 22);
   const int splits = a.splits, kvn = a.kv_heads;
   const int s = item % splits, kvh = (item / splits) % kvn, b = item / (splits * kvn);
   // wave through readfirstlane: the compiler then treats conditions on it
@@ -1245,6 +1249,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
           return true;
         }))
       return;
+    SH_MARK(misc, l, 16);
     if (!for_items<kOne>(w, nB, G, [&](int i) {
           if (i != w) attn_prefetch(a, P, i, kv);
           if (i == w) SH_TRACE(misc, l, 2);
@@ -1253,12 +1258,14 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
           return true;
         }))
       return;
+    SH_MARK(misc, l, 17);
     if (!for_items<kOne>(m0, nM, G, [&](int j) {
           if (!merge_item<kSP>(a, l, j, ep, smem, misc)) return false;
           if (j == m0) SH_TRACE(misc, l, 15);
           return true;
         }))
       return;
+    SH_MARK(misc, l, 18);
     // O, gate/up and down items request their weights when they start: at
     // batch 1 each workgroup's previous item is then a phase or more behind
     // Workgroups with an O item request their down item's weights before
@@ -1274,6 +1281,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
           return true;
         }))
       return;
+    SH_MARK(misc, l, 19);
     // The next layer's K / V and QKV weights: on workgroups with an O item
     // while the gate/up items run, on the others after their gate/up item.
     // Loads complete in issue order, and a wave also stalls at issuing a
@@ -1294,6 +1302,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
           return true;
         }))
       return;
+    SH_MARK(misc, l, 20);
     if (!hasC && next) {
       if (w < nB) attn_prefetch(a, layer_g(a, l + 1), w, kv);
       if (w < nA) load_weights<kLA, 1>(wa, layer_g(a, l + 1).wqkv, H, w);
@@ -1306,6 +1315,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
           return true;
         }))
       return;
+    SH_MARK(misc, l, 21);
   }
   if (a.head_on && !head_phase<kLA, kRows>(a, ep, lds)) return;
 #ifdef SH_DECODE_TRACE

@@ -666,7 +666,7 @@ SH_API int sh_debug_gpt2_trace(void *dst, size_t bytes) {
 
 #ifdef SH_DECODE_TRACE
 // Diagnostic builds only (-DSH_DECODE_TRACE): the decode-layers kernel's
-// per-workgroup phase timeline of the last step, [256][32][16] wall-clock ticks.
+// per-workgroup phase timeline of the last step, [2][256][32][24] wall-clock ticks.
 SH_API int sh_debug_decode_trace(void *dst, size_t bytes) {
   SH_HIP_TRY(decode_layers_trace(dst, bytes));
   return SH_OK;
