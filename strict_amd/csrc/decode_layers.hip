@@ -774,16 +774,32 @@ __device__ __forceinline__ void attn_prefetch(const LayersArgs &a, const LayerG 
   attn_load_v(a, P.vcache + kv_row * kD * a.vt_stride, p0, split_end_v(a, s), kv);
 }
 
+// The new token's k (wave 2) or v (wave 3) values e0, e0 + 1 into the
+// cache: K row `pos`, V^T column `pos`.
+__device__ __forceinline__ void append_new(const LayersArgs &a, SH_GLOBAL uint16_t *kb, SH_GLOBAL uint16_t *vtb,
+                                           int pos, int wave, int e0, _Float16 x0, _Float16 x1) {
+  const uint16_t u0 = __builtin_bit_cast(uint16_t, x0), u1 = __builtin_bit_cast(uint16_t, x1);
+  if (wave == 2) {
+    *reinterpret_cast<SH_GLOBAL uint32_t *>(kb + (size_t)pos * kD + e0) = (uint32_t)u0 | ((uint32_t)u1 << 16);
+  } else {
+    vtb[(size_t)e0 * a.vt_stride + pos] = u0;
+    vtb[(size_t)(e0 + 1) * a.vt_stride + pos] = u1;
+  }
+}
+
 // B: item = (b, KV head, split), its first K / V^T block requested by
 // attn_prefetch. Scores positions [p0, p0 + chunk) of the context for the
 // kG query heads of the KV head (Qwen3: RMSNorm of q and of the new k over
 // the head, RoPE rotate-half at this step's position; the split holding it
 // appends the new k / v to the cache) and writes the partial (unnormalised
 // V sum, max, sum) of each head as cells. Splits past the context write
-// nothing.
+// nothing. With `reuse`, the workgroup's previous item was the split
+// before this one of the same (row, KV head): its normed, rotated q and new
+// k / v are still in LDS, so this item neither polls the cells nor
+// normalises again (the values, and so the arithmetic, are the same).
 template <int kG>
 __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, int l, int item, unsigned ep,
-                          uint8_t *smem, Misc *misc, AttnKV &kv) {
+                          uint8_t *smem, Misc *misc, AttnKV &kv, bool reuse) {
   static_assert((kG + 2) * kD / 2 <= kT, "one pair of q / k / v cells per thread");
   static_assert(kG <= 4, "MFMA rows 0..3 of lanes 0..15 hold the heads");
   AttnLds<kG> &S = *reinterpret_cast<AttnLds<kG> *>(smem);
@@ -805,6 +821,8 @@ __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, 
   if (s >= active || cap <= 0 || L > a.max_pos) return true;  // uniform
   const int h0 = kvh * kG;
   const unsigned tag = tag_of(ep, l);
+  const int p1 = min(L, p0 + chunk), np = p1 - p0, pos = L - 1;
+  const bool holds_new = p1 == L;  // this split holds the new token (S.knew / S.vnew)
   // Each wave holds one head as a pair of cells per lane: waves 0 and 1 the
   // query heads h0 and h0 + 1, wave 2 the new k, wave 3 the new v; lane j
   // values e0 = 2 j and 2 j + 1. The RMSNorm of a head is a wave sum, and
@@ -812,56 +830,52 @@ __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, 
   // This step's norm gains and RoPE factors are requested before the wait.
   static_assert(kG == 2 && (kG + 2) * kD / 2 == kT, "one head per wave");
   const int e0 = 2 * lane, fe = e0 & (kD / 2 - 1);
-  const SH_GLOBAL float *gain = wave == 2 ? P.k_norm : P.q_norm;
   typedef float f32x2 __attribute__((ext_vector_type(2)));
-  const f32x2 g = *reinterpret_cast<const SH_GLOBAL f32x2 *>(gain + e0);
-  const f32x2 cs = *reinterpret_cast<const SH_GLOBAL f32x2 *>(gbl(a.rope) + (size_t)b * kD + fe);
-  const f32x2 sn = *reinterpret_cast<const SH_GLOBAL f32x2 *>(gbl(a.rope) + (size_t)b * kD + kD / 2 + fe);
-  float v0, v1;
-  {
-    const size_t qrow = (size_t)b * a.qkv_n;
-    size_t cell;
-    if (wave < 2) cell = qrow + (size_t)(h0 + wave) * kD + e0;
-    else if (wave == 2) cell = qrow + (size_t)a.heads * kD + kvh * kD + e0;
-    else cell = qrow + (size_t)(a.heads + kvn) * kD + kvh * kD + e0;
-    uint64_t cv[2];
-    const bool ok = spin_cells(a, a.qkvc, [&](int k) { return cell + k; }, 3ull, tag, cv);
-    if (!waits_ok(a, ok, misc)) return false;
-    SH_MARK(misc, l, 8);
-    v0 = cell_f32(cv[0]);
-    v1 = cell_f32(cv[1]);
-  }
-  const int p1 = min(L, p0 + chunk), np = p1 - p0, pos = L - 1;
-  const bool holds_new = p1 == L;  // this split holds the new token (S.knew / S.vnew)
-  if (wave < 3) {  // q heads and k: RMSNorm over the head, then RoPE
-    const float ss = wave_sum_rows(v0 * v0 + v1 * v1);
-    const float inv = 1.0f / sqrtf(ss / kD + a.eps);
-    v0 = v0 * inv * g.x;
-    v1 = v1 * inv * g.y;
-    const float o0 = __shfl_xor(v0, 32, 64), o1 = __shfl_xor(v1, 32, 64);
-    if (lane < 32) {
-      v0 = v0 * cs.x - o0 * sn.x;
-      v1 = v1 * cs.y - o1 * sn.y;
-    } else {
-      v0 = v0 * cs.x + o0 * sn.x;
-      v1 = v1 * cs.y + o1 * sn.y;
+  if (!reuse) {
+    const SH_GLOBAL float *gain = wave == 2 ? P.k_norm : P.q_norm;
+    const f32x2 g = *reinterpret_cast<const SH_GLOBAL f32x2 *>(gain + e0);
+    const f32x2 cs = *reinterpret_cast<const SH_GLOBAL f32x2 *>(gbl(a.rope) + (size_t)b * kD + fe);
+    const f32x2 sn = *reinterpret_cast<const SH_GLOBAL f32x2 *>(gbl(a.rope) + (size_t)b * kD + kD / 2 + fe);
+    float v0, v1;
+    {
+      const size_t qrow = (size_t)b * a.qkv_n;
+      size_t cell;
+      if (wave < 2) cell = qrow + (size_t)(h0 + wave) * kD + e0;
+      else if (wave == 2) cell = qrow + (size_t)a.heads * kD + kvh * kD + e0;
+      else cell = qrow + (size_t)(a.heads + kvn) * kD + kvh * kD + e0;
+      uint64_t cv[2];
+      const bool ok = spin_cells(a, a.qkvc, [&](int k) { return cell + k; }, 3ull, tag, cv);
+      if (!waits_ok(a, ok, misc)) return false;
+      SH_MARK(misc, l, 8);
+      v0 = cell_f32(cv[0]);
+      v1 = cell_f32(cv[1]);
     }
-  }
-  if (wave < 2) {
-    *reinterpret_cast<f32x2 *>(&S.qs[wave][e0]) = f32x2{v0 * a.scale, v1 * a.scale};
-  } else if (holds_new) {
-    const _Float16 h0v = (_Float16)v0, h1v = (_Float16)v1;
-    const uint16_t u0 = __builtin_bit_cast(uint16_t, h0v), u1 = __builtin_bit_cast(uint16_t, h1v);
-    if (wave == 2) {
-      S.knew[e0] = h0v;
-      S.knew[e0 + 1] = h1v;
-      *reinterpret_cast<SH_GLOBAL uint32_t *>(kb + (size_t)pos * kD + e0) = (uint32_t)u0 | ((uint32_t)u1 << 16);
-    } else {
-      S.vnew[e0] = h0v;
-      S.vnew[e0 + 1] = h1v;
-      vtb[(size_t)e0 * a.vt_stride + pos] = u0;
-      vtb[(size_t)(e0 + 1) * a.vt_stride + pos] = u1;
+    if (wave < 3) {  // q heads and k: RMSNorm over the head, then RoPE
+      const float ss = wave_sum_rows(v0 * v0 + v1 * v1);
+      const float inv = 1.0f / sqrtf(ss / kD + a.eps);
+      v0 = v0 * inv * g.x;
+      v1 = v1 * inv * g.y;
+      const float o0 = __shfl_xor(v0, 32, 64), o1 = __shfl_xor(v1, 32, 64);
+      if (lane < 32) {
+        v0 = v0 * cs.x - o0 * sn.x;
+        v1 = v1 * cs.y - o1 * sn.y;
+      } else {
+        v0 = v0 * cs.x + o0 * sn.x;
+        v1 = v1 * cs.y + o1 * sn.y;
+      }
     }
+    if (wave < 2) {
+      *reinterpret_cast<f32x2 *>(&S.qs[wave][e0]) = f32x2{v0 * a.scale, v1 * a.scale};
+    } else {  // the new k / v, kept for the run's split that holds the new token
+      const _Float16 h0v = (_Float16)v0, h1v = (_Float16)v1;
+      _Float16 *nw = wave == 2 ? S.knew : S.vnew;
+      nw[e0] = h0v;
+      nw[e0 + 1] = h1v;
+      if (holds_new) append_new(a, kb, vtb, pos, wave, e0, h0v, h1v);
+    }
+  } else if (holds_new && wave >= 2) {
+    const _Float16 *nw = wave == 2 ? S.knew : S.vnew;
+    append_new(a, kb, vtb, pos, wave, e0, nw[e0], nw[e0 + 1]);
   }
   lds_barrier();
   SH_MARK(misc, l, 9);
@@ -1209,6 +1223,18 @@ __device__ __forceinline__ bool for_items(int first, int n, int G, F &&f) {
   }
 }
 
+// Items first .. end - 1 in order (kOne: at most one).
+template <bool kOne, typename F>
+__device__ __forceinline__ bool for_run(int first, int end, F &&f) {
+  if constexpr (kOne) {
+    return first < end ? f(first) : true;
+  } else {
+    for (int i = first; i < end; i++)
+      if (!f(i)) return false;
+    return true;
+  }
+}
+
 template <int kG, int kLA, int kLC, int kLD, int kLE, int kSP, int kRows, bool kOne>
 __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -1234,10 +1260,15 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
   const int d0 = (w + G - nC % G) % G;  // this workgroup's first gate/up item
   const int m0 = G - 1 - w;             // its first merge item
   const bool hasC = w < nC;
+  // attention items: workgroup w runs items [bA, eA), one at batch 1; at
+  // larger batches a contiguous run, i.e. consecutive splits of one (row, KV
+  // head), whose items after the first reuse its q / k / v preparation
+  const int bA = kOne ? w : (int)((int64_t)w * nB / G);
+  const int eA = kOne ? min(w + 1, nB) : (int)((int64_t)(w + 1) * nB / G);
   AttnKV kv;
   u32x4 wa[kLA][1];  // this workgroup's first QKV item's weights
   if (w < nA) load_weights<kLA, 1>(wa, layer_g(a, 0).wqkv, H, w);
-  if (w < nB) attn_prefetch(a, layer_g(a, 0), w, kv);
+  if (bA < eA) attn_prefetch(a, layer_g(a, 0), bA, kv);
   for (int l = 0; l < a.n_layers; l++) {
     const LayerG P = layer_g(a, l);
     const bool next = l + 1 < a.n_layers;
@@ -1250,11 +1281,12 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
         }))
       return;
     SH_MARK(misc, l, 16);
-    if (!for_items<kOne>(w, nB, G, [&](int i) {
-          if (i != w) attn_prefetch(a, P, i, kv);
-          if (i == w) SH_TRACE(misc, l, 2);
-          if (!attn_item<kG>(a, P, l, i, ep, smem, misc, kv)) return false;
-          if (i == w) { SH_TRACE(misc, l, 3); SH_TRACE_WAIT(l, 1, misc); }
+    if (!for_run<kOne>(bA, eA, [&](int i) {
+          if (i != bA) attn_prefetch(a, P, i, kv);
+          if (i == bA) SH_TRACE(misc, l, 2);
+          const bool reuse = !kOne && i != bA && i % a.splits != 0;
+          if (!attn_item<kG>(a, P, l, i, ep, smem, misc, kv, reuse)) return false;
+          if (i == bA) { SH_TRACE(misc, l, 3); SH_TRACE_WAIT(l, 1, misc); }
           return true;
         }))
       return;
@@ -1292,7 +1324,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
     // ~2 us; on the workgroups with only a gate/up item, right after the
     // attention item, the burst slowed the merge and O items' polls.)
     if (hasC && next) {
-      if (w < nB) attn_prefetch(a, layer_g(a, l + 1), w, kv);
+      if (bA < eA) attn_prefetch(a, layer_g(a, l + 1), bA, kv);
       if (w < nA) load_weights<kLA, 1>(wa, layer_g(a, l + 1).wqkv, H, w);
     }
     if (!for_items<kOne>(d0, nD, G, [&](int i) {
@@ -1304,7 +1336,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
       return;
     SH_MARK(misc, l, 20);
     if (!hasC && next) {
-      if (w < nB) attn_prefetch(a, layer_g(a, l + 1), w, kv);
+      if (bA < eA) attn_prefetch(a, layer_g(a, l + 1), bA, kv);
       if (w < nA) load_weights<kLA, 1>(wa, layer_g(a, l + 1).wqkv, H, w);
     }
     if (!for_items<kOne>(w, nE, G, [&](int i) {
