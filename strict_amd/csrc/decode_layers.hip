@@ -42,6 +42,7 @@
 // With one wave per SIMD nothing hides an instruction's latency, so the item
 // code avoids runtime integer division, LDS-based lane shuffles in its
 // reductions (DPP within 16-lane rows instead) and single-wave serial loops.
+#include <type_traits>
 #include <hip/hip_runtime.h>
 
 #include "common.h"
@@ -774,6 +775,101 @@ __device__ __forceinline__ void attn_prefetch(const LayersArgs &a, const LayerG 
   attn_load_v(a, P.vcache + kv_row * kD * a.vt_stride, p0, split_end_v(a, s), kv);
 }
 
+// ---- K / V^T of a run's next attention item, staged in LDS -------------
+// Within a workgroup's run of attention items, each item requests its
+// successor's first block global -> LDS directly (buffer loads with the LDS
+// destination, inline asm, so the compiler neither waits for them nor
+// counts them) once its own block is in registers, and the successor copies
+// it from LDS into the registers attn_load_k / attn_load_v would fill. The
+// area overlays the GEMV staging, idle during the attention phase, after
+// the item's own LDS.
+//  - K: kBlk positions x 256 B, position p's 16-byte chunk c at chunk c ^ (p
+//    % 16) (16 lanes reading one chunk of 16 consecutive positions hit
+//    distinct banks); 40 loads of 4 positions.
+//  - V^T: kD rows (dims) x kBlk positions (320 B), chunk c of row d at c ^
+//    ((d / 4) % 4); 40 loads of 64 chunks.
+// Positions are clamped as the register path clamps them, so the values
+// are the same. Items past the context request nothing.
+constexpr int kStageRun = 8;  // shortest run whose items stage their successor's block
+constexpr int kStageOff = (int)((sizeof(AttnLds<2>) + 1023) / 1024 * 1024);
+constexpr int kStageK = kBlk * kD * 2;       // 40 KiB
+constexpr int kStageBytes = 2 * kStageK;     // + V^T
+constexpr int kStageLoads = kStageK / 1024;  // per operand: 40
+static_assert(kBlk % 4 == 0 && (kD * kBlk * 2) % 1024 == 0 && kStageLoads % 4 == 0, "stage layout");
+static_assert(kBlk / 8 % 4 == 0, "V^T chunk swizzle stays in the row");
+
+__device__ __forceinline__ void attn_stage_issue(const LayersArgs &a, const LayerG &P, int item,
+                                                 uint8_t *smem) {
+  const int splits = a.splits, kvn = a.kv_heads;
+  const int s = item % splits, kvh = (item / splits) % kvn, b = item / (splits * kvn);
+  const int p0 = s * a.chunk, L = cnst(a.pos)[b] + 1;
+  if (p0 >= L || p0 >= a.max_pos || L > a.max_pos) return;  // uniform: an item past the context
+  const size_t kv_row = (size_t)b * kvn + kvh;
+  const int pe_k = split_end_k(a, s), pe_v = split_end_v(a, s);
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  auto desc = [](uint64_t x, uint32_t bytes) {
+    return u32x4{(uint32_t)x, (uint32_t)(x >> 32) & 0xffffu, bytes, 0x00020000u};
+  };
+  const u32x4 kd = desc((uint64_t)(uintptr_t)(P.kcache + kv_row * a.max_pos * kD), (uint32_t)a.max_pos * kD * 2);
+  const u32x4 vd = desc((uint64_t)(uintptr_t)(P.vcache + kv_row * kD * a.vt_stride), (uint32_t)kD * a.vt_stride * 2);
+  const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)smem + kStageOff;
+  constexpr int kPer = kStageLoads / 4;  // loads per wave per operand
+#pragma unroll
+  for (int j = 0; j < kPer; j++) {
+    const int u = wave * kPer + j;
+    const int pos = 4 * u + (lane >> 4);
+    const int pc = min(p0 + pos, pe_k - 1);
+    const int vo = pc * kD * 2 + (((lane & 15) ^ (pos & 15)) * 16);
+    const uint32_t m0 = base + u * 1024;
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(vo), "s"(kd), "{m0}"(m0) : "memory");
+  }
+#pragma unroll
+  for (int j = 0; j < kPer; j++) {
+    const int u = wave * kPer + j;
+    const int f = 64 * u + lane, d = f / (kBlk / 8), c = f % (kBlk / 8);
+    const int pv = min(p0 + 8 * (c ^ ((d >> 2) & 3)), pe_v - 8);
+    const int vo = (d * a.vt_stride + pv) * 2;
+    const uint32_t m0 = base + kStageK + u * 1024;
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(vo), "s"(vd), "{m0}"(m0) : "memory");
+  }
+}
+
+// Uses every register of kv, so the compiler waits here for the loads that
+// filled them: a load still pending on some path where paths join makes it
+// wait for all loads (vmcnt(0)) at the next register it reuses, staging
+// loads included.
+__device__ __forceinline__ void attn_kv_ready(const AttnKV &kv) {
+#pragma unroll
+  for (int tt = 0; tt < kKT; tt++)
+    asm volatile("" ::"v"(kv.k[tt][0]), "v"(kv.k[tt][1]), "v"(kv.k[tt][2]), "v"(kv.k[tt][3]));
+#pragma unroll
+  for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+    for (int ks = 0; ks < kVS; ks++) asm volatile("" ::"v"(kv.v[nt][ks]));
+}
+
+// The staged block into the registers of attn_load_k / attn_load_v (item
+// positions from p0, the split's K end pe_k).
+__device__ __forceinline__ void attn_stage_read(const uint8_t *smem, int p0, int pe_k, AttnKV &kv) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, grp = lane >> 4;
+  const uint8_t *st = smem + kStageOff;
+#pragma unroll
+  for (int tt = 0; tt < kKT; tt++) {
+    const int pos = min(16 * (wave + 4 * tt) + r, pe_k - 1 - p0);
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++)
+      kv.k[tt][kk] = *reinterpret_cast<const f16x8 *>(st + pos * kD * 2 + (((4 * kk + grp) ^ (pos & 15)) * 16));
+  }
+#pragma unroll
+  for (int nt = 0; nt < 2; nt++) {
+    const int d = 32 * wave + 16 * nt + r;
+#pragma unroll
+    for (int ks = 0; ks < kVS; ks++)
+      kv.v[nt][ks] = *reinterpret_cast<const f16x8 *>(
+          st + kStageK + (d * (kBlk / 8) + ((4 * ks + grp) ^ ((d >> 2) & 3))) * 16);
+  }
+}
+
 // The new token's k (wave 2) or v (wave 3) values e0, e0 + 1 into the
 // cache: K row `pos`, V^T column `pos`.
 __device__ __forceinline__ void append_new(const LayersArgs &a, SH_GLOBAL uint16_t *kb, SH_GLOBAL uint16_t *vtb,
@@ -793,13 +889,17 @@ __device__ __forceinline__ void append_new(const LayersArgs &a, SH_GLOBAL uint16
 // the head, RoPE rotate-half at this step's position; the split holding it
 // appends the new k / v to the cache) and writes the partial (unnormalised
 // V sum, max, sum) of each head as cells. Splits past the context write
-// nothing. With `reuse`, the workgroup's previous item was the split
+// nothing. `runs`: the workgroup runs several items (staged: this item's
+// first block was staged in LDS by the previous one; next: the item whose
+// block this one stages, or -1). With `reuse`, the workgroup's previous
+// item was the split
 // before this one of the same (row, KV head): its normed, rotated q and new
 // k / v are still in LDS, so this item neither polls the cells nor
 // normalises again (the values, and so the arithmetic, are the same).
 template <int kG>
 __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, int l, int item, unsigned ep,
-                          uint8_t *smem, Misc *misc, AttnKV &kv, bool reuse) {
+                          uint8_t *smem, Misc *misc, AttnKV &kv, bool runs, bool reuse, bool staged,
+                          int next) {
   static_assert((kG + 2) * kD / 2 <= kT, "one pair of q / k / v cells per thread");
   static_assert(kG <= 4, "MFMA rows 0..3 of lanes 0..15 hold the heads");
   AttnLds<kG> &S = *reinterpret_cast<AttnLds<kG> *>(smem);
@@ -818,7 +918,15 @@ __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, 
 
   const int L = cnst(a.pos)[b] + 1;  // context including the new token
   const int active = (L + chunk - 1) / chunk;
-  if (s >= active || cap <= 0 || L > a.max_pos) return true;  // uniform
+  if (s >= active || cap <= 0 || L > a.max_pos) {  // uniform
+    // the next item's block is staged all the same; with none, a block
+    // staged for this one lands before the phase ends
+    if (next >= 0)
+      attn_stage_issue(a, P, next, smem);
+    else if (staged)
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return true;
+  }
   const int h0 = kvh * kG;
   const unsigned tag = tag_of(ep, l);
   const int p1 = min(L, p0 + chunk), np = p1 - p0, pos = L - 1;
@@ -879,6 +987,16 @@ __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, 
   }
   lds_barrier();
   SH_MARK(misc, l, 9);
+  // this item's first block, staged in LDS by the previous item, into kv;
+  // the next item's block is requested below, after every load this item
+  // waits for (loads complete in issue order; this item's further blocks, if
+  // any, wait for it)
+  if (staged) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's staging loads done
+    __builtin_amdgcn_s_barrier();                      // and every wave's
+    attn_stage_read(smem, p0, split_end_k(a, s), kv);
+    lds_barrier();  // all reads of the area done before it is written again
+  }
 
   // q as the MFMA A operand: row lane % 16 = head (zero past kG), k = 32 kk + 8 (lane / 16)
   // (read unconditionally from a clamped row, then selected: a conditional
@@ -896,6 +1014,16 @@ __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, 
         qa[kk][e + 4] = r < kG ? (_Float16)hi[e] : (_Float16)0.0f;
       }
     }
+  }
+  // (after the q reads: a wait the compiler places before them would
+  // otherwise wait for the staging loads)
+  if (runs) {
+    if (!staged) attn_kv_ready(kv);
+    // every load the compiler counts completes here, on every path (it
+    // applies a wait it sees to its own count), so no later wait it places
+    // for one of them also waits for the staging loads
+    __builtin_amdgcn_s_waitcnt(0);
+    if (next >= 0) attn_stage_issue(a, P, next, smem);
   }
   const int nblk = (np + kBlk - 1) / kBlk;
 
@@ -1281,15 +1409,32 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
         }))
       return;
     SH_MARK(misc, l, 16);
-    if (!for_run<kOne>(bA, eA, [&](int i) {
-          if (i != bA) attn_prefetch(a, P, i, kv);
-          if (i == bA) SH_TRACE(misc, l, 2);
-          const bool reuse = !kOne && i != bA && i % a.splits != 0;
-          if (!attn_item<kG>(a, P, l, i, ep, smem, misc, kv, reuse)) return false;
-          if (i == bA) { SH_TRACE(misc, l, 3); SH_TRACE_WAIT(l, 1, misc); }
-          return true;
-        }))
+    // the run's first block was requested into registers before the phase;
+    // in runs of kStageRun items or more every later one is staged in LDS by
+    // the item before it, in shorter ones requested when its item starts
+    // (two copies of the loop: where paths with and without staging join,
+    // the compiler's waits for the register path's loads would also wait
+    // for staging loads)
+    auto attn_run = [&](auto stg_c) {
+      constexpr bool kStg = decltype(stg_c)::value;
+      return for_run<kOne>(bA, eA, [&](int i) {
+        if (i != bA && !kStg) attn_prefetch(a, P, i, kv);
+        if (i == bA) SH_TRACE(misc, l, 2);
+        const bool reuse = !kOne && i != bA && i % a.splits != 0;
+        const int nx = kStg && i + 1 < eA ? i + 1 : -1;
+        if (!attn_item<kG>(a, P, l, i, ep, smem, misc, kv, kStg, reuse, kStg && i != bA, nx)) return false;
+        if (i == bA) { SH_TRACE(misc, l, 3); SH_TRACE_WAIT(l, 1, misc); }
+        return true;
+      });
+    };
+    if (!kOne && eA - bA >= kStageRun) {
+      if (!attn_run(std::integral_constant<bool, true>())) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no staging load lands after the exit
+        return;
+      }
+    } else if (!attn_run(std::integral_constant<bool, false>())) {
       return;
+    }
     SH_MARK(misc, l, 17);
     if (!for_items<kOne>(m0, nM, G, [&](int j) {
           if (!merge_item<kSP>(a, l, j, ep, smem, misc)) return false;
@@ -1428,6 +1573,7 @@ size_t decode_layers_lds(int B, int H, int heads, int inter, int *misc_offset) {
   size_t end = xs_max + 3 * 2 * 64 * 4 * sizeof(float);  // + wave-reduction area
   const size_t attn = attn_lds(2);
   if (attn > end) end = attn;
+  if ((size_t)kStageOff + kStageBytes > end) end = (size_t)kStageOff + kStageBytes;  // staged K / V^T
   if (sizeof(MergeLds) > end) end = sizeof(MergeLds);
   end = (end + 15) / 16 * 16;
   *misc_offset = (int)end;
