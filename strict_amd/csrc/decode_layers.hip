@@ -234,7 +234,8 @@ __device__ __forceinline__ bool waits_ok(const LayersArgs &a, bool ok, Misc *mis
 // Timeline of one step (diagnostic builds only), kept in LDS during the step
 // and written out when the kernel ends: per workgroup and layer, tr[0] holds
 // each phase's start (even slots 0..8: QKV, attention, O, gate/up, down),
-// end (odd slots), the end of its wait (10..14) and the merge end (15); tr[1]
+// end (odd slots), the end of its wait (10..14), the merge end (15) and the
+// ends of the workgroup's first eight attention items (16..23); tr[1]
 // holds marks inside items: QKV 0..3 (staged, MFMA, reduced, stored), down
 // 4..7, attention 8..13 (q/k/v polled, RoPE, scores, softmax, V sums,
 // stored), merge 14..15 (polled, stored), and the end of each phase's items
@@ -1424,6 +1425,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
         const int nx = kStg && i + 1 < eA ? i + 1 : -1;
         if (!attn_item<kG>(a, P, l, i, ep, smem, misc, kv, kStg, reuse, kStg && i != bA, nx)) return false;
         if (i == bA) { SH_TRACE(misc, l, 3); SH_TRACE_WAIT(l, 1, misc); }
+        if (i - bA < 8) SH_TRACE(misc, l, 16 + (i - bA));  // the run's first eight items' ends
         return true;
       });
     };
