@@ -55,7 +55,10 @@ namespace {
 constexpr int kT = 256;         // threads per workgroup (4 waves)
 constexpr int kD = 128;         // head dim
 constexpr int kMaxSplits = 64;  // splits per (row, KV head) a merge item combines
-constexpr int kMaxRowsPerPass = 4;  // batch rows staged together (1 at batch 1)
+// batch rows staged together (each pass is one round of cell polls): 1 at
+// batch 1, 4 up to batch 4, 8 above
+constexpr int kMaxRowsPerPass = 8;
+constexpr int kSmallBatchRows = 4;
 
 // Pointers the kernel reads from its argument table (LayerPtrs) are generic;
 // loads through them compile to flat instructions, which also count against
@@ -178,9 +181,10 @@ constexpr int kTraceWgs = 256, kTraceLayers = 32, kTraceSlots = 24;
 
 // Small LDS words after the phase areas.
 struct Misc {
-  float part[4][kMaxRowsPerPass];  // per-wave partial sums of squares
+  float part[4][kSmallBatchRows];  // per-wave partial sums of squares, rows 0..3 of a pass
   int vote[2][4];                  // per-wave votes of block_any (two alternating sets)
   int par[4];                      // each wave's current vote set
+  float part_hi[4][kMaxRowsPerPass - kSmallBatchRows];  // rows 4.. of a pass
 #ifdef SH_DECODE_TRACE
   unsigned long long t_wait;                          // when the last wait ended
   unsigned long long tr[2][kTraceLayers][kTraceSlots];  // this workgroup's timeline
@@ -367,10 +371,12 @@ __device__ __forceinline__ bool stage_chunk_ok(int K, int j) {
 // registers; the per-row sums of squares are combined across the four
 // waves through LDS. kChunks >= K / 1024. kLocal: the caller's waves read
 // only their own K quarter of xs, so no barrier follows the stores.
-template <int kChunks, int kRows, bool kLocal>
+template <int kChunks, int kRowsMax, bool kLocal>
 __device__ __forceinline__ bool stage_rms(const LayersArgs &a, const uint64_t *xc, const float *xp, unsigned tag,
                           const SH_GLOBAL float *g, int K, _Float16 *xs, Misc *misc) {
   typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+  // rows per pass: at most kRowsMax, and at most 64 cells per thread
+  constexpr int kRows = kRowsMax * kChunks * 4 <= 64 ? kRowsMax : 64 / (kChunks * 4);
   constexpr int kN = kRows * kChunks * 4;
   static_assert(kN <= 64, "cells per thread");
   const int B = kRows == 1 ? 1 : a.B, c4 = K >> 2, t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -424,14 +430,19 @@ __device__ __forceinline__ bool stage_rms(const LayersArgs &a, const uint64_t *x
           ss += (v[r][j][0] * v[r][j][0] + v[r][j][1] * v[r][j][1]) +
                 (v[r][j][2] * v[r][j][2] + v[r][j][3] * v[r][j][3]);
       ss = wave_sum_rows(ss);
-      if (lane == 0) misc->part[wave][r] = ss;
+      if (lane == 0) {
+        if (r < kSmallBatchRows) misc->part[wave][r] = ss;
+        else misc->part_hi[wave][r - kSmallBatchRows] = ss;
+      }
     }
     lds_barrier();
 #pragma unroll
     for (int r = 0; r < kRows; r++) {
       const int b = b0 + r;
       if (b >= B) break;
-      const float ss = (misc->part[0][r] + misc->part[1][r]) + (misc->part[2][r] + misc->part[3][r]);
+      const float(&pr)[4][kSmallBatchRows] = *reinterpret_cast<const float(*)[4][kSmallBatchRows]>(
+          r < kSmallBatchRows ? &misc->part[0][r] : &misc->part_hi[0][r - kSmallBatchRows]);
+      const float ss = (pr[0][0] + pr[1][0]) + (pr[2][0] + pr[3][0]);
       const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
 #pragma unroll
       for (int j = 0; j < kChunks; j++) {
@@ -454,9 +465,11 @@ __device__ __forceinline__ bool stage_rms(const LayersArgs &a, const uint64_t *x
 // tagged `tag`) -> xs (row stride K + 8), kRows rows per pass. A thread
 // stages the two-cell chunks stage_chunk(K, j), j < kChunks (kChunks >=
 // K / 1024). kLocal as for stage_rms.
-template <int kChunks, int kRows, bool kLocal>
+template <int kChunks, int kRowsMax, bool kLocal>
 __device__ __forceinline__ bool stage_f16(const LayersArgs &a, const uint64_t *cells, unsigned tag, int K,
                           _Float16 *xs, Misc *misc) {
+  // rows per pass: at most kRowsMax, and at most 64 cells per thread
+  constexpr int kRows = kRowsMax * kChunks * 2 <= 64 ? kRowsMax : 64 / (kChunks * 2);
   constexpr int kN = kRows * kChunks * 2;
   static_assert(kN <= 64, "cells per thread");
   const int B = kRows == 1 ? 1 : a.B, c4 = K >> 2, row_cells = K >> 1;
@@ -1394,10 +1407,16 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
   // head), whose items after the first reuse its q / k / v preparation
   const int bA = kOne ? w : (int)((int64_t)w * nB / G);
   const int eA = kOne ? min(w + 1, nB) : (int)((int64_t)(w + 1) * nB / G);
+  // the run's first K / V block requested into registers a phase ahead (in
+  // the previous layer's gate/up or down phase); the large-batch variant
+  // instead stages it in LDS when the attention phase starts (its cell poll
+  // covers the load), so no K / V registers are live through the GEMV
+  // phases, whose staging passes then hold 8 rows
+  constexpr bool kPre = kRows <= kSmallBatchRows;
   AttnKV kv;
   u32x4 wa[kLA][1];  // this workgroup's first QKV item's weights
   if (w < nA) load_weights<kLA, 1>(wa, layer_g(a, 0).wqkv, H, w);
-  if (bA < eA) attn_prefetch(a, layer_g(a, 0), bA, kv);
+  if (kPre && bA < eA) attn_prefetch(a, layer_g(a, 0), bA, kv);
   for (int l = 0; l < a.n_layers; l++) {
     const LayerG P = layer_g(a, l);
     const bool next = l + 1 < a.n_layers;
@@ -1418,12 +1437,17 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
     // for staging loads)
     auto attn_run = [&](auto stg_c) {
       constexpr bool kStg = decltype(stg_c)::value;
+      if (kStg && !kPre && bA < eA) {
+        lds_barrier();  // every wave is past the previous phase's LDS reads
+        attn_stage_issue(a, P, bA, smem);
+      }
       return for_run<kOne>(bA, eA, [&](int i) {
-        if (i != bA && !kStg) attn_prefetch(a, P, i, kv);
+        if ((i != bA || !kPre) && !kStg) attn_prefetch(a, P, i, kv);
         if (i == bA) SH_TRACE(misc, l, 2);
         const bool reuse = !kOne && i != bA && i % a.splits != 0;
         const int nx = kStg && i + 1 < eA ? i + 1 : -1;
-        if (!attn_item<kG>(a, P, l, i, ep, smem, misc, kv, kStg, reuse, kStg && i != bA, nx)) return false;
+        const bool staged = kStg && (i != bA || !kPre);
+        if (!attn_item<kG>(a, P, l, i, ep, smem, misc, kv, kStg, reuse, staged, nx)) return false;
         if (i == bA) { SH_TRACE(misc, l, 3); SH_TRACE_WAIT(l, 1, misc); }
         if (i - bA < 8) SH_TRACE(misc, l, 16 + (i - bA));  // the run's first eight items' ends
         return true;
@@ -1471,7 +1495,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
     // ~2 us; on the workgroups with only a gate/up item, right after the
     // attention item, the burst slowed the merge and O items' polls.)
     if (hasC && next) {
-      if (bA < eA) attn_prefetch(a, layer_g(a, l + 1), bA, kv);
+      if (kPre && bA < eA) attn_prefetch(a, layer_g(a, l + 1), bA, kv);
       if (w < nA) load_weights<kLA, 1>(wa, layer_g(a, l + 1).wqkv, H, w);
     }
     if (!for_items<kOne>(d0, nD, G, [&](int i) {
@@ -1483,7 +1507,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
       return;
     SH_MARK(misc, l, 20);
     if (!hasC && next) {
-      if (bA < eA) attn_prefetch(a, layer_g(a, l + 1), bA, kv);
+      if (kPre && bA < eA) attn_prefetch(a, layer_g(a, l + 1), bA, kv);
       if (w < nA) load_weights<kLA, 1>(wa, layer_g(a, l + 1).wqkv, H, w);
     }
     if (!for_items<kOne>(w, nE, G, [&](int i) {
@@ -1528,9 +1552,12 @@ const void *kernel_for(const Shape &s, int batch, bool one, int *max_splits) {
 #define SH_MATCH(G, LA, LC, LD, LE, SP)                                                            \
   if (s.g == G && s.la == LA && s.lc == LC && s.ld == LD && s.le == LE) {                          \
     if (max_splits) *max_splits = SP;                                                              \
-    if (batch > 1)                                                                                 \
+    if (batch > kSmallBatchRows)                                                                   \
       return reinterpret_cast<const void *>(                                                       \
           &decode_layers_kernel<G, LA, LC, LD, LE, SP, kMaxRowsPerPass, false>);                   \
+    if (batch > 1)                                                                                 \
+      return reinterpret_cast<const void *>(                                                       \
+          &decode_layers_kernel<G, LA, LC, LD, LE, SP, kSmallBatchRows, false>);                   \
     return one ? reinterpret_cast<const void *>(&decode_layers_kernel<G, LA, LC, LD, LE, SP, 1, true>) \
                : reinterpret_cast<const void *>(&decode_layers_kernel<G, LA, LC, LD, LE, SP, 1, false>); \
   }
@@ -1587,8 +1614,10 @@ size_t decode_layers_partial_cells(int heads) { return (size_t)kMaxBatch * heads
 hipError_t decode_layers_occupancy(const LayersArgs &a, size_t lds, int *blocks_per_cu) {
   const Shape sh = shape_of(a.H, a.heads, a.kv_heads, a.inter);
   int least = 1 << 30;
-  for (int v = 0; v < 3; v++) {
-    const void *k = kernel_for(sh, v == 2 ? kMaxBatch : 1, v == 0, nullptr);
+  // every variant: batch 1 (one item each / not), up to kSmallBatchRows, larger
+  const int batch_of[4] = {1, 1, kSmallBatchRows, kMaxBatch};
+  for (int v = 0; v < 4; v++) {
+    const void *k = kernel_for(sh, batch_of[v], v == 0, nullptr);
     if (!k) return hipErrorInvalidValue;
     hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;

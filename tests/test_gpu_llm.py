@@ -361,10 +361,13 @@ def test_qwen3_config4_greedy_256(ctx, config4):
     _batch_greedy_check(m, w, prompt, 256, "qwen3-config4-b1")
 
 
-@pytest.mark.parametrize("batch", [4, 16])
+@pytest.mark.parametrize("batch", [4, 6, 8, 16])
 def test_qwen3_config4_batch_vs_oracle(ctx, config4, batch):
-    # configs[4] at batch 4 and 16: every row its own prompt, each checked
-    # against its own oracle decoder (b = 16: four staging passes of 4 rows)
+    # configs[4] at batch 4 to 16: every row its own prompt, each checked
+    # against its own oracle decoder. b = 4: the small-batch kernel (staging
+    # passes of 4 rows); b = 6, 8, 16: the large-batch kernel (passes of 8
+    # rows) with runs of 6 attention items (each requests its own first K / V
+    # block) and of 8 / 16 (each stages its successor's block in LDS)
     m, w = config4
     prompts = np.random.default_rng(100 + batch).integers(0, QWEN_CONFIG4.vocab, (batch, 12))
     _, _, _, decs = _batch_greedy_check(m, w, prompts, 8, f"qwen3-config4-b{batch}")
