@@ -570,12 +570,17 @@ __device__ __forceinline__ void consume_cells(const uint64_t (&c)[4]) {
 // weights (load_weights, issued by the caller)
 template <int kL, int kRows>
 __device__ __forceinline__ bool qkv_item(const LayersArgs &a, const LayerG &P, int l, int i, unsigned ep,
-                         const Lds &s, const u32x4 (&w)[kL][1]) {
+                         const Lds &s, const u32x4 (&w)[kL][1], bool reuse) {
   const int lane = threadIdx.x & 63, col = lane & 15;
   const float sc = P.sqkv[i * 16 + col];
   __builtin_amdgcn_sched_barrier(0);
-  if (!stage_rms<(kL + 3) / 4, kRows, true>(a, a.x0c, l == 0 ? a.x_in : nullptr, tag_of(ep, l - 1), P.norm1,
-                               a.H, s.xs, s.misc))
+  // reuse: the workgroup's previous item staged this layer's rows already
+  // (each wave reads only its own K quarter of them); the barrier keeps
+  // this item's reduction writes behind the previous one's reads
+  if (reuse)
+    lds_barrier();
+  else if (!stage_rms<(kL + 3) / 4, kRows, true>(a, a.x0c, l == 0 ? a.x_in : nullptr, tag_of(ep, l - 1),
+                                                 P.norm1, a.H, s.xs, s.misc))
     return false;
   SH_MARK(s.misc, l, 0);
   f32x4 acc[1];
@@ -1413,21 +1418,28 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
   // covers the load), so no K / V registers are live through the GEMV
   // phases, whose staging passes then hold 8 rows
   constexpr bool kPre = kRows <= kSmallBatchRows;
+  // QKV items: every G-th from w; in the large-batch variant two
+  // consecutive tiles per workgroup [bQ, eQ) on one staged input, so each
+  // input row is read by half as many workgroups
+  const int gQ = kPre ? G : min(G, (nA + 1) / 2);
+  const int bQ = kPre ? w : (w < gQ ? (int)((int64_t)w * nA / gQ) : nA);
+  const int eQ = kPre ? nA : (w < gQ ? (int)((int64_t)(w + 1) * nA / gQ) : nA);
+  const bool hasQ = bQ < eQ;
   AttnKV kv;
   u32x4 wa[kLA][1];  // this workgroup's first QKV item's weights
-  if (w < nA) load_weights<kLA, 1>(wa, layer_g(a, 0).wqkv, H, w);
+  if (hasQ) load_weights<kLA, 1>(wa, layer_g(a, 0).wqkv, H, bQ);
   if (kPre && bA < eA) attn_prefetch(a, layer_g(a, 0), bA, kv);
   for (int l = 0; l < a.n_layers; l++) {
     const LayerG P = layer_g(a, l);
     const bool next = l + 1 < a.n_layers;
-    if (!for_items<kOne>(w, nA, G, [&](int i) {
-          if (i != w) load_weights<kLA, 1>(wa, P.wqkv, H, i);
-          if (i == w) SH_TRACE(misc, l, 0);
-          if (!qkv_item<kLA, kRows>(a, P, l, i, ep, lds, wa)) return false;
-          if (i == w) { SH_TRACE(misc, l, 1); SH_TRACE_WAIT(l, 0, misc); }
-          return true;
-        }))
-      return;
+    auto qkv_one = [&](int i) {
+      if (i != bQ) load_weights<kLA, 1>(wa, P.wqkv, H, i);
+      if (i == bQ) SH_TRACE(misc, l, 0);
+      if (!qkv_item<kLA, kRows>(a, P, l, i, ep, lds, wa, !kPre && i != bQ)) return false;
+      if (i == bQ) { SH_TRACE(misc, l, 1); SH_TRACE_WAIT(l, 0, misc); }
+      return true;
+    };
+    if (kPre ? !for_items<kOne>(w, nA, G, qkv_one) : !for_run<false>(bQ, eQ, qkv_one)) return;
     SH_MARK(misc, l, 16);
     // the run's first block was requested into registers before the phase;
     // in runs of kStageRun items or more every later one is staged in LDS by
@@ -1496,7 +1508,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
     // attention item, the burst slowed the merge and O items' polls.)
     if (hasC && next) {
       if (kPre && bA < eA) attn_prefetch(a, layer_g(a, l + 1), bA, kv);
-      if (w < nA) load_weights<kLA, 1>(wa, layer_g(a, l + 1).wqkv, H, w);
+      if (hasQ) load_weights<kLA, 1>(wa, layer_g(a, l + 1).wqkv, H, bQ);
     }
     if (!for_items<kOne>(d0, nD, G, [&](int i) {
           if (i == d0) SH_TRACE(misc, l, 6);
@@ -1508,7 +1520,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
     SH_MARK(misc, l, 20);
     if (!hasC && next) {
       if (kPre && bA < eA) attn_prefetch(a, layer_g(a, l + 1), bA, kv);
-      if (w < nA) load_weights<kLA, 1>(wa, layer_g(a, l + 1).wqkv, H, w);
+      if (hasQ) load_weights<kLA, 1>(wa, layer_g(a, l + 1).wqkv, H, bQ);
     }
     if (!for_items<kOne>(w, nE, G, [&](int i) {
           if (i == w) SH_TRACE(misc, l, 8);
