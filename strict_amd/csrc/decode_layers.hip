@@ -736,6 +736,12 @@ struct MergeLds {
   float part[4][kT][3];     // per wave: column pair's two sums and the l sum
 };
 
+// LDS of a merge run (all kMergeParts parts of a head in one item).
+struct MergeRunLds {
+  float gm[kT];
+  float part[kMergeParts][4][16][3];  // per part and wave, as MergeLds::part
+};
+
 // K and V^T registers of one block (the first block of an item is
 // requested ahead by attn_prefetch): k[tt][kk] holds K[position 16 (w +
 // 4 tt) + lane % 16][32 kk + 8 (lane / 16) ..], v[nt][ks] holds
@@ -1271,6 +1277,102 @@ __device__ __forceinline__ bool merge_item(const LayersArgs &a, int l, int item,
   return true;
 }
 
+// M, all kMergeParts parts of (row, query head) hb in one item (the
+// large-batch variant): one round of polls for every part's cells, the
+// split maxima and l sums combined once, then each part's arithmetic
+// exactly as merge_item's (so the results are the same bit for bit).
+template <int kSP>
+__device__ __forceinline__ bool merge_run(const LayersArgs &a, int l, int hb, unsigned ep, uint8_t *smem,
+                                          Misc *misc) {
+  constexpr int kPairs = kD / kMergeParts / 2, kGroups = kT / kPairs, kPer = kSP / kGroups;
+  constexpr int kC = 2 + 2 * kMergeParts;  // cells per split: (m, l), then each part's column pair
+  static_assert(kPer * kC <= 64 && kPairs == 16 && kGroups == 16, "cells per thread");
+  MergeRunLds &S = *reinterpret_cast<MergeRunLds *>(smem);
+  const int h = hb % a.heads, b = hb / a.heads;
+  const int t = threadIdx.x, q = t % kPairs, sg = t / kPairs;
+  const int L = cnst(a.pos)[b] + 1;
+  const int active = min((L + a.chunk - 1) / a.chunk, a.splits);
+  const size_t base = ((size_t)b * a.heads + h) * a.splits * kPStride;
+  const unsigned tag = tag_of(ep, l);
+  uint64_t mask = 0;
+#pragma unroll
+  for (int k = 0; k < kPer; k++)
+    if (sg + kGroups * k < active) mask |= ((1ull << kC) - 1) << (kC * k);
+  uint64_t cv[kPer * kC];
+  const bool ok = spin_cells(a, a.partc,
+                             [&](int c) {
+                               const int k = c / kC, r = c % kC;
+                               const int j = min(sg + kGroups * k, active - 1);
+                               const int p = (r - 2) >> 1;
+                               return base + (size_t)j * kPStride +
+                                      (r < 2 ? kD + r : kD / kMergeParts * p + 2 * q + ((r - 2) & 1));
+                             },
+                             mask, tag, cv);
+  if (!waits_ok(a, ok, misc)) return false;
+  SH_MARK(misc, l, 14);
+  float mg = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < kPer; k++)
+    if (sg + kGroups * k < active) mg = fmaxf(mg, cell_f32(cv[kC * k]));
+  float s0[kMergeParts], s1[kMergeParts], lg = 0.0f;
+#pragma unroll
+  for (int p = 0; p < kMergeParts; p++) s0[p] = s1[p] = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kPer; k++) {
+    if (sg + kGroups * k < active) {
+      const float wj = expf(cell_f32(cv[kC * k]) - mg);
+#pragma unroll
+      for (int p = 0; p < kMergeParts; p++) {
+        s0[p] += wj * cell_f32(cv[kC * k + 2 + 2 * p]);
+        s1[p] += wj * cell_f32(cv[kC * k + 3 + 2 * p]);
+      }
+      lg += wj * cell_f32(cv[kC * k + 1]);
+    }
+  }
+  if (q == 0) S.gm[sg] = mg;
+  lds_barrier();
+  float M = -INFINITY;
+#pragma unroll
+  for (int g = 0; g < kGroups; g++) M = fmaxf(M, S.gm[g]);
+  const float wg = mg == -INFINITY ? 0.0f : expf(mg - M);
+  lg *= wg;
+#pragma unroll
+  for (int off = 16; off <= 32; off <<= 1) lg += __shfl_xor(lg, off, 64);
+  const int wave = t >> 6;
+#pragma unroll
+  for (int p = 0; p < kMergeParts; p++) {
+    float x0 = s0[p] * wg, x1 = s1[p] * wg;
+#pragma unroll
+    for (int off = 16; off <= 32; off <<= 1) {
+      x0 += __shfl_xor(x0, off, 64);
+      x1 += __shfl_xor(x1, off, 64);
+    }
+    if ((t & 63) < kPairs) {
+      S.part[p][wave][q][0] = x0;
+      S.part[p][wave][q][1] = x1;
+      S.part[p][wave][q][2] = lg;
+    }
+  }
+  lds_barrier();
+  if (t < kPairs * kMergeParts) {
+    const int p = t / kPairs, qq = t % kPairs;
+    float v0 = 0.0f, v1 = 0.0f, lsum = 0.0f;
+#pragma unroll
+    for (int w4 = 0; w4 < 4; w4++) {
+      v0 += S.part[p][w4][qq][0];
+      v1 += S.part[p][w4][qq][1];
+      lsum += S.part[p][w4][qq][2];
+    }
+    const float inv = 1.0f / lsum;
+    const uint32_t packed = (uint32_t)f32_to_f16_bits(v0 * inv) |
+                            ((uint32_t)f32_to_f16_bits(v1 * inv) << 16);
+    cst1(a.attnc, (size_t)(b * a.heads + h) * (kD / 2) + (kD / kMergeParts * p + 2 * qq) / 2, packed, tag);
+  }
+  SH_MARK(misc, l, 15);
+  lds_barrier();  // the next item reuses the LDS
+  return true;
+}
+
 // ---- the kernel ----------------------------------------------------------------
 
 // H (steps with logits): logits[b][n] = head_scale[n] * (W_head
@@ -1474,12 +1576,22 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
       return;
     }
     SH_MARK(misc, l, 17);
-    if (!for_items<kOne>(m0, nM, G, [&](int j) {
-          if (!merge_item<kSP>(a, l, j, ep, smem, misc)) return false;
-          if (j == m0) SH_TRACE(misc, l, 15);
-          return true;
-        }))
+    // merge items: a part of a head each; in the large-batch variant a whole
+    // head each (one round of polls instead of kMergeParts in turn)
+    if constexpr (kPre) {
+      if (!for_items<kOne>(m0, nM, G, [&](int j) {
+            if (!merge_item<kSP>(a, l, j, ep, smem, misc)) return false;
+            if (j == m0) SH_TRACE(misc, l, 15);
+            return true;
+          }))
+        return;
+    } else if (!for_items<false>(m0, nM / kMergeParts, G, [&](int j) {
+                 if (!merge_run<kSP>(a, l, j, ep, smem, misc)) return false;
+                 if (j == m0) SH_TRACE(misc, l, 15);
+                 return true;
+               })) {
       return;
+    }
     SH_MARK(misc, l, 18);
     // O, gate/up and down items request their weights when they start: at
     // batch 1 each workgroup's previous item is then a phase or more behind
@@ -1616,6 +1728,7 @@ size_t decode_layers_lds(int B, int H, int heads, int inter, int *misc_offset) {
   if (attn > end) end = attn;
   if ((size_t)kStageOff + kStageBytes > end) end = (size_t)kStageOff + kStageBytes;  // staged K / V^T
   if (sizeof(MergeLds) > end) end = sizeof(MergeLds);
+  if (sizeof(MergeRunLds) > end) end = sizeof(MergeRunLds);
   end = (end + 15) / 16 * 16;
   *misc_offset = (int)end;
   return end + sizeof(Misc);
