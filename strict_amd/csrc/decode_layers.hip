@@ -1278,7 +1278,7 @@ __device__ __forceinline__ bool merge_item(const LayersArgs &a, int l, int item,
 }
 
 // M, all kMergeParts parts of (row, query head) hb in one item (the
-// large-batch variant): one round of polls for every part's cells, the
+// batched variants): one round of polls for every part's cells, the
 // split maxima and l sums combined once, then each part's arithmetic
 // exactly as merge_item's (so the results are the same bit for bit).
 template <int kSP>
@@ -1576,9 +1576,9 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
       return;
     }
     SH_MARK(misc, l, 17);
-    // merge items: a part of a head each; in the large-batch variant a whole
-    // head each (one round of polls instead of kMergeParts in turn)
-    if constexpr (kPre) {
+    // merge items: a part of a head each at batch 1; in the batched variants
+    // a whole head each (one round of polls instead of kMergeParts in turn)
+    if constexpr (kRows == 1) {
       if (!for_items<kOne>(m0, nM, G, [&](int j) {
             if (!merge_item<kSP>(a, l, j, ep, smem, misc)) return false;
             if (j == m0) SH_TRACE(misc, l, 15);
