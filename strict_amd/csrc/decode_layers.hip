@@ -1472,6 +1472,13 @@ __device__ __forceinline__ bool for_items(int first, int n, int G, F &&f) {
   }
 }
 
+// Active attention splits of row b: those within its context (none for a
+// row past the cache), the splits an attention item does work for.
+__device__ __forceinline__ int attn_active(const LayersArgs &a, int b) {
+  const int L = cnst(a.pos)[b] + 1;
+  return L > a.max_pos ? 0 : min((L + a.chunk - 1) / a.chunk, a.splits);
+}
+
 // Items first .. end - 1 in order (kOne: at most one).
 template <bool kOne, typename F>
 __device__ __forceinline__ bool for_run(int first, int end, F &&f) {
@@ -1510,10 +1517,56 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
   const int m0 = G - 1 - w;             // its first merge item
   const bool hasC = w < nC;
   // attention items: workgroup w runs items [bA, eA), one at batch 1; at
-  // larger batches a contiguous run, i.e. consecutive splits of one (row, KV
-  // head), whose items after the first reuse its q / k / v preparation
-  const int bA = kOne ? w : (int)((int64_t)w * nB / G);
-  const int eA = kOne ? min(w + 1, nB) : (int)((int64_t)(w + 1) * nB / G);
+  // larger batches a contiguous run of the active items (splits within
+  // their row's context), i.e. consecutive splits of one (row, KV head),
+  // whose items after the first reuse its q / k / v preparation. Only active
+  // items are counted, so every workgroup gets the same number of them (a
+  // split past the context costs nothing); bA / eA then index the active
+  // items and item_of maps such an index to its item.
+  // (the small-batch variant; the large-batch one partitions all items,
+  // which keeps each run within half of a (row, KV head)'s splits: counting
+  // only active items there measured 3.471 -> 3.534 ms at b=16)
+  constexpr bool kAct = !kOne && kRows <= kSmallBatchRows;
+  int nAct = nB;
+  if constexpr (kAct) {
+    nAct = 0;
+    for (int b = 0; b < B; b++) nAct += attn_active(a, b) * a.kv_heads;
+  }
+  const int bA = kOne ? w : (int)((int64_t)w * nAct / G);
+  const int eA = kOne ? min(w + 1, nB) : (int)((int64_t)(w + 1) * nAct / G);
+  // a position in the active items: row b, KV head kvh, split s of the
+  // row's act active ones (walked forward one item at a time: the row scan
+  // runs once per run and at row changes)
+  struct ActPos {
+    int b, kvh, s, act;
+  };
+  auto act_at = [&](int k) {
+    ActPos p{0, 0, 0, 0};
+    if (kOne || !kAct) return p;
+    for (; p.b < B; p.b++) {
+      p.act = attn_active(a, p.b);
+      const int n = p.act * a.kv_heads;
+      if (k < n) break;
+      k -= n;
+    }
+    if (p.act > 0) {
+      p.kvh = k / p.act;
+      p.s = k % p.act;
+    }
+    return p;
+  };
+  auto act_next = [&](ActPos p) {
+    if (++p.s < p.act) return p;
+    p.s = 0;
+    if (++p.kvh < a.kv_heads) return p;
+    p.kvh = 0;
+    do {
+      ++p.b;
+    } while (p.b < B && (p.act = attn_active(a, p.b)) == 0);
+    return p;
+  };
+  auto item_at = [&](const ActPos &p) { return (p.b * a.kv_heads + p.kvh) * a.splits + p.s; };
+  auto item_of = [&](int k) { return kOne ? k : (kAct ? item_at(act_at(k)) : k); };
   // the run's first K / V block requested into registers a phase ahead (in
   // the previous layer's gate/up or down phase); the large-batch variant
   // instead stages it in LDS when the attention phase starts (its cell poll
@@ -1530,7 +1583,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
   AttnKV kv;
   u32x4 wa[kLA][1];  // this workgroup's first QKV item's weights
   if (hasQ) load_weights<kLA, 1>(wa, layer_g(a, 0).wqkv, H, bQ);
-  if (kPre && bA < eA) attn_prefetch(a, layer_g(a, 0), bA, kv);
+  if (kPre && bA < eA) attn_prefetch(a, layer_g(a, 0), item_of(bA), kv);
   for (int l = 0; l < a.n_layers; l++) {
     const LayerG P = layer_g(a, l);
     const bool next = l + 1 < a.n_layers;
@@ -1553,17 +1606,26 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
       constexpr bool kStg = decltype(stg_c)::value;
       if (kStg && !kPre && bA < eA) {
         lds_barrier();  // every wave is past the previous phase's LDS reads
-        attn_stage_issue(a, P, bA, smem);
+        attn_stage_issue(a, P, item_of(bA), smem);
       }
-      return for_run<kOne>(bA, eA, [&](int i) {
-        if ((i != bA || !kPre) && !kStg) attn_prefetch(a, P, i, kv);
-        if (i == bA) SH_TRACE(misc, l, 2);
-        const bool reuse = !kOne && i != bA && i % a.splits != 0;
-        const int nx = kStg && i + 1 < eA ? i + 1 : -1;
-        const bool staged = kStg && (i != bA || !kPre);
+      ActPos cur{0, 0, 0, 0};
+      if constexpr (kAct) cur = act_at(bA);
+      return for_run<kOne>(bA, eA, [&](int k) {
+        ActPos nxt{0, 0, 0, 0};
+        int i = k;
+        if constexpr (kAct) {
+          nxt = act_next(cur);
+          i = item_at(cur);
+          cur = nxt;
+        }
+        if ((k != bA || !kPre) && !kStg) attn_prefetch(a, P, i, kv);
+        if (k == bA) SH_TRACE(misc, l, 2);
+        const bool reuse = !kOne && k != bA && i % a.splits != 0;
+        const int nx = kStg && k + 1 < eA ? (kOne || kAct ? item_at(nxt) : k + 1) : -1;
+        const bool staged = kStg && (k != bA || !kPre);
         if (!attn_item<kG>(a, P, l, i, ep, smem, misc, kv, kStg, reuse, staged, nx)) return false;
-        if (i == bA) { SH_TRACE(misc, l, 3); SH_TRACE_WAIT(l, 1, misc); }
-        if (i - bA < 8) SH_TRACE(misc, l, 16 + (i - bA));  // the run's first eight items' ends
+        if (k == bA) { SH_TRACE(misc, l, 3); SH_TRACE_WAIT(l, 1, misc); }
+        if (k - bA < 8) SH_TRACE(misc, l, 16 + (k - bA));  // the run's first eight items' ends
         return true;
       });
     };
@@ -1619,7 +1681,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
     // ~2 us; on the workgroups with only a gate/up item, right after the
     // attention item, the burst slowed the merge and O items' polls.)
     if (hasC && next) {
-      if (kPre && bA < eA) attn_prefetch(a, layer_g(a, l + 1), bA, kv);
+      if (kPre && bA < eA) attn_prefetch(a, layer_g(a, l + 1), item_of(bA), kv);
       if (hasQ) load_weights<kLA, 1>(wa, layer_g(a, l + 1).wqkv, H, bQ);
     }
     if (!for_items<kOne>(d0, nD, G, [&](int i) {
@@ -1631,7 +1693,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
       return;
     SH_MARK(misc, l, 20);
     if (!hasC && next) {
-      if (kPre && bA < eA) attn_prefetch(a, layer_g(a, l + 1), bA, kv);
+      if (kPre && bA < eA) attn_prefetch(a, layer_g(a, l + 1), item_of(bA), kv);
       if (hasQ) load_weights<kLA, 1>(wa, layer_g(a, l + 1).wqkv, H, bQ);
     }
     if (!for_items<kOne>(w, nE, G, [&](int i) {
