@@ -1532,8 +1532,20 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
     nAct = 0;
     for (int b = 0; b < B; b++) nAct += attn_active(a, b) * a.kv_heads;
   }
-  const int bA = kOne ? w : (int)((int64_t)w * nAct / G);
-  const int eA = kOne ? min(w + 1, nB) : (int)((int64_t)(w + 1) * nAct / G);
+  int bA = kOne ? w : (int)((int64_t)w * nAct / G);
+  int eA = kOne ? min(w + 1, nB) : (int)((int64_t)(w + 1) * nAct / G);
+  if constexpr (!kOne && !kAct) {
+    // large-batch variant: when the grid divides into the (row, KV head)
+    // pairs, each pair's workgroups split its active splits evenly (runs
+    // stay within one pair, and no workgroup gets the pair's inactive ones)
+    const int np = B * a.kv_heads;
+    if (G % np == 0) {
+      const int q = G / np, pr = w / q, part = w % q;
+      const int act = attn_active(a, pr / a.kv_heads);
+      bA = pr * a.splits + part * act / q;
+      eA = pr * a.splits + (part + 1) * act / q;
+    }
+  }
   // a position in the active items: row b, KV head kvh, split s of the
   // row's act active ones (walked forward one item at a time: the row scan
   // runs once per run and at row changes)
