@@ -13,22 +13,33 @@ import strict_amd
 from strict_amd import codegen as cg
 
 C_SHARP_INPUTS = {
-    # the shapes CSharpType's line parser reads (CSharpToCudaTranspiler.cs:46-75):
-    # a method line, then `\t\treturn ...;` or a `\t\t\t... = value;` line
-    "AddNumbers": "using System;\n\npublic class AddNumbers\n{\n\tpublic float Add(float first, float second)"
-                  "\n\t{\n\t\treturn first + second;\n\t}\n}\n",
-    "SubtractNumbers": "public class SubtractNumbers\n{\n\tpublic float Subtract(float first, float second)"
-                       "\n\t{\n\t\treturn first - second;\n\t}\n}\n",
-    "MultiplyNumbers": "namespace Samples;\n\npublic class MultiplyNumbers\n{\n\tpublic float Multiply("
-                       "float first, float second)\n\t{\n\t\treturn first * second;\n\t}\n}\n",
-    "InitializeDepths": "namespace Samples.Depth;\n\npublic class InitializeDepths : DepthImageProcessor\n{\n"
-                        "\tpublic InitializeDepths(float initialDepth = 5f) =>\n"
-                        "\t\tthis.initialDepth = initialDepth;\n\n\tprivate readonly float initialDepth;\n\n"
-                        "\tpublic void Process(DepthImage depthImage)\n\t{\n"
-                        "\t\tfor (var y = 0; y < depthImage.Height; y++)\n"
-                        "\t\tfor (var x = 0; x < depthImage.Width; x++)\n"
-                        "\t\t\tdepthImage.Depths[y * depthImage.Width + x] = initialDepth;\n\t}\n}\n",
-    "MissingReturnStatement": "\tfirst + second;\n",
+    # One-method C# files in the shapes CSharpType's line parser reads
+    # (CSharpToCudaTranspiler.cs:46-98): lines holding the type name, braces,
+    # `using`/`namespace`, `this.`, `\tprivate ` or `\t\tfor ` are skipped; a
+    # line starting `\t\treturn` or `\t\t\t` is the body; any other line is
+    # the method line, `<access> float|void Name(float a, ...)`.
+    "AddNumbers": "using System.Numerics;\n\nnamespace KernelSamples.Arithmetic;\n\n"
+                  "internal sealed class AddNumbers\n{\n\tinternal float Add(float left, float right)"
+                  "\n\t{\n\t\treturn left + right;\n\t}\n}\n",
+    # block-scoped namespace: the method line is indented twice and the body
+    # is a `\t\t\treturn` line
+    "SubtractNumbers": "namespace KernelSamples.Arithmetic\n{\n\tpublic record SubtractNumbers\n\t{\n"
+                       "\t\tpublic float Subtract(float minuend, float subtrahend)\n\t\t{\n"
+                       "\t\t\treturn minuend - subtrahend;\n\t\t}\n\t}\n}\n",
+    "MultiplyNumbers": "public struct MultiplyNumbers\n{\n\tpublic float Multiply(float factor, "
+                       "float multiplier)\n\t{\n\t\treturn factor * multiplier;\n\t}\n}\n",
+    # DepthImage expands to (input, width, height, initialDepth); the body is
+    # the right-hand side of the `\t\t\t... = value;` line
+    "InitializeDepths": "using System;\n\nnamespace DepthTools;\n\n"
+                        "public sealed class InitializeDepths(float initialDepth)\n{\n"
+                        "\tprivate float Start => initialDepth;\n\n"
+                        "\tpublic void Process(DepthImage image)\n\t{\n"
+                        "\t\tfor (var row = 0; row < image.Height; row++)\n"
+                        "\t\tfor (var column = 0; column < image.Width; column++)\n"
+                        "\t\t\timage.Depths[row * image.Width + column] = initialDepth;\n\t}\n}\n",
+    # an expression statement is not a return: no body line is found
+    "MissingReturnStatement": "public class MissingReturnStatement\n{\n\tpublic float Half(float value)"
+                              "\n\t{\n\t\tvalue / 2;\n\t}\n}\n",
     "TakesInts": "public class TakesInts\n{\n\tpublic float Twice(int value)\n\t{\n\t\treturn value + value;\n\t}\n}\n",
 }
 
@@ -190,7 +201,7 @@ def test_parse_add_numbers(tmp_path):
     m = t.methods[0]
     assert m.name == "Add"
     assert m.parameters[1].type == "Number" and m.return_type == "Number"
-    assert m.body_text() == "first + second"
+    assert m.body_text() == "left + right"
 
 
 def test_parse_depth_image_expands_to_four_parameters(tmp_path):
