@@ -83,12 +83,12 @@ def rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
 def attend(q: np.ndarray, k: np.ndarray, v: np.ndarray, visible=None) -> np.ndarray:
     """softmax(q k^T) v in fp64 for query rows q [T, d] (already scaled) over
     keys / values [P, d]; visible [T, P] (bool) hides positions where False."""
-    s = q.astype(np.float64) @ k.astype(np.float64).T
+    s = np.asarray(q, np.float64) @ np.asarray(k, np.float64).T
     if visible is not None:
         s = np.where(visible, s, -np.inf)
     s = s - s.max(axis=1, keepdims=True)
     e = np.exp(s)
-    return (e @ v.astype(np.float64)) / e.sum(axis=1, keepdims=True)
+    return (e @ np.asarray(v, np.float64)) / e.sum(axis=1, keepdims=True)
 
 
 def attn_decode(q: np.ndarray, k: np.ndarray, v: np.ndarray, lengths, scale: float) -> np.ndarray:
@@ -155,8 +155,14 @@ class Decoder:
             return f16(rms_norm(x, g, self.c.norm_eps))
         return f16(layer_norm(x, g, b, self.c.norm_eps))
 
-    def forward(self, tokens) -> np.ndarray:
-        """Runs tokens [T] (appended after the cached ones); returns logits [T, vocab]."""
+    # query rows per attention block of a long forward: a block's rows see the
+    # keys up to its last row's position only, which halves a long prompt's
+    # score work; every row's softmax covers exactly its visible keys either way
+    QUERY_BLOCK = 256
+
+    def forward(self, tokens, last_only: bool = False) -> np.ndarray:
+        """Runs tokens [T] (appended after the cached ones); returns logits
+        [T, vocab], or [1, vocab] of the last token when last_only."""
         c, w = self.c, self.w
         tokens = np.asarray(tokens, np.int64)
         T = len(tokens)
@@ -179,14 +185,18 @@ class Decoder:
             q = (q * scale).astype(np.float32)
             self.k[li] = np.concatenate([self.k[li], f16(k)])
             self.v[li] = np.concatenate([self.v[li], f16(v)])
-            K_, V_ = self.k[li], self.v[li]  # [P, KVH, d]
-            P = K_.shape[0]
+            K_ = self.k[li].astype(np.float64)  # [P, KVH, d]
+            V_ = self.v[li].astype(np.float64)
             out = np.empty((T, H, d), np.float32)
             # causal: token t (absolute pos self.pos + t) sees positions <= it
-            visible = np.arange(P)[None, :] <= (self.pos + np.arange(T))[:, None]
-            for hh in range(H):
-                kv = hh // G
-                out[:, hh, :] = attend(q[:, hh, :], K_[:, kv, :], V_[:, kv, :], visible)
+            for t0 in range(0, T, self.QUERY_BLOCK):
+                t1 = min(T, t0 + self.QUERY_BLOCK)
+                P = self.pos + t1  # keys any row of the block can see
+                visible = np.arange(P)[None, :] <= (self.pos + np.arange(t0, t1))[:, None]
+                for hh in range(H):
+                    kv = hh // G
+                    out[t0:t1, hh, :] = attend(q[t0:t1, hh, :], K_[:P, kv, :], V_[:P, kv, :],
+                                               visible)
             attn = f16(out.reshape(T, H * d))
             x = x + linear(attn, L["o"], L["o.scale"], L.get("o.bias"))
             h2 = self.norm(x, L["norm2.g"], L.get("norm2.b"))
@@ -199,6 +209,8 @@ class Decoder:
                 x = x + linear(act, L["proj"], L["proj.scale"], L.get("proj.bias"))
             x = x.astype(np.float32)
         self.pos += T
+        if last_only:
+            x = x[-1:]
         hf = self.norm(x, w.final_g, w.final_b)
         return linear(hf, w.head_w[: c.vocab], w.head_scale[: c.vocab])
 
@@ -267,7 +279,7 @@ def greedy_compare(gpu_tokens, decoder: Decoder, prompt, steps: int, logit_fn=No
     """Teacher-forced comparison: feeds the prompt, then at each step the GPU's
     token; returns (oracle argmax per step, per-step top-2 margin, oracle logits
     of each step when logit_fn is None)."""
-    logits = decoder.forward(prompt)[-1]
+    logits = decoder.forward(prompt, last_only=True)[-1]
     ours, margins, all_logits = [], [], []
     for j in range(steps):
         top = int(np.argmax(logits))
@@ -276,5 +288,5 @@ def greedy_compare(gpu_tokens, decoder: Decoder, prompt, steps: int, logit_fn=No
         margins.append(float(srt[-1] - srt[-2]))
         all_logits.append(logits)
         if j + 1 < steps:
-            logits = decoder.forward([int(gpu_tokens[j])])[-1]
+            logits = decoder.forward([int(gpu_tokens[j])], last_only=True)[-1]
     return np.array(ours), np.array(margins), all_logits

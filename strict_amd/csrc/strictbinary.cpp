@@ -244,7 +244,14 @@ struct Reader {
 // ---- readers (BinaryExecutable.cs:167-200, :278-292; BinaryType.cs:11-28,
 //      :43-62; BinaryMember.cs:9-13; BinaryMethod.cs:49-59) -----------------
 
-Value read_value(Reader &r, const NameTable &t) {
+// Values nest (a List of Lists ...); the reader recurses once per level, so
+// the depth is bounded and a deeper file is rejected rather than allowed to
+// exhaust the stack.
+constexpr int kMaxValueDepth = 256;
+
+Value read_value(Reader &r, const NameTable &t, int depth = 0) {
+  if (depth >= kMaxValueDepth)
+    throw_format(kInvalidFile, "Values nested deeper than %d levels", kMaxValueDepth);
   Value v;
   v.kind = r.byte();
   switch (v.kind) {
@@ -258,7 +265,7 @@ Value read_value(Reader &r, const NameTable &t) {
       v.text = t.at(r.seven());
       const int32_t n = r.seven();
       if (n < 0) throw_format(kInvalidFile, "Negative list length %d", n);
-      for (int32_t i = 0; i < n; i++) v.items.push_back(read_value(r, t));
+      for (int32_t i = 0; i < n; i++) v.items.push_back(read_value(r, t, depth + 1));
       break;
     }
     case kValueDictionary: {
@@ -266,8 +273,8 @@ Value read_value(Reader &r, const NameTable &t) {
       const int32_t n = r.seven();
       if (n < 0) throw_format(kInvalidFile, "Negative dictionary length %d", n);
       for (int32_t i = 0; i < n; i++) {
-        v.items.push_back(read_value(r, t));
-        v.items.push_back(read_value(r, t));
+        v.items.push_back(read_value(r, t, depth + 1));
+        v.items.push_back(read_value(r, t, depth + 1));
       }
       break;
     }
@@ -776,6 +783,12 @@ std::vector<ZipEntry> read_zip(const uint8_t *d, size_t n) {
       if (csize != usize) throw_format(kInvalidFile, "Stored entry %s has inconsistent sizes", z.name.c_str());
       z.data.assign(d + data_off, d + data_off + csize);
     } else if (method == 8) {
+      // deflate expands at most ~1032:1, so a larger declared size is a
+      // corrupt (or hostile) header; it is rejected before anything is
+      // allocated for it
+      if ((uint64_t)usize > (uint64_t)csize * 1032 + 64)
+        throw_format(kInvalidFile, "Entry %s declares %u bytes from %u compressed", z.name.c_str(),
+                     usize, csize);
       z.data.resize(usize);
       z_stream zs{};
       if (inflateInit2(&zs, -MAX_WBITS) != Z_OK) throw_format(kInvalidFile, "inflateInit2 failed");
@@ -1000,6 +1013,12 @@ SH_API int sh_strictbinary_load(const void *data, size_t bytes, sh_strictbinary 
   } catch (const FormatError &e) {
     delete b;
     return report(e);
+  } catch (const std::bad_alloc &) {
+    delete b;
+    return fail(SH_ERR_OUT_OF_MEMORY, "out of host memory reading the file");
+  } catch (const std::exception &e) {
+    delete b;
+    return fail(SH_ERR_INVALID_FILE, "InvalidFile: %s", e.what());
   }
   // the flat views point into the instructions' strings: built once the
   // types have their final place
@@ -1177,6 +1196,10 @@ SH_API int sh_strictbinary_serialize(sh_strictbinary *binary, void *data, size_t
       return report(e);
     } catch (const std::out_of_range &) {
       return fail(SH_ERR_INVALID_ARGUMENT, "a name is missing from the name table");
+    } catch (const std::bad_alloc &) {
+      return fail(SH_ERR_OUT_OF_MEMORY, "out of host memory serializing");
+    } catch (const std::exception &e) {
+      return fail(SH_ERR_INVALID_ARGUMENT, "serializing: %s", e.what());
     }
   }
   *bytes = binary->serialized.size();

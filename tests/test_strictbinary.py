@@ -369,6 +369,53 @@ def test_truncated_entry_is_invalid_file():
         sb.BinaryExecutable(data=zip_with("Number.bytecode", body[:-1]))
 
 
+def _nested_list(depth):
+    v = osb.number_list([1.0])
+    for _ in range(depth - 1):
+        v = osb.Value(osb.V_LIST, text="Strict/List(Number)", items=[v])
+    return v
+
+
+def test_deeply_nested_values_are_invalid_file():
+    # values nest one reader level per List; past 256 levels the file is
+    # rejected (a deflated entry of a few KB could otherwise nest deep
+    # enough to exhaust the stack)
+    def binary(depth):
+        return osb.write_strictbinary([run_type([
+            osb.Instr(osb.LOAD_CONSTANT, (R0,), value=_nested_list(depth)),
+            osb.Instr(osb.RETURN, (R0,))])])
+    assert len(sb.BinaryExecutable(data=binary(200)).entry_point.instructions) == 2
+    with pytest.raises(sb.InvalidFile, match="nested deeper than 256"):
+        sb.BinaryExecutable(data=binary(300))
+
+
+def test_declared_size_beyond_deflate_ratio_is_invalid_file():
+    # a central directory entry that declares ~4 GiB for a few compressed
+    # bytes is rejected before anything is allocated for it
+    body = osb.write_type(run_type([osb.Instr(osb.RETURN, (R0,))]))
+    buf = io.BytesIO()
+    with zipfile.ZipFile(buf, "w", zipfile.ZIP_DEFLATED) as z:
+        z.writestr("Number.bytecode", body)
+    data = bytearray(buf.getvalue())
+    cd = data.index(b"PK\x01\x02")
+    assert struct.unpack_from("<H", data, cd + 10)[0] == 8  # deflated
+    struct.pack_into("<I", data, cd + 24, 0xFFFFFFF0)
+    with pytest.raises(sb.InvalidFile, match="declares 4294967280 bytes"):
+        sb.BinaryExecutable(data=bytes(data))
+
+
+def test_list_longer_than_its_entry_is_invalid_file():
+    # a List declaring 2^31 - 1 items in an entry that ends after the count
+    body = osb.write_type(run_type([
+        osb.Instr(osb.LOAD_CONSTANT, (R0,), value=osb.number_list([7.0] * 3)),
+        osb.Instr(osb.RETURN, (R0,))]))
+    count = osb.seven_bit(3) + bytes([osb.V_SMALL, 7])
+    at = body.index(count)
+    cut = body[:at] + osb.seven_bit(2**31 - 1)
+    with pytest.raises(sb.InvalidFile, match="end of the stream"):
+        sb.BinaryExecutable(data=zip_with("Number.bytecode", cut))
+
+
 def test_duplicate_type_entries_are_rejected():
     buf = io.BytesIO()
     body = osb.write_type(run_type([osb.Instr(osb.RETURN, (R0,))]))
