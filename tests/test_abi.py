@@ -38,6 +38,42 @@ def test_python_binding_covers_every_symbol():
     assert set(declared_symbols()) == set(_lib.SIGNATURES)
 
 
+def _arity(params: str) -> int:
+    params = params.strip()
+    return 0 if params in ("", "void") else params.count(",") + 1
+
+
+def declared_arities():
+    out = {}
+    for h in (ROOT / "include").glob("*.h"):
+        for name, params in re.findall(r"SH_API\s+[\w\s\*]+?\b(sh_\w+)\s*\(([^)]*)\)", h.read_text()):
+            out[name] = _arity(params)
+    return out
+
+
+def csharp_bindings():
+    """name -> parameter count of every `static extern` in INTEGRATION.md's C# blocks."""
+    text = (ROOT / "INTEGRATION.md").read_text()
+    out = {}
+    for block in re.findall(r"```csharp\n(.*?)```", text, re.S):
+        block = re.sub(r"\[(?:MarshalAs|In|Out)\b[^\]]*\]", "", block)  # parameter attributes
+        for name, params in re.findall(r"static\s+extern\s+[\w\[\]\?]+\s+(sh_\w+)\s*\(([^)]*)\)", block):
+            out[name] = _arity(params)
+    return out
+
+
+def test_csharp_binding_covers_every_symbol():
+    # the P/Invoke layer a C# host adds declares every
+    # export of include/*.h, with the header's parameter count
+    declared, bound = declared_arities(), csharp_bindings()
+    assert set(declared) == set(declared_symbols())
+    missing = sorted(set(declared) - set(bound))
+    extra = sorted(set(bound) - set(declared))
+    assert not missing and not extra, (missing, extra)
+    wrong = {n: (declared[n], bound[n]) for n in declared if declared[n] != bound[n]}
+    assert not wrong, wrong
+
+
 def test_version_and_device_count():
     l = _lib.load()
     assert l.sh_version() >= 10000
