@@ -39,6 +39,11 @@
 // drains. Items of C and E sit on workgroups 0.., those of D after them and
 // the merge items on the last workgroups.
 //
+// Rounding: this file is compiled without floating-point contraction
+// (-ffp-contract=off) and writes each fused multiply-add it wants as fmaf, so
+// every instantiation (batch 1, small batch, large batch) rounds the same
+// way and a row of a batched step equals its batch-1 step bit for bit.
+//
 // With one wave per SIMD nothing hides an instruction's latency, so the item
 // code avoids runtime integer division, LDS-based lane shuffles in its
 // reductions (DPP within 16-lane rows instead) and single-wave serial loops.
@@ -427,8 +432,8 @@ __device__ __forceinline__ bool stage_rms(const LayersArgs &a, const uint64_t *x
 #pragma unroll
       for (int j = 0; j < kChunks; j++)
         if (stage_chunk_ok(K, j))
-          ss += (v[r][j][0] * v[r][j][0] + v[r][j][1] * v[r][j][1]) +
-                (v[r][j][2] * v[r][j][2] + v[r][j][3] * v[r][j][3]);
+          ss += fmaf(v[r][j][0], v[r][j][0], v[r][j][1] * v[r][j][1]) +
+                fmaf(v[r][j][2], v[r][j][2], v[r][j][3] * v[r][j][3]);
       ss = wave_sum_rows(ss);
       if (lane == 0) {
         if (r < kSmallBatchRows) misc->part[wave][r] = ss;
@@ -623,7 +628,7 @@ __device__ __forceinline__ bool o_item(const LayersArgs &a, const LayerG &P, int
 #pragma unroll
     for (int r = 0; r < kOutRows<kRows>; r++) {
       const int b = 4 * (lane >> 4) + r;
-      if (b < a.B) cst1(a.x1c, (size_t)b * a.H + i * 16 + col, bits_of(rv[r] + acc[0][r] * sc), tag);
+      if (b < a.B) cst1(a.x1c, (size_t)b * a.H + i * 16 + col, bits_of(fmaf(acc[0][r], sc, rv[r])), tag);
     }
   }
   return true;
@@ -685,7 +690,7 @@ __device__ __forceinline__ bool down_item(const LayersArgs &a, const LayerG &P, 
 #pragma unroll
     for (int r = 0; r < kOutRows<kRows>; r++) {
       const int b = 4 * (lane >> 4) + r;
-      const float v = rv[r] + acc[0][r] * sc;
+      const float v = fmaf(acc[0][r], sc, rv[r]);
       if (b < a.B) {
         // the last layer also writes the plain buffer the separate final
         // norm reads (steps whose LM head runs outside this kernel)
@@ -984,17 +989,17 @@ __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, 
       v1 = cell_f32(cv[1]);
     }
     if (wave < 3) {  // q heads and k: RMSNorm over the head, then RoPE
-      const float ss = wave_sum_rows(v0 * v0 + v1 * v1);
+      const float ss = wave_sum_rows(fmaf(v0, v0, v1 * v1));
       const float inv = 1.0f / sqrtf(ss / kD + a.eps);
       v0 = v0 * inv * g.x;
       v1 = v1 * inv * g.y;
       const float o0 = __shfl_xor(v0, 32, 64), o1 = __shfl_xor(v1, 32, 64);
       if (lane < 32) {
-        v0 = v0 * cs.x - o0 * sn.x;
-        v1 = v1 * cs.y - o1 * sn.y;
+        v0 = fmaf(v0, cs.x, -(o0 * sn.x));
+        v1 = fmaf(v1, cs.y, -(o1 * sn.y));
       } else {
-        v0 = v0 * cs.x + o0 * sn.x;
-        v1 = v1 * cs.y + o1 * sn.y;
+        v0 = fmaf(v0, cs.x, o0 * sn.x);
+        v1 = fmaf(v1, cs.y, o1 * sn.y);
       }
     }
     if (wave < 2) {
@@ -1229,9 +1234,9 @@ __device__ __forceinline__ bool merge_item(const LayersArgs &a, int l, int item,
   for (int k = 0; k < kPer; k++) {
     if (sg + kGroups * k < active) {
       const float wj = expf(cell_f32(cv[4 * k + 2]) - mg);
-      s0 += wj * cell_f32(cv[4 * k]);
-      s1 += wj * cell_f32(cv[4 * k + 1]);
-      lg += wj * cell_f32(cv[4 * k + 3]);
+      s0 = fmaf(wj, cell_f32(cv[4 * k]), s0);
+      s1 = fmaf(wj, cell_f32(cv[4 * k + 1]), s1);
+      lg = fmaf(wj, cell_f32(cv[4 * k + 3]), lg);
     }
   }
   if (q == 0) S.gm[sg] = mg;  // -inf for a group without active splits (its sums are 0)
@@ -1323,10 +1328,10 @@ __device__ __forceinline__ bool merge_run(const LayersArgs &a, int l, int hb, un
       const float wj = expf(cell_f32(cv[kC * k]) - mg);
 #pragma unroll
       for (int p = 0; p < kMergeParts; p++) {
-        s0[p] += wj * cell_f32(cv[kC * k + 2 + 2 * p]);
-        s1[p] += wj * cell_f32(cv[kC * k + 3 + 2 * p]);
+        s0[p] = fmaf(wj, cell_f32(cv[kC * k + 2 + 2 * p]), s0[p]);
+        s1[p] = fmaf(wj, cell_f32(cv[kC * k + 3 + 2 * p]), s1[p]);
       }
-      lg += wj * cell_f32(cv[kC * k + 1]);
+      lg = fmaf(wj, cell_f32(cv[kC * k + 1]), lg);
     }
   }
   if (q == 0) S.gm[sg] = mg;

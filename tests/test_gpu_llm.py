@@ -363,47 +363,100 @@ def test_qwen3_config4_greedy_256(ctx, config4):
 
 @pytest.mark.parametrize("batch", [4, 6, 8, 16])
 def test_qwen3_config4_batch_vs_oracle(ctx, config4, batch):
-    # configs[4] at batch 4 to 16: every row its own prompt, each checked
-    # against its own oracle decoder. b = 4: the small-batch kernel (staging
-    # passes of 4 rows); b = 6, 8, 16: the large-batch kernel (passes of 8
-    # rows) with runs of 6 attention items (each requests its own first K / V
-    # block) and of 8 / 16 (each stages its successor's block in LDS)
+    # configs[4] at batch 4 to 16 after 12-token prompts: every row its own
+    # prompt, each checked against its own oracle decoder, and every row's K
+    # and V^T cache entries against the oracle's. At this length each (row,
+    # KV head) has one active attention split, so every workgroup runs at
+    # most one attention item that does anything; the multi-item runs are
+    # the long-context tests below.
     m, w = config4
     prompts = np.random.default_rng(100 + batch).integers(0, QWEN_CONFIG4.vocab, (batch, 12))
     _, _, _, decs = _batch_greedy_check(m, w, prompts, 8, f"qwen3-config4-b{batch}")
     _check_kv_cache(m, decs, f"qwen3-config4-b{batch}")
 
 
-def test_qwen3_config4_batch16_kv4096_rows_match_single(ctx, config4):
-    # configs[4] at batch 16 over a 4096-token KV cache: rows from every
-    # staging pass (0, 5, 10, 15) against batch-1 runs of the same prompts
-    m, _ = config4
-    prompts = np.random.default_rng(7).integers(0, QWEN_CONFIG4.vocab, (16, 4096))
-    steps = 4
-    m.reset(16)
-    for i in range(prompts.shape[1]):
-        m.step(prompts[:, i], logits=(i == prompts.shape[1] - 1))
+def _batch_long_check(model, weights, prompts, steps, single_rows, oracle_rows, label):
+    """A batched run after long prompts against batch-1 runs of the same
+    prompts (logits bit-identical and tokens identical at every step: a
+    split's arithmetic does not depend on the batch or on which workgroup
+    runs it) and against teacher-forced oracle decoders for oracle_rows
+    (logits within LOGIT_REL_TOL, tokens identical except at near-ties)."""
+    B, T = prompts.shape
+    model.reset(B)
+    for i in range(T):
+        model.step(prompts[:, i], logits=(i == T - 1))
     toks, logits = [], []
     for j in range(steps):
-        logits.append(m.logits().copy())
-        toks.append(m.next_tokens().copy())
+        logits.append(model.logits().copy())
+        toks.append(model.next_tokens().copy())
         if j + 1 < steps:
-            m.step(None, logits=True)
-    worst = 0.0
-    for b in (0, 5, 10, 15):
-        m.reset(1)
-        for i in range(prompts.shape[1]):
-            m.step(prompts[b:b + 1, i], logits=(i == prompts.shape[1] - 1))
+            model.step(None, logits=True)
+    toks = np.array(toks)  # [steps, B]
+    for b in single_rows:
+        model.reset(1)
+        for i in range(T):
+            model.step(prompts[b:b + 1, i], logits=(i == T - 1))
         for j in range(steps):
-            single = m.logits()[0]
-            d = float(np.max(np.abs(single - logits[j][b])))
-            assert d <= LOGIT_REL_TOL * float(np.max(np.abs(single))), (b, j, d)
-            worst = max(worst, d)
-            assert int(m.next_tokens()[0]) == int(toks[j][b]), (b, j)
+            single = model.logits()[0]
+            assert np.array_equal(single, logits[j][b]), (
+                b, j, float(np.max(np.abs(single - logits[j][b]))))
+            assert int(model.next_tokens()[0]) == int(toks[j][b]), (b, j)
             if j + 1 < steps:
-                m.step(None, logits=True)
-    print(f"[qwen3-config4-b16-kv4096] rows 0/5/10/15 vs batch 1: tokens identical, "
-          f"logit max-abs-diff {worst:.3e}")
+                model.step(None, logits=True)
+    worst, ties = 0.0, 0
+    for b in oracle_rows:
+        ours, margins, ref = ollm.greedy_compare(toks[:, b], ollm.Decoder(weights), prompts[b], steps)
+        d = max(float(np.max(np.abs(g[b] - r))) for g, r in zip(logits, ref))
+        sc = max(float(np.max(np.abs(r))) for r in ref)
+        bad = toks[:, b] != ours
+        assert d <= LOGIT_REL_TOL * sc, (b, d, sc)
+        assert not np.any(bad & (margins >= 2 * d)), (b, np.nonzero(bad)[0])
+        worst, ties = max(worst, d), ties + int(bad.sum())
+    print(f"[{label}] B={B} after {T}-token prompts, {steps} steps: rows {list(single_rows)} "
+          f"bit-identical to batch 1; rows {list(oracle_rows)} vs oracle: logit max-abs-diff "
+          f"{worst:.3e}, token mismatches {ties} (all near-ties)")
+
+
+# Attention items at configs[4]'s split size (144 positions, 32 splits per
+# (row, KV head)): a context of ~2,200 positions has 16 active splits per
+# (row, KV head), one of ~4,100 has 29. The 256 workgroups' runs then are:
+#   b = 4  (small-batch kernel, the active items partitioned by a cursor):
+#          2 items each at 2,200, 3-4 at 4,100 -- later items reuse the run's
+#          q / k / v from LDS, and runs cross into the next KV head and row;
+#   b = 6  (large-batch kernel, all 1,536 items partitioned): 6 items each,
+#          runs crossing (row, KV head) pairs, inactive splits among them;
+#   b = 8  (large-batch, 4 workgroups per pair split its active splits):
+#          4 items each at 2,200;
+#   b = 12 (all 3,072 items partitioned): runs of 12, so each item stages its
+#          successor's first K / V^T block in LDS, across pair boundaries;
+#   b = 16 (2 workgroups per pair): runs of 14-15 with LDS staging at 4,100.
+# Rows always hold the same number of positions: sh_llm_step advances every
+# row of the batch by one, so no row has zero active splits while another
+# has some.
+
+@pytest.mark.parametrize("batch,rows", [(4, (0, 1, 2, 3)), (6, (0, 1, 2, 3, 4, 5)),
+                                        (8, (0, 1, 2, 3, 4, 5, 6, 7)), (12, (0, 5, 11))])
+def test_qwen3_config4_batch_long_prompt_rows(ctx, config4, batch, rows):
+    m, w = config4
+    prompts = np.random.default_rng(300 + batch).integers(0, QWEN_CONFIG4.vocab, (batch, 2200))
+    _batch_long_check(m, w, prompts, 4, rows, (batch - 1,), f"qwen3-config4-b{batch}-kv2200")
+
+
+def test_qwen3_config4_batch4_kv4096(ctx, config4):
+    # BASELINE configs[4] at batch 4 against a 4096-token KV cache: every row
+    # against batch 1, row 0 against the oracle
+    m, w = config4
+    prompts = np.random.default_rng(11).integers(0, QWEN_CONFIG4.vocab, (4, 4096))
+    _batch_long_check(m, w, prompts, 4, (0, 1, 2, 3), (0,), "qwen3-config4-b4-kv4096")
+
+
+def test_qwen3_config4_batch16_kv4096(ctx, config4):
+    # BASELINE configs[4] at batch 16 against a 4096-token KV cache: rows from
+    # both staging passes of the GEMV items (0-7, 8-15) against batch 1, row
+    # 15 against the oracle
+    m, w = config4
+    prompts = np.random.default_rng(7).integers(0, QWEN_CONFIG4.vocab, (16, 4096))
+    _batch_long_check(m, w, prompts, 4, (0, 5, 10, 15), (15,), "qwen3-config4-b16-kv4096")
 
 
 def test_qwen3_long_context_step(ctx, config4):
