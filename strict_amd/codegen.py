@@ -51,6 +51,8 @@ class InstructionType(enum.IntEnum):
     GreaterThan = 24
     Invoke = 31
     Return = 32
+    LoopBegin = 33
+    LoopEnd = 34
 
 
 REGISTER_COUNT = 16  # Register.cs: R0 .. R15
