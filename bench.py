@@ -512,6 +512,116 @@ def cpu_baseline_image_rows():
     return res
 
 
+GPU_FACTOR = 0.97  # TestPerformance.CudaGpuAndCpu's GpuFactor (TestPerformance.cs:56)
+
+
+def _download_into(ctx, host: np.ndarray, dev) -> None:
+    """Device bytes into an existing host array (sh_download, synchronous)."""
+    import ctypes
+
+    from strict_amd import _check
+
+    _check(ctx._l.sh_download(ctx.handle, host.ctypes.data_as(ctypes.c_void_p),
+                              ctypes.c_void_p(dev.ptr), host.nbytes))
+
+
+def gpu_and_cpu_modes(ctx, nt: int, reps: int = 5) -> dict:
+    """TestPerformance's CudaGpuAndCpu mode (TestPerformance.cs:53-61) for the
+    sigmoid, brightness, box-blur and fused rows: the HIP kernel runs the first
+    97 % of the work and its results are copied to host memory (the reference's
+    RunGpu leg ends with that copy, Cuda BlurPerformanceTests.cs:171-178), while
+    the C restatement runs the remaining 3 % as ParallelCpuChunks on the host
+    threads; the wall time of both, median of `reps`. Blur rows: the GPU share
+    is whole rows, computed over two more rows (their bottom-edge taps) that are
+    discarded. The combined output is checked against the GPU's whole result
+    (bit-exact; sigmoid's CPU share within 2 ulp)."""
+    import threading
+
+    import oracle
+    import strict_amd
+
+    rng = np.random.default_rng(7)
+    out = {}
+
+    def timed(gpu_leg, cpu_leg):
+        ts = []
+        for _ in range(reps + 1):  # the first is a warmup
+            th = threading.Thread(target=gpu_leg)
+            t0 = time.perf_counter()
+            th.start()
+            cpu_leg()
+            th.join()
+            ts.append((time.perf_counter() - t0) * 1e3)
+        return float(np.median(ts[1:]))
+
+    # sigmoid: elements [0, ng) on the GPU, [ng, N) on the CPU
+    x = rng.uniform(-8, 8, SIGMOID_N).astype(np.float32)
+    ng = int(SIGMOID_N * GPU_FACTOR) // 16 * 16
+    dx, dy = ctx.upload(x), ctx.empty(x.shape, np.float32)
+    y = np.zeros_like(x)
+
+    def sig_gpu():
+        ctx.sigmoid(dx, dy, ng)
+        _download_into(ctx, y[:ng], dy)
+
+    ms = timed(sig_gpu, lambda: oracle.perf_sigmoid(3, x[ng:], y[ng:], nt))
+    ctx.sigmoid(dx, dy, SIGMOID_N)
+    full = dy.to_host()
+    ulps = np.abs(y.view(np.int32).astype(np.int64) - full.view(np.int32).astype(np.int64))
+    assert np.array_equal(y[:ng], full[:ng]) and ulps.max() <= 2, "CudaGpuAndCpu sigmoid"
+    out["sigmoid"] = (ms, 8 * SIGMOID_N, f"{ng} elements on the GPU, {SIGMOID_N - ng} on the CPU")
+    for v in (dx, dy):
+        v.free()
+
+    # image rows: rows [0, R) on the GPU, [R, H) on the CPU
+    img = rng.integers(0, 256, IMG_BYTES, dtype=np.uint8)
+    R = int(IMG_H * GPU_FACTOR)
+    row = IMG_W * 4
+    src, dst = ctx.upload(img), ctx.empty(img.shape, np.uint8)
+    host = np.zeros_like(img)
+    cases = [
+        ("brightness", lambda h: ctx.adjust_brightness(src, dst, IMG_W, h, 4, 40, 0),
+         lambda: oracle.perf_brightness(3, img[R * row:], host[R * row:], 4, 40, nt,
+                                        pixels=(IMG_H - R) * IMG_W), 0),
+        ("box_blur", lambda h: ctx.box_blur5(src, dst, IMG_W, h, 4, strict_amd.BLUR_CONFIG),
+         lambda: oracle.perf_blur5_from(3, oracle.BLUR_CONFIG, img, host, IMG_W, IMG_H, 4, nt,
+                                        first=R * IMG_W, pixels=(IMG_H - R) * IMG_W), 2),
+        ("fused", lambda h: ctx.brightness_blur5(src, dst, IMG_W, h, 4, 40, 0,
+                                                 strict_amd.BLUR_CONFIG),
+         lambda: oracle.perf_blur5_from(3, oracle.BLUR_FUSED, img, host, IMG_W, IMG_H, 4, nt,
+                                        first=R * IMG_W, pixels=(IMG_H - R) * IMG_W, delta=40), 2),
+    ]
+    for name, gpu_op, cpu_leg, halo in cases:
+        host[:] = 0
+
+        def gpu_leg():
+            gpu_op(R + halo)
+            _download_into(ctx, host[:R * row], dst)
+
+        ms = timed(gpu_leg, cpu_leg)
+        gpu_op(IMG_H)
+        assert np.array_equal(host, dst.to_host()), f"CudaGpuAndCpu {name}"
+        out[name] = (ms, 2 * IMG_BYTES, f"rows 0..{R - 1} on the GPU, {R}..{IMG_H - 1} on the CPU")
+    for v in (src, dst):
+        v.free()
+    return out
+
+
+def add_gpu_and_cpu(entry: dict, mode: tuple) -> dict:
+    """A cpu_baseline with TestPerformance's CudaGpuAndCpu beside its four CPU
+    modes (not part of `value`, which stays the best CPU-only mode)."""
+    ms, nbytes, split = mode
+    e = dict(entry)
+    e["modes"] = dict(e["modes"], CudaGpuAndCpu=round(nbytes / 1e6 / ms, 4))
+    e["modes_ms"] = dict(e["modes_ms"], CudaGpuAndCpu=round(ms, 3))
+    e["CudaGpuAndCpu"] = (f"TestPerformance.CudaGpuAndCpu (TestPerformance.cs:53-61) over the whole "
+                          f"config input: {split} (ParallelCpuChunks, {e['cores']} threads) at "
+                          f"once, the GPU share's results copied to host memory as the "
+                          f"reference's RunGpu does; wall time, median of 5; output checked "
+                          f"against the GPU's whole result")
+    return e
+
+
 def cpu_baseline_gemm():
     """The oracle's fp32 product (numpy BLAS) of the 4096^3 operands: the
     reference has no GEMM, so the build's own fp32 path is the baseline."""
@@ -593,13 +703,17 @@ def cpu_baseline_gpt2(seconds: float):
                       f"{t_total:.1f} s"}
 
 
-def attach_cpu_baselines(kernels, headline_cpu, seconds):
+def attach_cpu_baselines(kernels, headline_cpu, seconds, both=None):
     """One cpu_baseline per kernels[] row (reported beside the GPU figure, not a target)."""
     rows = {}
     log("cpu baselines: image rows (TestPerformance modes)")
     img = cpu_baseline_image_rows()
     log("cpu baselines: sigmoid")
     rows["sigmoid"] = cpu_baseline_sigmoid()
+    if both:
+        rows["sigmoid"] = add_gpu_and_cpu(rows["sigmoid"], both["sigmoid"])
+        for key in ("brightness", "box_blur", "fused"):
+            img[key] = add_gpu_and_cpu(img[key], both[key])
     log("cpu baselines: GEMM / GEMV")
     gemm = cpu_baseline_gemm()
     gemv = cpu_baseline_gemv()
@@ -763,6 +877,11 @@ def main() -> int:
                     "frac": round(achieved / HBM_PEAK_GBS, 4),
                     "traffic": read_traffic("sigmoid_f32")}
         warmup = 5
+    both = None
+    if not args.no_cpu_baseline and (kernels or args.workload == "image"):
+        log("CudaGpuAndCpu mode (97 % GPU, 3 % CPU)")
+        both = gpu_and_cpu_modes(ctx, cpu_threads())
+        log(f"CudaGpuAndCpu: { {k: round(v[0], 3) for k, v in both.items()} } ms")
     from strict_amd import yardstick
 
     yardstick.release()  # hipBLASLt handles and workspace, before the context goes
@@ -776,7 +895,7 @@ def main() -> int:
             cpu = cpu_baseline_sigmoid()
         log(f"cpu baseline: {cpu}")
         if kernels or args.workload == "image":
-            img_rows = attach_cpu_baselines(kernels, cpu, args.cpu_seconds)
+            img_rows = attach_cpu_baselines(kernels, cpu, args.cpu_seconds, both)
             if args.workload == "image":
                 cpu = img_rows["fused"]
 

@@ -73,6 +73,8 @@ def _declare(l) -> None:
     l.or_perf_brightness.restype = d
     l.or_perf_blur5.argtypes = [i, i, P, P, i, i, i, i, lg, i, i]
     l.or_perf_blur5.restype = d
+    l.or_perf_blur5_from.argtypes = [i, i, P, P, i, i, i, i, lg, lg, i, i]
+    l.or_perf_blur5_from.restype = d
     l.or_perf_cross_blur.argtypes = [i, P, i, i, lg, i, i]
     l.or_perf_cross_blur.restype = d
 
@@ -259,6 +261,14 @@ def perf_blur5(mode: int, kind: int, img, out, width: int, height: int, channels
     n = width * height if pixels is None else pixels
     return lib().or_perf_blur5(mode, kind, _p(img), _p(out), width, height, channels, delta, n,
                                chunk, nthreads)
+
+
+def perf_blur5_from(mode: int, kind: int, img, out, width: int, height: int, channels: int,
+                    nthreads: int, first: int, pixels: int, delta: int = 0,
+                    chunk: int = CHUNK_SIZE) -> float:
+    """ms for one mode over output pixels [first, first + pixels) (a CudaGpuAndCpu CPU share)."""
+    return lib().or_perf_blur5_from(mode, kind, _p(img), _p(out), width, height, channels, delta,
+                                    first, pixels, chunk, nthreads)
 
 
 def perf_cross_blur(mode: int, image, width: int, height: int, iterations: int, nthreads: int,

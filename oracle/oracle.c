@@ -332,6 +332,7 @@ typedef struct {
   const uint8_t *in;
   uint8_t *out;
   int width, height, channels, delta, kind;
+  long first; /* index 0 is output pixel `first` */
 } blur_px_ctx;
 
 static void blur_pixel(const blur_px_ctx *c, int row, int col) {
@@ -361,14 +362,24 @@ static void blur_pixel(const blur_px_ctx *c, int row, int col) {
 
 __attribute__((noinline)) static void blur_chunk(void *p, long start, long chunk) {
   const blur_px_ctx *c = (const blur_px_ctx *)p;
-  for (long n = start; n < start + chunk; n++) blur_pixel(c, (int)(n / c->width), (int)(n % c->width));
+  for (long n = c->first + start; n < c->first + start + chunk; n++)
+    blur_pixel(c, (int)(n / c->width), (int)(n % c->width));
 }
 
 double or_perf_blur5(int mode, int kind, const uint8_t *in, uint8_t *out, int width, int height,
                      int channels, int delta, long pixels, int chunk, int nthreads) {
-  blur_px_ctx c = {in, out, width, height, channels, delta, kind};
+  return or_perf_blur5_from(mode, kind, in, out, width, height, channels, delta, 0, pixels, chunk,
+                            nthreads);
+}
+
+double or_perf_blur5_from(int mode, int kind, const uint8_t *in, uint8_t *out, int width,
+                          int height, int channels, int delta, long first, long pixels, int chunk,
+                          int nthreads) {
+  blur_px_ctx c = {in, out, width, height, channels, delta, kind, first};
   long total = (long)width * (long)height;
-  return perf_run(mode, pixels < total ? pixels : total, chunk, blur_chunk, &c, nthreads);
+  if (first < 0 || first > total) return -1.0;
+  if (pixels > total - first) pixels = total - first;
+  return perf_run(mode, pixels, chunk, blur_chunk, &c, nthreads);
 }
 
 /* The CUDA harness's CPU blur (Strict.Compiler.Cuda.Tests/BlurPerformanceTests.cs:160-169):

@@ -81,6 +81,11 @@ double or_perf_brightness(int mode, const uint8_t *in, uint8_t *out, long pixels
  * the taps brightened by delta on channels 0..2 (the fused brightness + blur) */
 double or_perf_blur5(int mode, int kind, const uint8_t *in, uint8_t *out, int width, int height,
                      int channels, int delta, long pixels, int chunk, int nthreads);
+/* the same over output pixels [first, first + pixels) (index n is pixel first + n):
+ * the CPU share of TestPerformance's CudaGpuAndCpu mode (TestPerformance.cs:53-61) */
+double or_perf_blur5_from(int mode, int kind, const uint8_t *in, uint8_t *out, int width,
+                          int height, int channels, int delta, long first, long pixels, int chunk,
+                          int nthreads);
 /* Cuda.Tests/BlurPerformanceTests.cs:160-169: the in-place 5-point cross /5
  * over the RGBA byte stream, indices modulo width * height * 4, chunks
  * starting below width * 4 skipped; the reference runs width * height * 100

@@ -302,6 +302,27 @@ def test_perf_modes_brightness_and_blurs_equal_the_image_oracles(mode):
         assert not out[n * 4:].any()
 
 
+@pytest.mark.parametrize("mode", range(4))
+def test_perf_blur5_from_covers_the_tail_rows(mode):
+    # the CPU share of CudaGpuAndCpu: output pixels [first, first + pixels)
+    # of the whole image, its clamp-to-edge / in-bounds taps reaching above
+    # `first`; pixels outside the range untouched
+    w, h = 37, 29
+    img = np.random.default_rng(3).integers(0, 256, w * h * 4, dtype=np.uint8)
+    first = 25 * w + 3
+    n = _chunked_prefix(w * h - first, mode)
+    for kind, delta, ref in [(oracle.BLUR_REFERENCE, 0, oracle.blur5_reference(img, w, h, 4)),
+                             (oracle.BLUR_CONFIG, 0, oracle.blur5_config(img, w, h, 4)),
+                             (oracle.BLUR_FUSED, -40,
+                              oracle.brightness_blur5_config(img, w, h, -40, 4))]:
+        out = np.zeros_like(img)
+        oracle.perf_blur5_from(mode, kind, img, out, w, h, 4, nthreads=3, first=first,
+                               pixels=w * h - first, delta=delta)
+        lo, hi = first * 4, (first + n) * 4
+        assert np.array_equal(out[lo:hi], ref[lo:hi]), kind
+        assert not out[:lo].any() and not out[hi:].any()
+
+
 def test_cross_blur_hand_worked_single_thread():
     # Cuda.Tests/BlurPerformanceTests.cs:160-169 worked by hand on a 2x1 RGBA
     # image (size 8, width * 4 = 8): indices 0..7 are skipped (:162), and for
