@@ -125,9 +125,13 @@ class Weights:
         self.inv_freq = inv_freq
 
 
-def linear(h16: np.ndarray, w: np.ndarray, scale: np.ndarray, bias=None) -> np.ndarray:
-    """(h16 @ w.T) * scale (+ bias), fp32."""
-    y = (h16.astype(np.float32) @ w.T).astype(np.float32) * scale.astype(np.float32)
+def linear(h16: np.ndarray, w: np.ndarray, scale: np.ndarray, bias=None,
+           accumulate=np.float32) -> np.ndarray:
+    """(h16 @ w.T) * scale (+ bias), fp32. The dot products are summed in
+    `accumulate` (fp32 BLAS by default; np.float64 gives the exactly rounded
+    sum of the exact products, a second valid order used to show how far two
+    correct implementations drift apart through fp16 re-rounding)."""
+    y = (h16.astype(accumulate) @ w.T.astype(accumulate)).astype(np.float32) * scale.astype(np.float32)
     if bias is not None:
         y = y + bias.astype(np.float32)
     return y.astype(np.float32)
@@ -136,8 +140,9 @@ def linear(h16: np.ndarray, w: np.ndarray, scale: np.ndarray, bias=None) -> np.n
 class Decoder:
     """Greedy decoder over one sequence with a KV cache."""
 
-    def __init__(self, weights: Weights):
+    def __init__(self, weights: Weights, accumulate=np.float32):
         self.w = weights
+        self.acc = accumulate  # the linears' summation type (see linear)
         c = weights.cfg
         self.c = c
         self.k = [np.zeros((0, c.kv_heads, c.head_dim), np.float32) for _ in range(c.layers)]
@@ -175,7 +180,7 @@ class Decoder:
         scale = np.float32(1.0 / np.sqrt(np.float32(d)))
         for li, L in enumerate(w.layers):
             h = self.norm(x, L["norm1.g"], L.get("norm1.b"))
-            qkv = linear(h, L["qkv"], L["qkv.scale"], L.get("qkv.bias"))
+            qkv = linear(h, L["qkv"], L["qkv.scale"], L.get("qkv.bias"), self.acc)
             q = qkv[:, : H * d].reshape(T, H, d)
             k = qkv[:, H * d:(H + KVH) * d].reshape(T, KVH, d)
             v = qkv[:, (H + KVH) * d:].reshape(T, KVH, d)
@@ -198,21 +203,21 @@ class Decoder:
                     out[t0:t1, hh, :] = attend(q[t0:t1, hh, :], K_[:P, kv, :], V_[:P, kv, :],
                                                visible)
             attn = f16(out.reshape(T, H * d))
-            x = x + linear(attn, L["o"], L["o.scale"], L.get("o.bias"))
+            x = x + linear(attn, L["o"], L["o.scale"], L.get("o.bias"), self.acc)
             h2 = self.norm(x, L["norm2.g"], L.get("norm2.b"))
             if c.arch == QWEN3:
-                gu = linear(h2, L["gate_up"], L["gate_up.scale"])
+                gu = linear(h2, L["gate_up"], L["gate_up.scale"], None, self.acc)
                 act = f16(silu(gu[:, : c.intermediate]) * gu[:, c.intermediate:])
-                x = x + linear(act, L["down"], L["down.scale"])
+                x = x + linear(act, L["down"], L["down.scale"], None, self.acc)
             else:
-                act = f16(gelu_tanh(linear(h2, L["fc"], L["fc.scale"], L.get("fc.bias"))))
-                x = x + linear(act, L["proj"], L["proj.scale"], L.get("proj.bias"))
+                act = f16(gelu_tanh(linear(h2, L["fc"], L["fc.scale"], L.get("fc.bias"), self.acc)))
+                x = x + linear(act, L["proj"], L["proj.scale"], L.get("proj.bias"), self.acc)
             x = x.astype(np.float32)
         self.pos += T
         if last_only:
             x = x[-1:]
         hf = self.norm(x, w.final_g, w.final_b)
-        return linear(hf, w.head_w[: c.vocab], w.head_scale[: c.vocab])
+        return linear(hf, w.head_w[: c.vocab], w.head_scale[: c.vocab], None, self.acc)
 
 
 def load_from_model(model) -> Weights:

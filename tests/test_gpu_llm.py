@@ -163,6 +163,17 @@ def _greedy_check(model, prompt, steps, label):
     print(f"[{label}] {steps} steps: logit max-abs-diff {max_diff:.3e} (max |logit| {scale:.3f}), "
           f"token mismatches {int(mismatch.sum())} (near-ties {ties}), "
           f"min top-2 margin {margins.min():.3e}")
+    if mismatch.any():
+        # second opinion at the near-ties: the oracle again with every linear
+        # summed in fp64 (another valid summation order); how far the two
+        # oracles drift apart is the precision floor of fp16 activations
+        ours64, _, ref64 = ollm.greedy_compare(gpu_tokens, ollm.Decoder(weights, np.float64),
+                                               np.asarray(prompt), steps)
+        floor = max(float(np.max(np.abs(a - b))) for a, b in zip(ref_logits, ref64))
+        sides = int(np.sum(mismatch & (ours64 == gpu_tokens)))
+        print(f"[{label}] fp32-summed vs fp64-summed oracle: logit max-abs-diff {floor:.3e}; "
+              f"at the {int(mismatch.sum())} mismatched step(s) the fp64-summed oracle picks "
+              f"the GPU's token {sides} time(s)")
     assert max_diff <= LOGIT_REL_TOL * scale, (max_diff, scale)
     assert not np.any(mismatch & (margins >= 2 * max_diff)), np.nonzero(mismatch)[0]
     return max_diff, ties

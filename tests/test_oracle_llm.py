@@ -110,11 +110,23 @@ def _assert_close(ours, ref):
     return err / scale
 
 
+@pytest.mark.parametrize("acc", [np.float32, np.float64], ids=["fp32-sums", "fp64-sums"])
 @pytest.mark.parametrize("pair", [_qwen3_pair, _gpt2_pair])
-def test_oracle_prefill_matches_transformers(pair):
+def test_oracle_prefill_matches_transformers(pair, acc):
+    # both summation orders of the linears (the second-opinion decoder the
+    # GPU tests consult at near-ties sums in fp64)
     model, w = pair()
     tokens = np.random.default_rng(1).integers(0, w.cfg.vocab, 24)
-    _assert_close(ollm.Decoder(w).forward(tokens), _hf_logits(model, tokens))
+    _assert_close(ollm.Decoder(w, accumulate=acc).forward(tokens), _hf_logits(model, tokens))
+
+
+def test_linear_fp64_sums_match_double_precision_sums():
+    rng = np.random.default_rng(4)
+    h = rng.normal(0, 1, (3, 64)).astype(np.float16).astype(np.float32)
+    w = rng.normal(0, 0.02, (5, 64)).astype(np.float32)
+    exact = np.array([[sum(float(a) * float(b) for a, b in zip(hr, wr)) for wr in w] for hr in h])
+    got = ollm.linear(h, w, np.ones(5, np.float32), accumulate=np.float64)
+    assert np.array_equal(got, exact.astype(np.float32))
 
 
 @pytest.mark.parametrize("pair", [_qwen3_pair, _gpt2_pair])
