@@ -554,9 +554,12 @@ def gpu_and_cpu_modes(ctx, nt: int, reps: int = 5) -> dict:
             ts.append((time.perf_counter() - t0) * 1e3)
         return float(np.median(ts[1:]))
 
-    # sigmoid: elements [0, ng) on the GPU, [ng, N) on the CPU
+    # sigmoid: elements [0, ng) on the GPU, [ng, N) on the CPU. ParallelCpuChunks
+    # runs whole chunks of 100 only (TestPerformance.cs:47-48), so the CPU share
+    # is a multiple of 400 (100 per chunk, and ng 16-byte aligned: N % 16 == 0)
     x = rng.uniform(-8, 8, SIGMOID_N).astype(np.float32)
-    ng = int(SIGMOID_N * GPU_FACTOR) // 16 * 16
+    cpu_n = int(round(SIGMOID_N * (1 - GPU_FACTOR) / 400)) * 400
+    ng = SIGMOID_N - cpu_n
     dx, dy = ctx.upload(x), ctx.empty(x.shape, np.float32)
     y = np.zeros_like(x)
 
@@ -575,7 +578,9 @@ def gpu_and_cpu_modes(ctx, nt: int, reps: int = 5) -> dict:
 
     # image rows: rows [0, R) on the GPU, [R, H) on the CPU
     img = rng.integers(0, 256, IMG_BYTES, dtype=np.uint8)
-    R = int(IMG_H * GPU_FACTOR)
+    # whole rows; the CPU rows times the width a multiple of the chunk of 100
+    step = 100 // np.gcd(IMG_W, 100)
+    R = IMG_H - int(np.ceil(IMG_H * (1 - GPU_FACTOR) / step)) * step
     row = IMG_W * 4
     src, dst = ctx.upload(img), ctx.empty(img.shape, np.uint8)
     host = np.zeros_like(img)
