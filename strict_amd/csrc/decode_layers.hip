@@ -122,15 +122,24 @@ __device__ __forceinline__ unsigned ld_err(const unsigned *p) {
 
 // Cell stores are relaxed agent-scope atomics (global stores with the
 // device-scope cache policy): once complete they are visible to every CU.
-__device__ __forceinline__ void cst1(uint64_t *base, size_t cell, uint32_t v, unsigned tag) {
-  __hip_atomic_store(base + cell, (uint64_t)v | ((uint64_t)tag << 32), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
+// `local`: a workgroup-scope store instead, which lands in the XCD's L2 and
+// stays there; the agent-scope polls of the same XCD's CUs see it (one hop
+// ~0.22 us against ~0.4-0.53 us measured in a ping-pong between workgroups),
+// those of other XCDs do not until the kernel ends. Only for cells whose
+// every consumer runs on the producer's XCD.
+__device__ __forceinline__ void cst1(uint64_t *base, size_t cell, uint32_t v, unsigned tag,
+                                     bool local = false) {
+  const uint64_t c = (uint64_t)v | ((uint64_t)tag << 32);
+  if (local)
+    __hip_atomic_store(base + cell, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  else
+    __hip_atomic_store(base + cell, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ void cst2(uint64_t *base, size_t cell, uint32_t v0, uint32_t v1,
-                                     unsigned tag) {
-  cst1(base, cell, v0, tag);
-  cst1(base, cell + 1, v1, tag);
+                                     unsigned tag, bool local = false) {
+  cst1(base, cell, v0, tag, local);
+  cst1(base, cell + 1, v1, tag, local);
 }
 
 __device__ __forceinline__ float f32_of(uint32_t u) { return __builtin_bit_cast(float, u); }
@@ -572,10 +581,11 @@ __device__ __forceinline__ void consume_cells(const uint64_t (&c)[4]) {
 }
 
 // A: qkv[b][16 i + c] = scale * (W_qkv RMSNorm(x)); w holds the item's
-// weights (load_weights, issued by the caller)
+// weights (load_weights, issued by the caller); local: every consumer of the
+// cells runs on this XCD (cst1)
 template <int kL, int kRows>
 __device__ __forceinline__ bool qkv_item(const LayersArgs &a, const LayerG &P, int l, int i, unsigned ep,
-                         const Lds &s, const u32x4 (&w)[kL][1], bool reuse) {
+                         const Lds &s, const u32x4 (&w)[kL][1], bool reuse, bool local) {
   const int lane = threadIdx.x & 63, col = lane & 15;
   const float sc = P.sqkv[i * 16 + col];
   __builtin_amdgcn_sched_barrier(0);
@@ -598,7 +608,7 @@ __device__ __forceinline__ bool qkv_item(const LayersArgs &a, const LayerG &P, i
 #pragma unroll
     for (int r = 0; r < kOutRows<kRows>; r++) {
       const int b = 4 * (lane >> 4) + r;
-      if (b < a.B) cst1(a.qkvc, (size_t)b * a.qkv_n + i * 16 + col, bits_of(acc[0][r] * sc), tag);
+      if (b < a.B) cst1(a.qkvc, (size_t)b * a.qkv_n + i * 16 + col, bits_of(acc[0][r] * sc), tag, local);
     }
   }
   SH_MARK(s.misc, l, 3);
@@ -918,8 +928,9 @@ __device__ __forceinline__ void append_new(const LayersArgs &a, SH_GLOBAL uint16
 // kG query heads of the KV head (Qwen3: RMSNorm of q and of the new k over
 // the head, RoPE rotate-half at this step's position; the split holding it
 // appends the new k / v to the cache) and writes the partial (unnormalised
-// V sum, max, sum) of each head as cells. Splits past the context write
-// nothing. `runs`: the workgroup runs several items (staged: this item's
+// V sum, max, sum) of each head as cells (local: every consumer of them
+// runs on this XCD, cst1). Splits past the context write nothing. `runs`:
+// the workgroup runs several items (staged: this item's
 // first block was staged in LDS by the previous one; next: the item whose
 // block this one stages, or -1). With `reuse`, the workgroup's previous
 // item was the split
@@ -929,7 +940,7 @@ __device__ __forceinline__ void append_new(const LayersArgs &a, SH_GLOBAL uint16
 template <int kG>
 __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, int l, int item, unsigned ep,
                           uint8_t *smem, Misc *misc, AttnKV &kv, bool runs, bool reuse, bool staged,
-                          int next) {
+                          int next, bool local) {
   static_assert((kG + 2) * kD / 2 <= kT, "one pair of q / k / v cells per thread");
   static_assert(kG <= 4, "MFMA rows 0..3 of lanes 0..15 hold the heads");
   AttnLds<kG> &S = *reinterpret_cast<AttnLds<kG> *>(smem);
@@ -1174,12 +1185,13 @@ __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, 
     for (int g = 0; g < kG; g++) {
       const size_t pp = (((size_t)b * a.heads + h0 + g) * splits + s) * kPStride;
 #pragma unroll
-      for (int nt = 0; nt < 2; nt++) cst1(a.partc, pp + 32 * wave + 16 * nt + lane, bits_of(oacc[nt][g]), tag);
+      for (int nt = 0; nt < 2; nt++)
+        cst1(a.partc, pp + 32 * wave + 16 * nt + lane, bits_of(oacc[nt][g]), tag, local);
     }
   }
   if (t < kG) {
     const size_t pp = (((size_t)b * a.heads + h0 + t) * splits + s) * kPStride;
-    cst2(a.partc, pp + kD, bits_of(M[t]), bits_of(lsum[t]), tag);
+    cst2(a.partc, pp + kD, bits_of(M[t]), bits_of(lsum[t]), tag, local);
   }
   SH_MARK(misc, l, 13);
   return true;
@@ -1519,7 +1531,26 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
   const int nA = a.qkv_n / 16, nB = B * a.kv_heads * a.splits, nM = B * a.heads * kMergeParts;
   const int nC = H / 16, nD = a.inter / 16, nE = H / 16;
   const int d0 = (w + G - nC % G) % G;  // this workgroup's first gate/up item
-  const int m0 = G - 1 - w;             // its first merge item
+  // XCD-local placement (batch 1, a.xcd): workgroup w = h + 8 j, on XCD h
+  // (workgroups go to the XCDs round robin), runs KV head h's j-th QKV tile
+  // (its kG query heads' q tiles, then its k, then its v tiles), its split j
+  // and, on the last kG * kMergeParts workgroups of the XCD, its query
+  // heads' merge items: the QKV -> attention and attention -> merge cells
+  // never leave the XCD.
+  const bool xl = kOne && a.xcd != 0;
+  const int xh = w & 7, xj = w >> 3, xw = G >> 3;
+  constexpr int kTiles = kD / 16;  // 16-row tiles per head
+  const int xq = xj < kG * kTiles ? xh * kG * kTiles + xj
+                 : xj < (kG + 1) * kTiles ? a.heads * kTiles + xh * kTiles + (xj - kG * kTiles)
+                                          : (a.heads + a.kv_heads) * kTiles + xh * kTiles +
+                                                (xj - (kG + 1) * kTiles);
+  const int xm = xj >= xw - kG * kMergeParts ? xh * kG * kMergeParts + (xj - (xw - kG * kMergeParts)) : nM;
+  const int m0 = xl ? xm : G - 1 - w;  // its first merge item
+  if (xl && threadIdx.x == 0) {
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    if ((xcc & 0xf) != (unsigned)xh) atomicOr(a.err, 2u);  // every wait then fails at once
+  }
   const bool hasC = w < nC;
   // attention items: workgroup w runs items [bA, eA), one at batch 1; at
   // larger batches a contiguous run of the active items (splits within
@@ -1537,8 +1568,8 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
     nAct = 0;
     for (int b = 0; b < B; b++) nAct += attn_active(a, b) * a.kv_heads;
   }
-  int bA = kOne ? w : (int)((int64_t)w * nAct / G);
-  int eA = kOne ? min(w + 1, nB) : (int)((int64_t)(w + 1) * nAct / G);
+  int bA = kOne ? (xl ? xh * a.splits + xj : w) : (int)((int64_t)w * nAct / G);
+  int eA = kOne ? min(bA + 1, nB) : (int)((int64_t)(w + 1) * nAct / G);
   if constexpr (!kOne && !kAct) {
     // large-batch variant: when the grid divides into the (row, KV head)
     // pairs, each pair's workgroups split its active splits evenly (runs
@@ -1594,7 +1625,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
   // consecutive tiles per workgroup [bQ, eQ) on one staged input, so each
   // input row is read by half as many workgroups
   const int gQ = kPre ? G : min(G, (nA + 1) / 2);
-  const int bQ = kPre ? w : (w < gQ ? (int)((int64_t)w * nA / gQ) : nA);
+  const int bQ = kPre ? (xl ? xq : w) : (w < gQ ? (int)((int64_t)w * nA / gQ) : nA);
   const int eQ = kPre ? nA : (w < gQ ? (int)((int64_t)(w + 1) * nA / gQ) : nA);
   const bool hasQ = bQ < eQ;
   AttnKV kv;
@@ -1607,11 +1638,11 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
     auto qkv_one = [&](int i) {
       if (i != bQ) load_weights<kLA, 1>(wa, P.wqkv, H, i);
       if (i == bQ) SH_TRACE(misc, l, 0);
-      if (!qkv_item<kLA, kRows>(a, P, l, i, ep, lds, wa, !kPre && i != bQ)) return false;
+      if (!qkv_item<kLA, kRows>(a, P, l, i, ep, lds, wa, !kPre && i != bQ, xl)) return false;
       if (i == bQ) { SH_TRACE(misc, l, 1); SH_TRACE_WAIT(l, 0, misc); }
       return true;
     };
-    if (kPre ? !for_items<kOne>(w, nA, G, qkv_one) : !for_run<false>(bQ, eQ, qkv_one)) return;
+    if (kPre ? !for_items<kOne>(bQ, nA, G, qkv_one) : !for_run<false>(bQ, eQ, qkv_one)) return;
     SH_MARK(misc, l, 16);
     // the run's first block was requested into registers before the phase;
     // in runs of kStageRun items or more every later one is staged in LDS by
@@ -1640,7 +1671,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
         const bool reuse = !kOne && k != bA && i % a.splits != 0;
         const int nx = kStg && k + 1 < eA ? (kOne || kAct ? item_at(nxt) : k + 1) : -1;
         const bool staged = kStg && (k != bA || !kPre);
-        if (!attn_item<kG>(a, P, l, i, ep, smem, misc, kv, kStg, reuse, staged, nx)) return false;
+        if (!attn_item<kG>(a, P, l, i, ep, smem, misc, kv, kStg, reuse, staged, nx, xl)) return false;
         if (k == bA) { SH_TRACE(misc, l, 3); SH_TRACE_WAIT(l, 1, misc); }
         if (k - bA < 8) SH_TRACE(misc, l, 16 + (k - bA));  // the run's first eight items' ends
         return true;
@@ -1784,6 +1815,13 @@ size_t attn_lds(int g) {
 }
 
 }  // namespace
+
+bool decode_layers_xcd_ok(const LayersArgs &a, int grid) {
+  if (a.B != 1 || grid % 8 != 0 || a.kv_heads != 8 || a.heads % a.kv_heads != 0) return false;
+  const int per = grid / 8, g = a.heads / a.kv_heads;
+  return a.splits == per && (g + 2) * (kD / 16) == per && g * kMergeParts <= per &&
+         a.qkv_n == (a.heads + 2 * a.kv_heads) * kD && one_item_each(a, grid);
+}
 
 bool decode_layers_supported(int layers, int H, int heads, int kv_heads, int head_dim, int inter) {
   if (layers < 1 || layers > kMaxDecodeLayers) return false;

@@ -172,12 +172,35 @@ __device__ __forceinline__ bool stage_chunk_ok(int K, int j) {
   return (threadIdx.x & 63) + 64 * j < (K >> 4);
 }
 
-// LayerNorm of the fp32 row x (K values: cells tagged `tag`, or the plain
-// buffer xp) with gains g and biases b -> xs (fp16). A thread holds the
+// The first layer's input row straight from the embedding tables: row `tok`
+// of the tied head (fp16 tiled) plus the position row `wpe_row`, summed in
+// fp32 (the per-op path's embed kernel does the same sum).
+struct Emb {
+  int tok = -1;  // < 0: the row comes from cells
+  const SH_XGLOBAL uint16_t *wte = nullptr, *wpe_row = nullptr;
+};
+
+// Values k .. k + 3 of the embedded row (k a multiple of 4: contiguous in
+// both tables).
+__device__ __forceinline__ f32x4 emb4(const Emb &e, int k, int K) {
+  const u32x2 t = *reinterpret_cast<const SH_XGLOBAL u32x2 *>(e.wte + f16_tiled_offset(e.tok, k, K));
+  const u32x2 p = *reinterpret_cast<const SH_XGLOBAL u32x2 *>(e.wpe_row + k);
+  return f32x4{f16_bits_to_f32((uint16_t)t.x) + f16_bits_to_f32((uint16_t)p.x),
+               f16_bits_to_f32((uint16_t)(t.x >> 16)) + f16_bits_to_f32((uint16_t)(p.x >> 16)),
+               f16_bits_to_f32((uint16_t)t.y) + f16_bits_to_f32((uint16_t)p.y),
+               f16_bits_to_f32((uint16_t)(t.y >> 16)) + f16_bits_to_f32((uint16_t)(p.y >> 16))};
+}
+
+__device__ __forceinline__ float emb1(const Emb &e, int k, int K) {
+  return f16_bits_to_f32(e.wte[f16_tiled_offset(e.tok, k, K)]) + f16_bits_to_f32(e.wpe_row[k]);
+}
+
+// LayerNorm of the fp32 row x (K values: cells tagged `tag`, or the embedded
+// row e when e.tok >= 0) with gains g and biases b -> xs (fp16). A thread holds the
 // 4-value chunks stage_chunk(K, j), j < kC. kLocal: the caller's waves read
 // only their own K quarter of xs, so no barrier follows the stores.
 template <int kC, bool kLocal>
-__device__ __forceinline__ bool stage_ln(const Gpt2Args &a, const uint64_t *xc, const float *xp,
+__device__ __forceinline__ bool stage_ln(const Gpt2Args &a, const uint64_t *xc, const Emb &e,
                                          unsigned tag, const SH_XGLOBAL float *g,
                                          const SH_XGLOBAL float *bta, int K, Lds &S) {
   const int c4 = K >> 2;
@@ -189,10 +212,9 @@ __device__ __forceinline__ bool stage_ln(const Gpt2Args &a, const uint64_t *xc, 
     bv[j] = *reinterpret_cast<const SH_XGLOBAL f32x4 *>(bta + c * 4);
   }
   bool ok = true;
-  if (xp) {
+  if (e.tok >= 0) {
 #pragma unroll
-    for (int j = 0; j < kC; j++)
-      v[j] = *reinterpret_cast<const SH_XGLOBAL f32x4 *>(gbl(xp) + min(stage_chunk(K, j), c4 - 1) * 4);
+    for (int j = 0; j < kC; j++) v[j] = emb4(e, min(stage_chunk(K, j), c4 - 1) * 4, K);
   } else {
     uint64_t cv[kC * 4];
     uint64_t mask = 0;
@@ -260,11 +282,11 @@ __device__ __forceinline__ bool stage_f16(const Gpt2Args &a, const uint64_t *cel
 // A: qkv[16 i + c] = W_qkv LayerNorm(x) + b; w holds the item's weights
 template <int kLH>
 __device__ __forceinline__ bool qkv_item(const Gpt2Args &a, const LayerP &P, int l, int i, unsigned ep,
-                                         Lds &S, const u32x4 (&w)[kLH]) {
+                                         const Emb &e, Lds &S, const u32x4 (&w)[kLH]) {
   const int lane = threadIdx.x & 63, col = lane & 15;
   const float bias = P.bqkv[i * 16 + col];
   __builtin_amdgcn_sched_barrier(0);
-  if (!stage_ln<(kLH * 128 + 1023) / 1024, true>(a, a.x0c, l == 0 ? a.x_in : nullptr, tag_of(ep, l - 1),
+  if (!stage_ln<(kLH * 128 + 1023) / 1024, true>(a, a.x0c, l == 0 ? e : Emb{}, tag_of(ep, l - 1),
                                             P.ln1_g, P.ln1_b, a.H, S))
     return false;
   SH_G2WAIT(l, 0);
@@ -511,14 +533,14 @@ __device__ __forceinline__ bool stage_attn(const Gpt2Args &a, unsigned tag, int 
 // C: x_mid[16 i + c] = x[.] + W_o attn + b
 template <int kLH>
 __device__ __forceinline__ bool o_item(const Gpt2Args &a, const LayerP &P, int l, int i, unsigned ep,
-                                       int L, Lds &S) {
+                                       int L, const Emb &e, Lds &S) {
   const int lane = threadIdx.x & 63, col = lane & 15;
   u32x4 w[kLH];
   load_weights<kLH>(w, P.wo, a.H, i);
   const float bias = P.bo[i * 16 + col];
   const size_t cell = (size_t)i * 16 + col;
-  uint64_t rc = cld(a.x0c, cell);  // the residual (layer 0: the plain input)
-  const float x0 = l == 0 ? gbl(a.x_in)[cell] : 0.0f;
+  uint64_t rc = cld(a.x0c, cell);  // the residual (layer 0: the embedded row)
+  const float x0 = l == 0 ? emb1(e, (int)cell, a.H) : 0.0f;
   __builtin_amdgcn_sched_barrier(0);
   if (!stage_attn<(kLH * 128 + 255) / 256>(a, tag_of(ep, l), L, S)) return false;
   SH_G2WAIT(l, 2);
@@ -545,7 +567,7 @@ __device__ __forceinline__ bool fc_item(const Gpt2Args &a, const LayerP &P, int 
   load_weights<kLH>(w, P.wfc, a.H, i);
   const float bias = P.bfc[i * 16 + col];
   __builtin_amdgcn_sched_barrier(0);
-  if (!stage_ln<(kLH * 128 + 1023) / 1024, true>(a, a.x1c, nullptr, tag_of(ep, l), P.ln2_g, P.ln2_b, a.H, S))
+  if (!stage_ln<(kLH * 128 + 1023) / 1024, true>(a, a.x1c, Emb{}, tag_of(ep, l), P.ln2_g, P.ln2_b, a.H, S))
     return false;
   SH_G2WAIT(l, 3);
   const f32x4 acc = reduce_waves(mfma_weights<kLH>(w, S.xs), S);
@@ -560,8 +582,8 @@ __device__ __forceinline__ bool fc_item(const Gpt2Args &a, const LayerP &P, int 
 }
 
 // E: x[16 i + c] = x_mid[.] + W_proj act + b (w: the item's weights, requested
-// by the caller); the last layer also writes the plain buffer the final
-// LayerNorm reads
+// by the caller); the last layer also writes x to the plain buffer x_in (the
+// model's residual-stream tensor)
 template <int kLH, int kLI>
 __device__ __forceinline__ bool proj_item(const Gpt2Args &a, const LayerP &P, int l, int i, unsigned ep,
                                           Lds &S, const u32x4 (&w)[kLI]) {
@@ -605,7 +627,7 @@ __device__ __forceinline__ bool head_phase(const Gpt2Args &a, unsigned ep, Lds &
                                            u32x4 (&wb)[2][4 * kLH]) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, G = gridDim.x, w = blockIdx.x;
   const int first = w + G * wave, step = 4 * G, nT = a.head_tiles;
-  if (!stage_ln<(kLH * 128 + 1023) / 1024, false>(a, a.x0c, nullptr, tag_of(ep, a.n_layers - 1),
+  if (!stage_ln<(kLH * 128 + 1023) / 1024, false>(a, a.x0c, Emb{}, tag_of(ep, a.n_layers - 1),
                                             gbl(a.final_g), gbl(a.final_b), a.H, S))
     return false;
   const _Float16 *xrow = S.xs + 8 * (lane >> 4);
@@ -637,11 +659,32 @@ __device__ __forceinline__ bool head_phase(const Gpt2Args &a, unsigned ep, Lds &
     const unsigned long long o = __shfl_xor(best, off, 64);
     best = o > best ? o : best;
   }
-  unsigned long long *slot = a.keys + ((w * 4 + wave) % kKeySlots) * kKeyStride;
+  unsigned long long *slot =
+      a.keys + (size_t)(ep & 1) * kKeySet + ((w * 4 + wave) % kKeySlots) * kKeyStride;
   if (lane == 0 && best != 0 &&
       best > __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
     atomicMax(slot, best);
   return true;
+}
+
+// The step's bookkeeping, by workgroup 0 after its last item: the step
+// number, the row's length and position, the history entry, and the key set
+// this step read cleared for the next step's LM head. Every workgroup with an
+// item has read the epoch word, lens and (QKV items) the keys by then: it read
+// them first, and its items' cells carry the step's tag, its context or its
+// token, while workgroup 0's last item waited, through each layer's chain of
+// exchanges, on cells that depend on every item of the step. (A workgroup
+// with no item that read the words after this would wait on tags no one
+// writes: its wait times out and sets err.)
+__device__ __forceinline__ void finish_step(const Gpt2Args &a, unsigned ep0, int pos, int tok) {
+  const int t = threadIdx.x;
+  if (t < kKeySlots) gbl(a.keys)[(size_t)(ep0 & 1) * kKeySet + (size_t)t * kKeyStride] = 0ull;
+  if (t == 0) {
+    if (pos < a.hist_len) gbl(a.hist)[pos] = tok;
+    gbl(a.pos)[0] = pos;
+    gbl(a.lens)[0] = pos + 1;
+    gbl(a.epoch)[0] = ep0 + 1;
+  }
 }
 
 template <int kLH, int kLI>
@@ -650,10 +693,26 @@ __global__ __launch_bounds__(kT, 1) void gpt2_layers_kernel(const Gpt2Args a) {
   if (threadIdx.x < 4) S.votes.par[threadIdx.x] = 0;
   lds_barrier();
   SH_G2MARK(0, 10);
-  const unsigned ep = *cnst(a.epoch);
-  const int L = cnst(a.pos)[0] + 1;  // context including this step's token
+  // The step: number ep (the epoch word holds the previous one), position
+  // pos = lens[0]; its token is read from the previous step's key set by the
+  // workgroups with QKV items (the O items are among them), which embed it.
+  // These words change only in finish_step, after every workgroup has read
+  // them (see there), so atomic loads, read once: no reload can see the new
+  // values.
+  const unsigned ep0 = __builtin_amdgcn_readfirstlane(
+      __hip_atomic_load(a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  const unsigned ep = ep0 + 1;
+  const int pos = __builtin_amdgcn_readfirstlane(
+      __hip_atomic_load(a.lens, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  const int L = pos + 1;  // context including this step's token
   const int G = gridDim.x, w = blockIdx.x;
   const int nA = a.qkv_n / 16, nB = a.heads * kGpt2Splits, nC = a.H / 16, nD = a.inter / 16;
+  Emb emb;
+  if (w < nA) {
+    emb.tok = step_token(a.keys + (size_t)(ep0 & 1) * kKeySet, 0, a.vocab);
+    emb.wte = gbl(a.head_w);
+    emb.wpe_row = gbl(a.wpe) + (size_t)min(pos, a.max_pos - 1) * a.H;
+  }
   const int bi = w - (G - nB);  // this workgroup's attention item (when >= 0)
   const bool hasD = w >= nC && w < nC + nD;
   AttnKV kv;
@@ -663,7 +722,7 @@ __global__ __launch_bounds__(kT, 1) void gpt2_layers_kernel(const Gpt2Args a) {
   for (int l = 0; l < a.n_layers; l++) {
     const LayerP P = layer_p(a, l);
     const bool next = l + 1 < a.n_layers;
-    if (w < nA && !qkv_item<kLH>(a, P, l, w, ep, S, wa)) return;
+    if (w < nA && !qkv_item<kLH>(a, P, l, w, ep, emb, S, wa)) return;
     if (bi >= 0) {
       if (!attn_item(a, P, l, bi, ep, L, S, kv)) return;
       if (next && !hasD) attn_prefetch(a, layer_p(a, l + 1), bi, L, kv);
@@ -679,7 +738,7 @@ __global__ __launch_bounds__(kT, 1) void gpt2_layers_kernel(const Gpt2Args a) {
       load_weights<kLI>(wp, P.wproj, a.inter, w);
       if (next && w < nA) load_weights<kLH>(wa, layer_p(a, l + 1).wqkv, a.H, w);
     }
-    if (w < nC && !o_item<kLH>(a, P, l, w, ep, L, S)) return;
+    if (w < nC && !o_item<kLH>(a, P, l, w, ep, L, emb, S)) return;
     if (hasD) {
       if (!fc_item<kLH>(a, P, l, w - nC, ep, S)) return;
       if (next) {
@@ -695,9 +754,10 @@ __global__ __launch_bounds__(kT, 1) void gpt2_layers_kernel(const Gpt2Args a) {
   if (a.head_on) {
     u32x4 wb[2][4 * kLH];
     head_load<kLH>(wb[0], a, w + G * (threadIdx.x >> 6));  // before the final norm's wait
-    head_phase<kLH>(a, ep, S, wb);
+    if (!head_phase<kLH>(a, ep, S, wb)) return;
     SH_G2MARK(0, 11);
   }
+  if (w == 0) finish_step(a, ep0, pos, emb.tok);
 }
 
 // (loads per lane for K = hidden, K = intermediate) per supported shape

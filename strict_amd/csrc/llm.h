@@ -20,6 +20,14 @@ constexpr int kMaxSplitChunk = 1024; // positions one attention workgroup may sc
 constexpr int kKeySlots = 32;
 constexpr int kKeyStride = 32;
 static_assert(kKeyStride >= kMaxBatch, "a slot row holds every batch row");
+// The model holds two such key sets of kKeySet keys each. A persistent
+// layers kernel (one launch per step) of step number e reads this step's
+// tokens from set (e - 1) & 1, its LM head writes set e & 1, and its
+// workgroup 0 clears set (e - 1) & 1 after its last item (every workgroup
+// has read the tokens by then), ready for step e + 1's head. The per-op path
+// reads, clears and writes the set of the current step number, which it does
+// not advance.
+constexpr int kKeySet = kKeySlots * kKeyStride;
 
 enum { kWeightFp8 = 0, kWeightFp16 = 1 };
 enum { kProNone = 0, kProRms = 1, kProLayer = 2 };
@@ -68,6 +76,8 @@ struct AttnArgs {
 
 struct EmbedArgs {
   unsigned long long *keys = nullptr;  // [kKeySlots][kKeyStride] argmax keys (token = ~low word)
+  unsigned long long *keys_clear = nullptr;  // key set whose row b the kernel zeroes for
+                                             // this step's LM head (may be `keys`)
   int *lens = nullptr;                 // [B] tokens cached so far (advanced here)
   int *pos = nullptr;                  // [B] position of this step's token (written here)
   int *hist = nullptr;                 // [B][hist_len] token history
@@ -119,9 +129,14 @@ struct LayersArgs {
                                        // (embed kernel), last layer's output
   uint64_t *x0c = nullptr, *x1c = nullptr, *qkvc = nullptr, *partc = nullptr;
   uint64_t *attnc = nullptr, *actc = nullptr;
-  unsigned *err = nullptr;             // set when a wait timed out (sticky)
+  unsigned *err = nullptr;             // set when a wait timed out (sticky); bit 1: a
+                                       // workgroup was off its XCD in XCD-local mode
   unsigned long long spin_ticks = 0;   // wall-clock ticks a wait may take
   int lds_misc = 0;                    // byte offset of the small LDS scratch words
+  // batch 1: KV head h's QKV, attention and merge items on the workgroups
+  // w % 8 == h (XCD h), their cells stored into that XCD's L2
+  // (decode_layers_xcd_ok must hold)
+  int xcd = 0;
   // final RMSNorm + LM head inside the kernel (steps with logits; head_on 0:
   // the kernel ends with the last layer)
   int head_on = 0;
@@ -131,13 +146,18 @@ struct LayersArgs {
   int head_tiles = 0, n_valid = 0;     // 16-row tiles; columns that are real tokens
   float *logits = nullptr;             // [B][logits_ld]
   int logits_ld = 0;
-  unsigned long long *keys = nullptr;  // [kKeySlots][kKeyStride] greedy argmax keys (zeroed by the embed kernel)
+  unsigned long long *keys = nullptr;  // [kKeySlots][kKeyStride] the key set this step's LM
+                                       // head writes (row b zeroed by the embed kernel)
 };
 
 // Model shapes the kernel is instantiated for (16-byte weight loads per lane
 // of the qkv, o, gate/up and down items) and the query heads per KV head.
 // Returns false for any other shape (the runner then keeps per-op kernels).
 bool decode_layers_supported(int layers, int H, int heads, int kv_heads, int head_dim, int inter);
+// Whether a (batch 1, `grid` workgroups) fits the XCD-local placement: eight
+// KV heads, one per XCD, each with grid / 8 QKV tiles (its query heads' q,
+// its k and v) and grid / 8 attention splits.
+bool decode_layers_xcd_ok(const LayersArgs &a, int grid);
 // Most attention splits per (row, KV head) the shape's kernel merges.
 int decode_layers_max_splits(int H, int heads, int kv_heads, int inter);
 // Cells of the attention-partial buffer partc.
@@ -179,9 +199,17 @@ struct Gpt2Args {
   int n_layers = 0, H = 0, heads = 0, inter = 0, qkv_n = 0, max_pos = 0;
   int chunk = 16;                    // positions per attention split
   float eps = 1e-5f, scale = 0.125f;  // LayerNorm epsilon, attention 1 / sqrt(64)
-  const int *pos = nullptr;          // [1] this step's position (embed kernel)
-  const unsigned *epoch = nullptr;   // this step's number (embed kernel)
-  float *x_in = nullptr;             // [H] first layer's input, last layer's output
+  // the step's embedding and bookkeeping (the kernel is the step's only
+  // launch): the token from key set (epoch) & 1, the position lens[0]; at the
+  // end workgroup 0 stores epoch + 1, lens[0] + 1, pos[0] and the history
+  // entry, and clears that key set
+  unsigned *epoch = nullptr;         // steps run so far (this step is epoch + 1)
+  int *lens = nullptr;               // [1] tokens cached so far
+  int *pos = nullptr;                // [1] this step's position (written at the end)
+  int *hist = nullptr;               // [hist_len] token history
+  int hist_len = 0, vocab = 0;
+  const uint16_t *wpe = nullptr;     // positions [max_pos][H] fp16 (token rows: head_w)
+  float *x_in = nullptr;             // [H] last layer's output
   uint64_t *x0c = nullptr, *x1c = nullptr, *qkvc = nullptr, *partc = nullptr, *actc = nullptr;
   unsigned *err = nullptr;           // set when a wait timed out (sticky)
   unsigned long long spin_ticks = 0;  // wall-clock ticks a wait may take
@@ -191,7 +219,7 @@ struct Gpt2Args {
   const float *final_g = nullptr, *final_b = nullptr;
   int head_tiles = 0, n_valid = 0;   // 16-row tiles; columns that are real tokens
   float *logits = nullptr;           // [logits_ld]
-  unsigned long long *keys = nullptr;  // [kKeySlots][kKeyStride] greedy argmax keys
+  unsigned long long *keys = nullptr;  // [2][kKeySet] the two greedy argmax key sets
 };
 // Shapes the kernel is built for (GPT-2 small and a reduced test shape),
 // max_pos <= 1024, and a grid of `grid` workgroups holding every phase's items.

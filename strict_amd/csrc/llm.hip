@@ -82,6 +82,7 @@ struct sh_llm {
   size_t kv_layer_elems = 0;
   hipGraphExec_t graph[2] = {nullptr, nullptr};
   int graph_batch[2] = {-1, -1};
+  unsigned long long *graph_keys[2] = {nullptr, nullptr};  // key set a graph was captured on
   bool use_graphs = true;  // STRICT_HIP_LLM_GRAPHS=0: enqueue every step eagerly
   // persistent decode-layers kernel (Qwen3 shapes it is built for;
   // STRICT_HIP_LLM_LAYERS=0 keeps the per-op kernels)
@@ -92,6 +93,10 @@ struct sh_llm {
   int layers_grid = 0;
   size_t layers_lds = 0;
   unsigned *epoch = nullptr;
+  // the device's step number (*epoch), mirrored: one more per step of a
+  // layers kernel; its parity selects the current key set
+  unsigned epoch_host = 0;
+  bool xcd_off = false;  // a step found a workgroup off its XCD: no XCD-local placement
   // persistent GPT-2 layers kernel (batch 1; other batches keep the per-op
   // kernels, which share its cache layout)
   bool gpt2_kernel = false;
@@ -159,14 +164,33 @@ Linear *find_linear(sh_llm *m, const std::string &name, int layer) {
   return nullptr;
 }
 
+// The key set of the current step number: the one the next step reads its
+// tokens from, and the one the last step's LM head wrote.
+unsigned long long *key_set(sh_llm *m, unsigned ahead = 0) {
+  return m->keys + (size_t)((m->epoch_host + ahead) & 1u) * kKeySet;
+}
+
 int enqueue_step(sh_llm *m, bool logits) {
   const sh_llm_config &c = m->cfg;
   hipStream_t s = stream_of(m->ctx);
   const int B = m->batch, H = c.hidden, d = c.head_dim;
   const int pro = m->qwen ? kProRms : kProLayer;
 
+  const bool gpt2_layers = m->gpt2_kernel && B == 1;
+  // keys this step reads its tokens from and its LM head writes: a layers
+  // kernel step advances the step number, so the head writes the other set
+  unsigned long long *keys_in = key_set(m);
+  unsigned long long *keys_out = key_set(m, m->layers_kernel || gpt2_layers ? 1 : 0);
+  if (gpt2_layers) {
+    // the GPT-2 layers kernel embeds the token itself: one launch per step
+    m->ga.head_on = logits ? 1 : 0;
+    SH_HIP_TRY(launch_gpt2_layers(s, m->ga, m->gpt2_grid));
+    m->epoch_host++;
+    return SH_OK;
+  }
   EmbedArgs e;
-  e.keys = m->keys;
+  e.keys = keys_in;
+  e.keys_clear = keys_out;
   e.lens = m->lens;
   e.pos = m->pos;
   e.hist = m->hist;
@@ -184,21 +208,18 @@ int enqueue_step(sh_llm *m, bool logits) {
   e.inv_freq = m->inv_freq;
   e.rope = m->rope;
   e.half = d / 2;
-  float *x_final = m->x;  // the layers kernels read and write m->x too
-  const bool gpt2_layers = m->gpt2_kernel && B == 1;
-  if (m->layers_kernel || gpt2_layers) e.epoch = m->epoch;
+  float *x_final = m->x;  // the layers kernel reads and writes m->x too
+  if (m->layers_kernel) e.epoch = m->epoch;
   SH_HIP_TRY(launch_embed(s, e, B));
 
   if (m->layers_kernel) {
     m->la.head_on = logits && m->head_in_layers ? 1 : 0;
+    m->la.keys = keys_out;
     SH_HIP_TRY(launch_decode_layers(s, m->la, m->layers_grid, m->layers_lds, m->coop_layers));
-  }
-  if (gpt2_layers) {
-    m->ga.head_on = logits ? 1 : 0;
-    SH_HIP_TRY(launch_gpt2_layers(s, m->ga, m->gpt2_grid));
+    m->epoch_host++;
   }
   for (Layer &L : m->layers) {
-    if (m->layers_kernel || gpt2_layers) break;  // every layer ran in the kernel above
+    if (m->layers_kernel) break;  // every layer ran in the kernel above
     GemvArgs g;
     g.w = L.qkv.w;
     g.scale = L.qkv.scale;
@@ -280,7 +301,7 @@ int enqueue_step(sh_llm *m, bool logits) {
     SH_HIP_TRY(launch_gemv(s, dn, m->wtype, kProNone, kEpiResidual, 0));
   }
 
-  if (logits && !(m->layers_kernel && m->head_in_layers) && !gpt2_layers) {
+  if (logits && !(m->layers_kernel && m->head_in_layers)) {
     GemvArgs nrm;
     nrm.x = x_final;
     nrm.x_ld = H;
@@ -303,7 +324,7 @@ int enqueue_step(sh_llm *m, bool logits) {
     h.n_valid = c.vocab;
     h.out = m->logits;
     h.out_ld = m->vocab_pad;
-    h.argmax = m->keys;
+    h.argmax = keys_out;
     // grid-striding over the head's tiles (one tile per workgroup ran the
     // fp16 GPT-2 head at 2 TB/s)
     SH_HIP_TRY(launch_gemv(s, h, m->wtype, kProNone, kEpiLogits, 2048));
@@ -389,7 +410,6 @@ int setup_layers_kernel(sh_llm *m) {
   a.n_valid = c.vocab;
   a.logits = m->logits;
   a.logits_ld = m->vocab_pad;
-  a.keys = m->keys;
   m->layers_grid = cus;
   m->layers_kernel = true;
   return SH_OK;
@@ -420,7 +440,12 @@ int setup_gpt2_kernel(sh_llm *m) {
   a.chunk = gpt2_layers_chunk(c.max_positions);
   a.eps = c.norm_eps;
   a.scale = 1.0f / std::sqrt((float)c.head_dim);
+  a.lens = m->lens;
   a.pos = m->pos;
+  a.hist = m->hist;
+  a.hist_len = c.max_positions;
+  a.vocab = c.vocab;
+  a.wpe = m->wpe;
   a.spin_ticks = (unsigned long long)clock_khz * 50;  // 50 ms per wait
   int per_cu = 0;
   SH_HIP_TRY(gpt2_layers_occupancy(a, &per_cu));
@@ -456,7 +481,7 @@ int setup_gpt2_kernel(sh_llm *m) {
   a.head_tiles = m->head.N / 16;
   a.n_valid = c.vocab;
   a.logits = m->logits;
-  a.keys = m->keys;
+  a.keys = m->keys;  // both sets: the kernel picks them by the step number
   m->gpt2_grid = cus;
   m->gpt2_kernel = true;
   return SH_OK;
@@ -637,7 +662,7 @@ SH_API int sh_llm_create(sh_ctx *ctx, const sh_llm_config *config, sh_llm **out)
       (rc = alloc_n(m, (size_t)B * c.kv_heads, &m->counters)) ||
       (rc = alloc_n(m, (size_t)B, &m->lens)) || (rc = alloc_n(m, (size_t)B, &m->pos)) ||
       (rc = alloc_n(m, (size_t)B * c.max_positions, &m->hist)) ||
-      (rc = alloc_n(m, (size_t)kKeySlots * kKeyStride, &m->keys)))
+      (rc = alloc_n(m, (size_t)2 * kKeySet, &m->keys)))
     return cleanup(rc);
   // norm gains start at 1 (biases and weights at 0)
   for (Layer &L : m->layers) {
@@ -801,7 +826,13 @@ SH_API int sh_llm_reset(sh_llm *m, int batch) {
     return fail(SH_ERR_INVALID_ARGUMENT, "batch %d outside 1..%d", batch, m->cfg.max_batch);
   hipStream_t s = stream_of(m->ctx);
   SH_HIP_TRY(hipMemsetAsync(m->lens, 0, (size_t)m->cfg.max_batch * 4, s));
-  SH_HIP_TRY(hipMemsetAsync(m->keys, 0, (size_t)kKeySlots * kKeyStride * 8, s));
+  SH_HIP_TRY(hipMemsetAsync(m->keys, 0, (size_t)2 * kKeySet * 8, s));
+  if (m->epoch) {
+    // the device's step number to the mirror's: a layers kernel whose wait
+    // timed out may have ended before storing it (tags only ever grow)
+    SH_HIP_TRY(hipMemcpyAsync(m->epoch, &m->epoch_host, 4, hipMemcpyHostToDevice, s));
+    SH_HIP_TRY(hipStreamSynchronize(s));
+  }
   SH_HIP_TRY(hipMemsetAsync(m->counters, 0, (size_t)m->cfg.max_batch * m->cfg.kv_heads * 4, s));
   m->batch = batch;
   m->splits = attention_splits(batch, m->cfg.kv_heads, m->cfg.max_positions);
@@ -822,6 +853,10 @@ SH_API int sh_llm_reset(sh_llm *m, int batch) {
     a.B = batch;
     a.splits = sp;
     a.chunk = ((c.max_positions + sp - 1) / sp + 15) / 16 * 16;
+    // XCD-local placement at batch 1 (STRICT_HIP_LLM_XCD=0: off; also off
+    // for the model's life once a step found a workgroup off its XCD)
+    const char *xe = getenv("STRICT_HIP_LLM_XCD");
+    a.xcd = !(xe && xe[0] == '0') && !m->xcd_off && decode_layers_xcd_ok(a, m->layers_grid) ? 1 : 0;
     m->layers_lds = decode_layers_lds(batch, c.hidden, c.heads, c.intermediate, &a.lds_misc);
     SH_HIP_TRY(hipMemsetAsync(a.err, 0, 4, s));
   }
@@ -845,13 +880,15 @@ SH_API int sh_llm_step(sh_llm *m, const int32_t *tokens, int want_logits) {
         return fail(SH_ERR_INVALID_ARGUMENT, "token %d of row %d outside the vocabulary", tokens[b], b);
       keys[b] = (unsigned long long)(0xffffffffu - (uint32_t)tokens[b]);
     }
-    SH_HIP_TRY(hipMemcpyAsync(m->keys, keys, sizeof(keys), hipMemcpyHostToDevice, s));
+    SH_HIP_TRY(hipMemcpyAsync(key_set(m), keys, sizeof(keys), hipMemcpyHostToDevice, s));
     SH_HIP_TRY(hipStreamSynchronize(s));  // `keys` is a stack array
   }
   const int g = want_logits ? 1 : 0;
   if (!m->use_graphs || m->layers_kernel || (m->gpt2_kernel && m->batch == 1)) {
     if ((rc = enqueue_step(m, want_logits != 0)) != SH_OK) return rc;
-  } else if (m->graph_batch[g] != m->batch) {
+  } else if (m->graph_batch[g] != m->batch || m->graph_keys[g] != key_set(m)) {
+    // (a layers kernel's steps at another batch may have moved the step
+    // number to the other key set since the capture)
     if (m->graph[g]) (void)hipGraphExecDestroy(m->graph[g]);
     m->graph[g] = nullptr;
     m->graph_batch[g] = -1;
@@ -870,6 +907,7 @@ SH_API int sh_llm_step(sh_llm *m, const int32_t *tokens, int want_logits) {
     (void)hipGraphDestroy(graph);
     if (e != hipSuccess) return hip_fail(e, "instantiating the decode graph");
     m->graph_batch[g] = m->batch;
+    m->graph_keys[g] = key_set(m);
   } else {
     SH_HIP_TRY(hipGraphLaunch(m->graph[g], s));
   }
@@ -883,13 +921,18 @@ SH_API int sh_llm_next_tokens(sh_llm *m, int32_t *tokens) {
   if (rc != SH_OK) return rc;
   unsigned long long keys[kKeySlots * kKeyStride];
   hipStream_t s = stream_of(m->ctx);
-  SH_HIP_TRY(hipMemcpyAsync(keys, m->keys, sizeof(keys), hipMemcpyDeviceToHost, s));
+  SH_HIP_TRY(hipMemcpyAsync(keys, key_set(m), sizeof(keys), hipMemcpyDeviceToHost, s));
   unsigned err = 0;
   if (m->layers_kernel)
     SH_HIP_TRY(hipMemcpyAsync(&err, m->la.err, 4, hipMemcpyDeviceToHost, s));
   else if (m->gpt2_kernel && m->batch == 1)
     SH_HIP_TRY(hipMemcpyAsync(&err, m->ga.err, 4, hipMemcpyDeviceToHost, s));
   SH_HIP_TRY(hipStreamSynchronize(s));
+  if (m->layers_kernel && (err & 2u)) {
+    m->xcd_off = true;
+    return fail(SH_ERR_HIP, "decode-layers kernel: a workgroup ran off the XCD its placement assumes "
+                            "(step state lost; reset the model, which turns the XCD-local placement off)");
+  }
   if (err)
     return fail(SH_ERR_HIP, "decode-layers kernel: a wait between workgroups timed out (step state lost; reset the model)");
   for (int b = 0; b < m->batch; b++) {

@@ -7,6 +7,7 @@
 #include <cstdint>
 
 #include "common.h"
+#include "llm.h"
 
 namespace sh {
 
@@ -82,6 +83,43 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int n) {
   uint32_t u = __builtin_bit_cast(uint32_t, v);
   u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
   return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)n);
+}
+
+// The token of batch row b: the largest of its keys over the kKeySlots slots
+// of key set `keys` (token = ~ low word; out-of-vocabulary tokens read as 0).
+// Called by a whole wave; the result is wave-uniform.
+__device__ __forceinline__ int step_token(const unsigned long long *keys, int b, int vocab) {
+  const int lane = threadIdx.x & 63;
+  unsigned long long key = 0;
+  if (lane < kKeySlots)
+    key = __hip_atomic_load(keys + (size_t)lane * kKeyStride + b, __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const unsigned long long o = __shfl_xor(key, off, 64);
+    key = o > key ? o : key;
+  }
+  int tok = (int)(0xffffffffu - (uint32_t)(key & 0xffffffffu));
+  if (tok < 0 || tok >= vocab) tok = 0;
+  return __builtin_amdgcn_readfirstlane(tok);
+}
+
+// Byte offset of W[n][k] in an FP8 tiled matrix with K columns (1 KiB tiles
+// of 16 rows x 64 K; 8 consecutive k of a row are contiguous).
+__device__ __forceinline__ size_t fp8_tiled_offset(int n, int k, int K) {
+  const int kt = k >> 6, k64 = k & 63, half = k64 >> 5, kk = k64 & 31;
+  const int lane = (n & 15) + 16 * (kk >> 3);
+  return ((size_t)(n >> 4) * (size_t)(K >> 6) + (size_t)kt) * 1024 + (size_t)lane * 16 +
+         (size_t)(half * 8 + (kk & 7));
+}
+
+// Element offset of W[n][k] in an fp16 tiled matrix with K columns (1 KiB
+// tiles of 16 rows x 32 K; 8 consecutive k of a row are contiguous).
+__device__ __forceinline__ size_t f16_tiled_offset(int n, int k, int K) {
+  const int kt = k >> 5, kk = k & 31;
+  const int lane = (n & 15) + 16 * (kk >> 3);
+  return (((size_t)(n >> 4) * (size_t)(K >> 5) + (size_t)kt) * 64 + (size_t)lane) * 8 +
+         (size_t)(kk & 7);
 }
 
 __device__ __forceinline__ float gelu_tanh(float x) {

@@ -58,22 +58,6 @@ __device__ __forceinline__ uint8_t f32_to_e4m3(float f) {
 
 // ---- tiled offsets -------------------------------------------------------
 
-// Byte offset of W[n][k] in an FP8 tiled matrix with K columns.
-__device__ __forceinline__ size_t fp8_tiled_offset(int n, int k, int K) {
-  const int kt = k >> 6, k64 = k & 63, half = k64 >> 5, kk = k64 & 31;
-  const int lane = (n & 15) + 16 * (kk >> 3);
-  return ((size_t)(n >> 4) * (size_t)(K >> 6) + (size_t)kt) * 1024 + (size_t)lane * 16 +
-         (size_t)(half * 8 + (kk & 7));
-}
-
-// Element offset of W[n][k] in an fp16 tiled matrix with K columns.
-__device__ __forceinline__ size_t f16_tiled_offset(int n, int k, int K) {
-  const int kt = k >> 5, kk = k & 31;
-  const int lane = (n & 15) + 16 * (kk >> 3);
-  return (((size_t)(n >> 4) * (size_t)(K >> 5) + (size_t)kt) * 64 + (size_t)lane) * 8 +
-         (size_t)(kk & 7);
-}
-
 // Source row of tiled row n when the layer is a gate/up pair stored with its
 // 16-row tiles interleaved (gate tile p, up tile p, ...): logical input is
 // [gate (I rows); up (I rows)].
@@ -785,8 +769,9 @@ __global__ __launch_bounds__(kThreads) void norm_rows_kernel(const GemvArgs a) {
 
 // grid (B): reads the token of row b from its argmax keys (the largest over
 // the slots; the host writes prompt tokens as keys too), records it in the
-// history, clears the keys for this step's LM head, advances the row's
-// position and writes the fp32
+// history, clears row b of the key set this step's LM head writes (the one it
+// read, or the other set after a decode-layers kernel step), advances the
+// row's position and writes the fp32
 // residual stream: Qwen3 dequantises the tied FP8 head row, GPT-2 adds the
 // fp16 token (tied head) and position rows.
 __global__ __launch_bounds__(kThreads) void embed_kernel(const EmbedArgs a) {
@@ -796,7 +781,7 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const EmbedArgs a) {
     unsigned long long key = 0;
     if (t < kKeySlots) {
       key = a.keys[t * kKeyStride + b];
-      a.keys[t * kKeyStride + b] = 0;
+      a.keys_clear[t * kKeyStride + b] = 0;
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {

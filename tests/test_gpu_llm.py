@@ -243,13 +243,17 @@ def test_per_op_path_without_graphs(ctx, monkeypatch, cfg):
     assert np.array_equal(runs[0][1], runs[1][1])
 
 
-@pytest.mark.parametrize("cfg", [QWEN_SMALL, GPT2_SMALL_TEST], ids=["qwen3", "gpt2"])
-def test_decode_layers_wait_failure_reported_and_reset_recovers(ctx, cfg):
+@pytest.mark.parametrize("cfg,err,text", [(QWEN_SMALL, 1, "timed out"), (GPT2_SMALL_TEST, 1, "timed out"),
+                                          (QWEN_SMALL, 2, "off the XCD")],
+                         ids=["qwen3", "gpt2", "qwen3-placement-bit"])
+def test_decode_layers_wait_failure_reported_and_reset_recovers(ctx, cfg, err, text):
     # The bounded waits of the persistent layers kernels (Qwen3's decode-layers
     # kernel, GPT-2's layers kernel): the host sets the sticky error word
     # before a step, so every wait between workgroups gives up after a few
     # polls and the kernel ends normally; sh_llm_next_tokens reports the
-    # failed step, and sh_llm_reset clears the error.
+    # failed step (bit 1: the Qwen3 kernel found a workgroup off the XCD its
+    # XCD-local placement assumes, which also turns that placement off), and
+    # sh_llm_reset clears the error.
     prompt = np.random.default_rng(5).integers(0, cfg.vocab, 12)
     with llm.Model(ctx, cfg) as m:
         assert m.uses_layers_kernel
@@ -259,11 +263,11 @@ def test_decode_layers_wait_failure_reported_and_reset_recovers(ctx, cfg):
         m.reset(1)
         for i, t in enumerate(prompt):
             m.step([int(t)], logits=(i == len(prompt) - 1))
-        m.write("layers.err", 0, np.array([1], np.uint32))
+        m.write("layers.err", 0, np.array([err], np.uint32))
         m.step(None, logits=True)
         with pytest.raises(strict_amd.StrictHipError) as e:
             m.next_tokens()
-        assert "timed out" in str(e.value)
+        assert text in str(e.value)
         assert m.read("layers.err", 0, np.uint32)[0] != 0
         m.reset(1)
         assert m.read("layers.err", 0, np.uint32)[0] == 0
@@ -370,6 +374,35 @@ def test_qwen3_config4_greedy_256(ctx, config4):
     m, w = config4
     prompt = np.random.default_rng(42).integers(0, QWEN_CONFIG4.vocab, (1, 32))
     _batch_greedy_check(m, w, prompt, 256, "qwen3-config4-b1")
+
+
+def test_qwen3_config4_xcd_local_placement_bit_identical(ctx, config4, monkeypatch):
+    # Batch 1 at configs[4]'s shape runs XCD-local: KV head h's QKV tiles,
+    # attention splits and merge items on XCD h, their cells stored into
+    # that XCD's L2. The items and their arithmetic are the same as with the
+    # default placement (STRICT_HIP_LLM_XCD=0), so logits and tokens of 24
+    # greedy steps after a 600-token prompt (19 active splits) are equal bit
+    # for bit.
+    m, _ = config4
+    prompt = np.random.default_rng(77).integers(0, QWEN_CONFIG4.vocab, 600)
+    runs = []
+    for xcd in ("1", "0"):
+        monkeypatch.setenv("STRICT_HIP_LLM_XCD", xcd)
+        m.reset(1)
+        for i, t in enumerate(prompt):
+            m.step([int(t)], logits=(i == len(prompt) - 1))
+        toks, logits = [], []
+        for j in range(24):
+            logits.append(m.logits()[0].copy())
+            toks.append(int(m.next_tokens()[0]))
+            if j + 1 < 24:
+                m.step(None, logits=True)
+        runs.append((np.array(toks), np.array(logits)))
+        print(f"STRICT_HIP_LLM_XCD={xcd}: tokens {toks[:8]}", flush=True)
+    monkeypatch.delenv("STRICT_HIP_LLM_XCD")
+    m.reset(1)
+    assert np.array_equal(runs[0][0], runs[1][0])
+    assert np.array_equal(runs[0][1], runs[1][1])
 
 
 @pytest.mark.parametrize("batch", [4, 6, 8, 16])
@@ -546,6 +579,33 @@ def test_generate_matches_stepwise(ctx):
         assert np.array_equal(gen, np.array(steps))
         hist = m.read("hist", 0, np.int32)[: len(prompt)]
         assert np.array_equal(hist, prompt)
+
+
+def test_gpt2_key_sets_across_batch_sizes(ctx):
+    # GPT-2 runs its layers kernel at batch 1 (one launch per step, which
+    # embeds the token itself and advances the step number, alternating the
+    # two argmax key sets) and the per-op path, graph-replayed, at batch 2.
+    # Between the two rounds' batch-2 runs, 15 + 16 = 31 layers-kernel steps
+    # move the current key set; each run must repeat the first round's tokens
+    # (a graph replayed on the other key set would not), and the history
+    # must hold the prompt and the generated tokens.
+    prompts = np.random.default_rng(31).integers(0, GPT2_SMALL_TEST.vocab, (2, 10))
+    plan = ((1, 7), (2, 6), (1, 6))
+    with llm.Model(ctx, GPT2_SMALL_TEST) as m:
+        m.init_random(seed=3, stddev=0.02)
+        first = {}
+        for rnd in range(2):
+            for b, steps in plan:
+                m.reset(b)
+                toks = m.generate(prompts[:b], steps)
+                print(f"round {rnd} batch {b} steps {steps}: {toks[0][:6]}", flush=True)
+                if rnd == 0:
+                    first[(b, steps)] = toks
+                else:
+                    assert np.array_equal(toks, first[(b, steps)]), (b, steps)
+                hist = m.read("hist", 0, np.int32)[:10 + steps - 1]
+                assert np.array_equal(hist[:10], prompts[0])
+                assert np.array_equal(hist[10:], toks[0][:steps - 1])
 
 
 def test_llm_rejects_bad_arguments(ctx):
