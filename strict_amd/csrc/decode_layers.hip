@@ -142,6 +142,13 @@ __device__ __forceinline__ void cst2(uint64_t *base, size_t cell, uint32_t v0, u
   cst1(base, cell + 1, v1, tag, local);
 }
 
+// The XCD this wave runs on (hardware register XCC_ID).
+__device__ __forceinline__ unsigned xcc_id() {
+  unsigned v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return v & 0xf;
+}
+
 __device__ __forceinline__ float f32_of(uint32_t u) { return __builtin_bit_cast(float, u); }
 __device__ __forceinline__ uint32_t bits_of(float f) { return __builtin_bit_cast(uint32_t, f); }
 
@@ -1531,14 +1538,18 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
   const int nA = a.qkv_n / 16, nB = B * a.kv_heads * a.splits, nM = B * a.heads * kMergeParts;
   const int nC = H / 16, nD = a.inter / 16, nE = H / 16;
   const int d0 = (w + G - nC % G) % G;  // this workgroup's first gate/up item
-  // XCD-local placement (batch 1, a.xcd): workgroup w = h + 8 j, on XCD h
-  // (workgroups go to the XCDs round robin), runs KV head h's j-th QKV tile
-  // (its kG query heads' q tiles, then its k, then its v tiles), its split j
-  // and, on the last kG * kMergeParts workgroups of the XCD, its query
-  // heads' merge items: the QKV -> attention and attention -> merge cells
-  // never leave the XCD.
+  // XCD-local placement (batch 1, a.xcd): the workgroup on XCD h (XCC_ID)
+  // with rank j = w / 8 runs KV head h's j-th QKV tile (its kG query heads'
+  // q tiles, then its k, then its v tiles), its split j and, on the last
+  // kG * kMergeParts ranks, its query heads' merge items: the QKV ->
+  // attention and attention -> merge cells never leave the XCD. Workgroups
+  // go to the XCDs round robin from an XCD that varies between launches
+  // (measured: w on XCD w % 8 in a fresh process, on (w + 7) % 8 after
+  // other launches), so an XCD holds one residue class of w mod 8 and
+  // (XCD, w / 8) names every role once.
   const bool xl = kOne && a.xcd != 0;
-  const int xh = w & 7, xj = w >> 3, xw = G >> 3;
+  const unsigned xcc = xl ? xcc_id() : 0u;
+  const int xh = (int)(xcc & 7), xj = w >> 3, xw = G >> 3;
   constexpr int kTiles = kD / 16;  // 16-row tiles per head
   const int xq = xj < kG * kTiles ? xh * kG * kTiles + xj
                  : xj < (kG + 1) * kTiles ? a.heads * kTiles + xh * kTiles + (xj - kG * kTiles)
@@ -1546,11 +1557,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
                                                 (xj - (kG + 1) * kTiles);
   const int xm = xj >= xw - kG * kMergeParts ? xh * kG * kMergeParts + (xj - (xw - kG * kMergeParts)) : nM;
   const int m0 = xl ? xm : G - 1 - w;  // its first merge item
-  if (xl && threadIdx.x == 0) {
-    unsigned xcc;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-    if ((xcc & 0xf) != (unsigned)xh) atomicOr(a.err, 2u);  // every wait then fails at once
-  }
+  if (xl && threadIdx.x == 0 && xcc >= 8) atomicOr(a.err, 2u);  // every wait then fails at once
   const bool hasC = w < nC;
   // attention items: workgroup w runs items [bA, eA), one at batch 1; at
   // larger batches a contiguous run of the active items (splits within

@@ -37,7 +37,7 @@
 // and layer: slots 0..4 the ends of its A..E items, 5..9 the ends of their
 // waits, 10 the kernel's start (layer 0), 11 the head's end (layer 0),
 // 12..15 the ends of the attention item's q / k / v staging, scores,
-// softmax and V sums.
+// softmax and V sums; layer 15 slot 15: the XCD the workgroup ran on.
 constexpr int kTrWgs = 256, kTrLayers = 16, kTrSlots = 16;
 __device__ unsigned long long g_gpt2_trace[kTrWgs][kTrLayers][kTrSlots];
 #define SH_G2MARK(l, slot)                                                              \
@@ -279,10 +279,11 @@ __device__ __forceinline__ bool stage_f16(const Gpt2Args &a, const uint64_t *cel
   return true;
 }
 
-// A: qkv[16 i + c] = W_qkv LayerNorm(x) + b; w holds the item's weights
+// A: qkv[16 i + c] = W_qkv LayerNorm(x) + b; w holds the item's weights;
+// local: every consumer of the cells runs on this XCD (cst)
 template <int kLH>
 __device__ __forceinline__ bool qkv_item(const Gpt2Args &a, const LayerP &P, int l, int i, unsigned ep,
-                                         const Emb &e, Lds &S, const u32x4 (&w)[kLH]) {
+                                         const Emb &e, Lds &S, const u32x4 (&w)[kLH], bool local) {
   const int lane = threadIdx.x & 63, col = lane & 15;
   const float bias = P.bqkv[i * 16 + col];
   __builtin_amdgcn_sched_barrier(0);
@@ -291,7 +292,7 @@ __device__ __forceinline__ bool qkv_item(const Gpt2Args &a, const LayerP &P, int
     return false;
   SH_G2WAIT(l, 0);
   f32x4 acc = reduce_waves(mfma_weights<kLH>(w, S.xs), S);
-  if (threadIdx.x < 16) cst(a.qkvc, (size_t)i * 16 + col, bits_of(acc[0] + bias), tag_of(ep, l));
+  if (threadIdx.x < 16) cst(a.qkvc, (size_t)i * 16 + col, bits_of(acc[0] + bias), tag_of(ep, l), local);
   SH_G2MARK(l, 0);
   return true;
 }
@@ -707,22 +708,45 @@ __global__ __launch_bounds__(kT, 1) void gpt2_layers_kernel(const Gpt2Args a) {
   const int L = pos + 1;  // context including this step's token
   const int G = gridDim.x, w = blockIdx.x;
   const int nA = a.qkv_n / 16, nB = a.heads * kGpt2Splits, nC = a.H / 16, nD = a.inter / 16;
+  // this workgroup's QKV tile (qa) and attention item (bi), when >= 0: by
+  // default the QKV tiles on workgroups 0.. and the attention items on the
+  // last ones; XCD-local (a.xcd): the workgroup on XCD x (XCC_ID) with rank
+  // j = w / 8 runs for head x (j < 12) and head x + 8 (12 <= j < 24) their
+  // 12 QKV tiles (q, k, v: 4 each), and their splits on j = 24 .. 27 and
+  // 28 .. 31, so the q / k / v cells never leave the XCD. Workgroups go to
+  // the XCDs round robin from an XCD that varies between launches, so an
+  // XCD holds one residue class of w mod 8 and (XCD, w / 8) names every
+  // role once.
+  const bool xl = a.xcd != 0;
+  int qa = w < nA ? w : -1, bi = w - (G - nB);
+  if (xl) {
+    constexpr int kT4 = kHd / 16, kT12 = 3 * kT4;  // tiles per head: of q (k, v); of all three
+    const unsigned xcc = xcc_id();
+    const int x = (int)(xcc & 7), j = w >> 3;
+    const int hq = j < kT12 ? x : (j < 2 * kT12 ? x + 8 : a.heads), t = j % kT12;
+    qa = hq < a.heads ? (t / kT4) * a.heads * kT4 + hq * kT4 + t % kT4 : -1;
+    const int jb = j - 2 * kT12, hb = jb < kGpt2Splits ? x : x + 8;
+    bi = jb >= 0 && hb < a.heads ? hb * kGpt2Splits + jb % kGpt2Splits : -1;
+    if (threadIdx.x == 0 && xcc >= 8) atomicOr(a.err, 2u);  // every wait then fails
+  }
+#ifdef SH_GPT2_TRACE
+  if (threadIdx.x == 0 && w < kTrWgs) g_gpt2_trace[w][kTrLayers - 1][kTrSlots - 1] = xcc_id();
+#endif
   Emb emb;
-  if (w < nA) {
+  if (qa >= 0 || w < nC || w == 0) {
     emb.tok = step_token(a.keys + (size_t)(ep0 & 1) * kKeySet, 0, a.vocab);
     emb.wte = gbl(a.head_w);
     emb.wpe_row = gbl(a.wpe) + (size_t)min(pos, a.max_pos - 1) * a.H;
   }
-  const int bi = w - (G - nB);  // this workgroup's attention item (when >= 0)
   const bool hasD = w >= nC && w < nC + nD;
   AttnKV kv;
   u32x4 wa[kLH];
-  if (w < nA) load_weights<kLH>(wa, layer_p(a, 0).wqkv, a.H, w);
+  if (qa >= 0) load_weights<kLH>(wa, layer_p(a, 0).wqkv, a.H, qa);
   if (bi >= 0) attn_prefetch(a, layer_p(a, 0), bi, L, kv);
   for (int l = 0; l < a.n_layers; l++) {
     const LayerP P = layer_p(a, l);
     const bool next = l + 1 < a.n_layers;
-    if (w < nA && !qkv_item<kLH>(a, P, l, w, ep, emb, S, wa)) return;
+    if (qa >= 0 && !qkv_item<kLH>(a, P, l, qa, ep, emb, S, wa, xl)) return;
     if (bi >= 0) {
       if (!attn_item(a, P, l, bi, ep, L, S, kv)) return;
       if (next && !hasD) attn_prefetch(a, layer_p(a, l + 1), bi, L, kv);
@@ -736,20 +760,20 @@ __global__ __launch_bounds__(kT, 1) void gpt2_layers_kernel(const Gpt2Args a) {
     u32x4 wp[kLI];
     if (w < nC) {
       load_weights<kLI>(wp, P.wproj, a.inter, w);
-      if (next && w < nA) load_weights<kLH>(wa, layer_p(a, l + 1).wqkv, a.H, w);
+      if (next && qa >= 0) load_weights<kLH>(wa, layer_p(a, l + 1).wqkv, a.H, qa);
     }
     if (w < nC && !o_item<kLH>(a, P, l, w, ep, L, emb, S)) return;
     if (hasD) {
       if (!fc_item<kLH>(a, P, l, w - nC, ep, S)) return;
       if (next) {
         if (bi >= 0) attn_prefetch(a, layer_p(a, l + 1), bi, L, kv);
-        if (w < nA) load_weights<kLH>(wa, layer_p(a, l + 1).wqkv, a.H, w);
+        if (qa >= 0) load_weights<kLH>(wa, layer_p(a, l + 1).wqkv, a.H, qa);
       }
     }
     if (w < nC) {
       if (!proj_item<kLH, kLI>(a, P, l, w, ep, S, wp)) return;
     }
-    if (next && w < nA && w >= nC + nD) load_weights<kLH>(wa, layer_p(a, l + 1).wqkv, a.H, w);
+    if (next && qa >= 0 && w >= nC + nD) load_weights<kLH>(wa, layer_p(a, l + 1).wqkv, a.H, qa);
   }
   if (a.head_on) {
     u32x4 wb[2][4 * kLH];
@@ -788,6 +812,13 @@ bool gpt2_layers_supported(int layers, int H, int heads, int head_dim, int inter
 
 int gpt2_layers_chunk(int max_pos) {
   return ((max_pos + kGpt2Splits - 1) / kGpt2Splits + 15) / 16 * 16;
+}
+
+bool gpt2_layers_xcd_ok(const Gpt2Args &a, int grid) {
+  // 2 heads per XCD at most, each with 12 QKV tiles and kGpt2Splits splits
+  return grid % 8 == 0 && a.heads <= 16 && a.qkv_n == 3 * a.heads * kHd && a.H == a.heads * kHd &&
+         2 * (3 * kHd / 16 + kGpt2Splits) <= grid / 8 && a.qkv_n / 16 <= grid &&
+         a.heads * kGpt2Splits <= grid;
 }
 
 size_t gpt2_layers_partial_cells(int heads) { return (size_t)heads * kGpt2Splits * kGpt2PStride; }

@@ -129,13 +129,13 @@ struct LayersArgs {
                                        // (embed kernel), last layer's output
   uint64_t *x0c = nullptr, *x1c = nullptr, *qkvc = nullptr, *partc = nullptr;
   uint64_t *attnc = nullptr, *actc = nullptr;
-  unsigned *err = nullptr;             // set when a wait timed out (sticky); bit 1: a
-                                       // workgroup was off its XCD in XCD-local mode
+  unsigned *err = nullptr;             // set when a wait timed out (sticky); bit 1: an
+                                       // XCD id outside 0..7 in XCD-local mode
   unsigned long long spin_ticks = 0;   // wall-clock ticks a wait may take
   int lds_misc = 0;                    // byte offset of the small LDS scratch words
   // batch 1: KV head h's QKV, attention and merge items on the workgroups
-  // w % 8 == h (XCD h), their cells stored into that XCD's L2
-  // (decode_layers_xcd_ok must hold)
+  // of XCD h, their cells stored into that XCD's L2 (decode_layers_xcd_ok
+  // must hold)
   int xcd = 0;
   // final RMSNorm + LM head inside the kernel (steps with logits; head_on 0:
   // the kernel ends with the last layer)
@@ -211,8 +211,13 @@ struct Gpt2Args {
   const uint16_t *wpe = nullptr;     // positions [max_pos][H] fp16 (token rows: head_w)
   float *x_in = nullptr;             // [H] last layer's output
   uint64_t *x0c = nullptr, *x1c = nullptr, *qkvc = nullptr, *partc = nullptr, *actc = nullptr;
-  unsigned *err = nullptr;           // set when a wait timed out (sticky)
+  unsigned *err = nullptr;           // set when a wait timed out (sticky); bit 1: an
+                                     // XCD id outside 0..7 in XCD-local mode
   unsigned long long spin_ticks = 0;  // wall-clock ticks a wait may take
+  // head h's QKV tiles and attention splits on the workgroups of XCD h % 8,
+  // the q / k / v cells stored into that XCD's L2 (gpt2_layers_xcd_ok must
+  // hold)
+  int xcd = 0;
   // final LayerNorm + LM head inside the kernel (steps with logits)
   int head_on = 0;
   const uint16_t *head_w = nullptr;  // fp16 tiled [head_tiles * 16][H] (tied embedding)
@@ -226,6 +231,9 @@ struct Gpt2Args {
 bool gpt2_layers_supported(int layers, int H, int heads, int head_dim, int inter, int max_pos,
                            int grid);
 int gpt2_layers_chunk(int max_pos);
+// Whether the XCD-local placement fits: with `grid` workgroups, grid / 8 per
+// XCD, the heads h and h + 8 of XCD h % 8 with their QKV tiles and splits.
+bool gpt2_layers_xcd_ok(const Gpt2Args &a, int grid);
 size_t gpt2_layers_partial_cells(int heads);
 hipError_t gpt2_layers_occupancy(const Gpt2Args &a, int *blocks_per_cu);
 // Ordinary launch on stream s; needs its `grid` workgroups resident together

@@ -96,7 +96,8 @@ struct sh_llm {
   // the device's step number (*epoch), mirrored: one more per step of a
   // layers kernel; its parity selects the current key set
   unsigned epoch_host = 0;
-  bool xcd_off = false;  // a step found a workgroup off its XCD: no XCD-local placement
+  bool xcd_off = false;  // a step failed in XCD-local placement: none (either layers
+                         // kernel) from the next reset on
   // persistent GPT-2 layers kernel (batch 1; other batches keep the per-op
   // kernels, which share its cache layout)
   bool gpt2_kernel = false;
@@ -860,7 +861,11 @@ SH_API int sh_llm_reset(sh_llm *m, int batch) {
     m->layers_lds = decode_layers_lds(batch, c.hidden, c.heads, c.intermediate, &a.lds_misc);
     SH_HIP_TRY(hipMemsetAsync(a.err, 0, 4, s));
   }
-  if (m->gpt2_kernel) SH_HIP_TRY(hipMemsetAsync(m->ga.err, 0, 4, s));
+  if (m->gpt2_kernel) {
+    const char *xe = getenv("STRICT_HIP_LLM_XCD");
+    m->ga.xcd = !(xe && xe[0] == '0') && !m->xcd_off && gpt2_layers_xcd_ok(m->ga, m->gpt2_grid) ? 1 : 0;
+    SH_HIP_TRY(hipMemsetAsync(m->ga.err, 0, 4, s));
+  }
   return SH_OK;
 }
 
@@ -928,11 +933,14 @@ SH_API int sh_llm_next_tokens(sh_llm *m, int32_t *tokens) {
   else if (m->gpt2_kernel && m->batch == 1)
     SH_HIP_TRY(hipMemcpyAsync(&err, m->ga.err, 4, hipMemcpyDeviceToHost, s));
   SH_HIP_TRY(hipStreamSynchronize(s));
-  if (m->layers_kernel && (err & 2u)) {
+  // a failed step in XCD-local placement turns it off from the next reset
+  // on: a grid whose workgroups were not spread over the XCDs round robin
+  // would leave roles unrun, and their consumers' waits would time out
+  if (err && ((m->layers_kernel && m->la.xcd) || (m->gpt2_kernel && m->batch == 1 && m->ga.xcd)))
     m->xcd_off = true;
-    return fail(SH_ERR_HIP, "decode-layers kernel: a workgroup ran off the XCD its placement assumes "
-                            "(step state lost; reset the model, which turns the XCD-local placement off)");
-  }
+  if (err & 2u)
+    return fail(SH_ERR_HIP, "layers kernel: a workgroup read an XCD id outside 0..7 in XCD-local "
+                            "placement (step state lost; reset the model, which turns that placement off)");
   if (err)
     return fail(SH_ERR_HIP, "decode-layers kernel: a wait between workgroups timed out (step state lost; reset the model)");
   for (int b = 0; b < m->batch; b++) {

@@ -244,15 +244,15 @@ def test_per_op_path_without_graphs(ctx, monkeypatch, cfg):
 
 
 @pytest.mark.parametrize("cfg,err,text", [(QWEN_SMALL, 1, "timed out"), (GPT2_SMALL_TEST, 1, "timed out"),
-                                          (QWEN_SMALL, 2, "off the XCD")],
-                         ids=["qwen3", "gpt2", "qwen3-placement-bit"])
+                                          (QWEN_SMALL, 2, "outside 0..7"), (GPT2_SMALL_TEST, 2, "outside 0..7")],
+                         ids=["qwen3", "gpt2", "qwen3-placement-bit", "gpt2-placement-bit"])
 def test_decode_layers_wait_failure_reported_and_reset_recovers(ctx, cfg, err, text):
     # The bounded waits of the persistent layers kernels (Qwen3's decode-layers
     # kernel, GPT-2's layers kernel): the host sets the sticky error word
     # before a step, so every wait between workgroups gives up after a few
     # polls and the kernel ends normally; sh_llm_next_tokens reports the
-    # failed step (bit 1: the Qwen3 kernel found a workgroup off the XCD its
-    # XCD-local placement assumes, which also turns that placement off), and
+    # failed step (bit 1: a workgroup read an XCD id outside 0..7 in the
+    # XCD-local placement; a failed step in that placement turns it off), and
     # sh_llm_reset clears the error.
     prompt = np.random.default_rng(5).integers(0, cfg.vocab, 12)
     with llm.Model(ctx, cfg) as m:
@@ -579,6 +579,34 @@ def test_generate_matches_stepwise(ctx):
         assert np.array_equal(gen, np.array(steps))
         hist = m.read("hist", 0, np.int32)[: len(prompt)]
         assert np.array_equal(hist, prompt)
+
+
+@pytest.mark.parametrize("cfg", [GPT2_SMALL_TEST, llm.GPT2_SMALL], ids=["small-shape", "gpt2-small"])
+def test_gpt2_xcd_local_placement_bit_identical(ctx, monkeypatch, cfg):
+    # The GPT-2 layers kernel with head h's QKV tiles and attention splits on
+    # XCD h % 8 (q / k / v cells stored into that XCD's L2) against the
+    # default placement (STRICT_HIP_LLM_XCD=0): same items, same arithmetic,
+    # so tokens and logits of 20 greedy steps after a 40-token prompt are
+    # equal bit for bit.
+    prompt = np.random.default_rng(8).integers(0, cfg.vocab, 40)
+    runs = []
+    with llm.Model(ctx, cfg) as m:
+        m.init_random(seed=5, stddev=0.02)
+        for xcd in ("1", "0"):
+            monkeypatch.setenv("STRICT_HIP_LLM_XCD", xcd)
+            m.reset(1)
+            for i, t in enumerate(prompt):
+                m.step([int(t)], logits=(i == len(prompt) - 1))
+            toks, logits = [], []
+            for j in range(20):
+                logits.append(m.logits()[0].copy())
+                toks.append(int(m.next_tokens()[0]))
+                if j + 1 < 20:
+                    m.step(None, logits=True)
+            runs.append((np.array(toks), np.array(logits)))
+            print(f"STRICT_HIP_LLM_XCD={xcd}: tokens {toks[:8]}", flush=True)
+    assert np.array_equal(runs[0][0], runs[1][0])
+    assert np.array_equal(runs[0][1], runs[1][1])
 
 
 def test_gpt2_key_sets_across_batch_sizes(ctx):
