@@ -505,18 +505,24 @@ SH_API int sh_llm_load_linear(sh_llm *model, const char *name, int layer, const 
  * "<linear>.w" (tiled layout), "<linear>.scale", "<linear>.bias", "norm1.g",
  * "norm1.b", "norm2.g", "norm2.b", "q_norm", "k_norm", "final.g", "final.b",
  * "wpe", "inv_freq", "kcache", "vcache" (per layer), "logits", "hist", "lens";
- * "layers.err" exists only when the persistent decode-layers kernel runs the
- * layers (Qwen3 shapes it is built for, cooperative launch available, and
- * STRICT_HIP_LLM_LAYERS not "0" when the model is created). */
+ * "layers.err" exists only when a persistent layers kernel runs the layers:
+ * the Qwen3 decode-layers kernel (shapes it is built for, cooperative launch
+ * available) or the GPT-2 layers kernel (batch 1), with STRICT_HIP_LLM_LAYERS
+ * not "0" when the model is created. */
 SH_API int sh_llm_tensor(sh_llm *model, const char *name, int layer, void **device_ptr,
                          size_t *bytes);
-/* Starts `batch` empty sequences (clears the KV lengths). */
+/* Starts `batch` empty sequences (clears the KV lengths, the greedy keys and
+ * a failed step's error word). */
 SH_API int sh_llm_reset(sh_llm *model, int batch);
 /* One decode step for every sequence: embeds tokens[b] (host array) or, when
  * tokens is NULL, the greedy token the previous step produced; runs the layers;
  * with want_logits, the LM head writes logits and the greedy (argmax) token. */
 SH_API int sh_llm_step(sh_llm *model, const int32_t *tokens, int want_logits);
-/* Waits for the stream and copies the greedy tokens of the last step (host). */
+/* Waits for the stream and copies the greedy tokens of the last step (host).
+ * SH_ERR_HIP when a persistent layers kernel's wait between workgroups gave up
+ * in a step since the last reset: the steps' state is lost and the model needs
+ * sh_llm_reset (which also turns an XCD-local placement off for the rest of
+ * the model's life if the failed step used it). */
 SH_API int sh_llm_next_tokens(sh_llm *model, int32_t *tokens);
 /* prompt[b * prompt_len + i] (host): prompt_len steps, then greedy decoding
  * until `steps` tokens per sequence are produced into out[b * steps + j]. */
