@@ -37,7 +37,8 @@
 // and layer: slots 0..4 the ends of its A..E items, 5..9 the ends of their
 // waits, 10 the kernel's start (layer 0), 11 the head's end (layer 0),
 // 12..15 the ends of the attention item's q / k / v staging, scores,
-// softmax and V sums; layer 15 slot 15: the XCD the workgroup ran on.
+// softmax and V sums; layer 15 slot 15: the XCD the workgroup ran on;
+// layer n_layers slot 0: the end of the LM head's final-LayerNorm wait.
 constexpr int kTrWgs = 256, kTrLayers = 16, kTrSlots = 16;
 __device__ unsigned long long g_gpt2_trace[kTrWgs][kTrLayers][kTrSlots];
 #define SH_G2MARK(l, slot)                                                              \
@@ -631,6 +632,7 @@ __device__ __forceinline__ bool head_phase(const Gpt2Args &a, unsigned ep, Lds &
   if (!stage_ln<(kLH * 128 + 1023) / 1024, false>(a, a.x0c, Emb{}, tag_of(ep, a.n_layers - 1),
                                             gbl(a.final_g), gbl(a.final_b), a.H, S))
     return false;
+  SH_G2MARK(a.n_layers, 0);
   const _Float16 *xrow = S.xs + 8 * (lane >> 4);
   unsigned long long best = 0;
   auto tile = [&](const u32x4 (&wt)[4 * kLH], int j) {
