@@ -266,7 +266,8 @@ __device__ __forceinline__ bool waits_ok(const LayersArgs &a, bool ok, Misc *mis
 // stored), merge 14..15 (polled, stored), and the end of each phase's items
 // on this workgroup (all of them, not only the first): 16 QKV, 17
 // attention, 18 merge, 19 O, 20 gate/up, 21 down; 22 an attention item's
-// start (with 8..13, the workgroup's last item's).
+// start (with 8..13, the workgroup's last item's); at layer n_layers, 0 the
+// end of the LM head's final-RMSNorm wait and 1 the workgroup's end.
 __device__ unsigned long long g_decode_trace[2][kTraceWgs][kTraceLayers][kTraceSlots];
 __device__ __forceinline__ void trace_mark(Misc *misc, int set, int l, int slot) {
   if (threadIdx.x == 0 && l < kTraceLayers) misc->tr[set][l][slot] = wall_clock64();
@@ -1427,6 +1428,7 @@ __device__ __forceinline__ bool head_phase(const LayersArgs &a, unsigned ep, con
   if (!stage_rms<(kLA + 3) / 4, kRows, false>(a, a.x0c, nullptr, tag_of(ep, a.n_layers - 1), gbl(a.final_g),
                                        H, s.xs, s.misc))
     return false;
+  SH_MARK(s.misc, a.n_layers, 0);  // the final RMSNorm's input has arrived
   const int arow = lane & 15, acol = 8 * (lane >> 4);
   const _Float16 *xrow = s.xs + (arow < B ? arow : 0) * (H + 8) + acol;
   unsigned long long best[4] = {0, 0, 0, 0};
@@ -1762,6 +1764,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
     SH_MARK(misc, l, 21);
   }
   if (a.head_on && !head_phase<kLA, kRows>(a, ep, lds)) return;
+  SH_MARK(misc, a.n_layers, 1);
 #ifdef SH_DECODE_TRACE
   lds_barrier();
   if (w < kTraceWgs)

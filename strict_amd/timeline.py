@@ -68,7 +68,8 @@ def _sub(a: np.ndarray, b: np.ndarray) -> float:
 def decode(prompt_len: int) -> str:
     """Qwen3 decode-layers kernel, batch 1 (tr[0]: per phase start / end /
     wait end, merge end, first attention items' ends; tr[1]: marks inside
-    items)."""
+    items, and at layer n_layers the LM head's final-RMSNorm wait end and
+    the workgroup's end)."""
     import strict_amd
     from strict_amd import _lib, llm
 
@@ -119,6 +120,13 @@ def decode(prompt_len: int) -> str:
     out.append("  down item: staged %.0f, MFMA %.0f, cross-wave sum %.0f, store %.0f" % (
         per(lambda l: _sub(t[:, l, 14], t2[:, l, 4])), per(lambda l: _sub(t2[:, l, 4], t2[:, l, 5])),
         per(lambda l: _sub(t2[:, l, 5], t2[:, l, 6])), per(lambda l: _sub(t2[:, l, 6], t2[:, l, 7]))))
+    hw, he, de = t2[:, L, 0], t2[:, L, 1], _max(t[:, L - 1, 9])
+    head_bytes = cfg.vocab * cfg.hidden + cfg.vocab * 4  # FP8 rows and their scales
+    if (hw >= 0).any() and (he >= 0).any():
+        span = _max(he) - _med(hw)
+        out.append(f"  LM head: final-RMSNorm input arrived {_med(hw) - de:.0f} after the last down end "
+                   f"(median), then {span:.0f} to the last workgroup's end: {head_bytes / span / 1e3:.2f} TB/s "
+                   f"over {head_bytes:,} B of head rows and scales")
     return "\n".join(out)
 
 
