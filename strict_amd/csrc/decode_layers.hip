@@ -21,11 +21,14 @@
 // producer never waits for its stores to complete, and a consumer needs one
 // memory round trip once the data has landed (a flag word would cost the
 // producer's store-completion wait, the flag poll and then the data read).
-// Every cell access is a relaxed 64-bit agent-scope atomic: the memory
-// model keeps those coherent across the XCDs' separate L2 caches (measured
-// here: ~0.35-0.45 us from a store to another XCD's poll seeing it, against
-// ~0.55-0.63 us through uncached memory), and the compiler neither hoists
-// such a load out of a spin loop nor waits after each one.
+// Every cell load is a relaxed 64-bit agent-scope atomic, and so is every
+// cell store except the XCD-local ones (cst1): the memory model keeps those
+// coherent across the XCDs' separate L2 caches (measured here: ~0.35-0.45
+// us from a store to another XCD's poll seeing it, against ~0.55-0.63 us
+// through uncached memory), and the compiler neither hoists such a load out
+// of a spin loop nor waits after each one. The XCD-local stores (workgroup
+// scope) stay in the producer's XCD L2, where the polls of that XCD's CUs
+// find them sooner.
 //
 // Weights and K / V do not depend on the step's activations, so each
 // workgroup requests them for its next items right after it has finished

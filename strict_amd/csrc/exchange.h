@@ -2,9 +2,10 @@
 // within a launch travel in 8-byte cells of device memory, payload in the
 // low word and the producing (step, layer) tag in the high word. A consumer
 // loads the cells it needs until each carries the tag it expects, so the data
-// is its own completion flag. Every cell access is a relaxed 64-bit
-// agent-scope atomic, which the memory model keeps coherent across the XCDs'
-// separate L2 caches. Every wait is bounded by a wall-clock limit; a timeout
+// is its own completion flag. Every cell load is a relaxed 64-bit
+// agent-scope atomic, and so is every cell store except the XCD-local ones
+// (cst with `local`): the memory model keeps those coherent across the
+// XCDs' separate L2 caches. Every wait is bounded by a wall-clock limit; a timeout
 // sets the sticky error word, after which every other wait gives up at once,
 // so the grid always drains.
 //
