@@ -60,6 +60,8 @@
 namespace sh {
 namespace {
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
 constexpr int kT = 256;         // threads per workgroup (4 waves)
 constexpr int kD = 128;         // head dim
 constexpr int kMaxSplits = 64;  // splits per (row, KV head) a merge item combines
@@ -389,16 +391,41 @@ __device__ __forceinline__ bool stage_chunk_ok(int K, int j) {
   return (threadIdx.x & 63) + 64 * j < (K >> 4);
 }
 
+// The first layer's input of a batch-1 step that embeds its own token
+// (LayersArgs::fold): row `tok` of the tied FP8 head times its scale, each
+// value converted as the embed kernel converts it (E4M3 -> fp16 -> fp32,
+// then the scale).
+struct EmbQ {
+  int tok = -1;  // < 0: the input comes from x_in (the embed kernel's) or cells
+  const SH_GLOBAL uint8_t *head8 = nullptr;
+  float scale = 0.0f;
+};
+
+// Values k .. k + 3 (k a multiple of 4: four contiguous bytes of the tile).
+__device__ __forceinline__ f32x4 embq4(const EmbQ &e, int k, int K) {
+  const uint32_t q = *reinterpret_cast<const SH_GLOBAL uint32_t *>(e.head8 + fp8_tiled_offset(e.tok, k, K));
+  const f16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(q, 1.0f, false);
+  const f16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(q, 1.0f, true);
+  return f32x4{(float)lo[0] * e.scale, (float)lo[1] * e.scale, (float)hi[0] * e.scale,
+               (float)hi[1] * e.scale};
+}
+
+__device__ __forceinline__ float embq1(const EmbQ &e, int k, int K) {
+  const uint8_t q = e.head8[fp8_tiled_offset(e.tok, k, K)];
+  return (float)__builtin_amdgcn_cvt_scalef32_pk_f16_fp8((uint32_t)q, 1.0f, false)[0] * e.scale;
+}
+
 // Rows [B][K] of fp32 x -> RMSNorm with gains g -> xs (fp16, row stride
 // K + 8), kRows rows per pass. The rows come from cells xc tagged `tag` or,
 // for the first layer, from the plain buffer xp the embedding kernel wrote
-// before this launch. Each thread keeps its 4-value chunks (stage_chunk) in
+// before this launch or (batch 1, e.tok >= 0) from the embedding table. Each thread keeps its 4-value chunks (stage_chunk) in
 // registers; the per-row sums of squares are combined across the four
 // waves through LDS. kChunks >= K / 1024. kLocal: the caller's waves read
 // only their own K quarter of xs, so no barrier follows the stores.
 template <int kChunks, int kRowsMax, bool kLocal>
 __device__ __forceinline__ bool stage_rms(const LayersArgs &a, const uint64_t *xc, const float *xp, unsigned tag,
-                          const SH_GLOBAL float *g, int K, _Float16 *xs, Misc *misc) {
+                          const SH_GLOBAL float *g, int K, _Float16 *xs, Misc *misc,
+                          const EmbQ &e = EmbQ{}) {
   typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
   // rows per pass: at most kRowsMax, and at most 64 cells per thread
   constexpr int kRows = kRowsMax * kChunks * 4 <= 64 ? kRowsMax : 64 / (kChunks * 4);
@@ -412,7 +439,10 @@ __device__ __forceinline__ bool stage_rms(const LayersArgs &a, const uint64_t *x
   for (int b0 = 0; b0 < B; b0 += kRows) {
     f32x4 v[kRows][kChunks];
     bool ok = true;
-    if (xp) {
+    if (kRowsMax == 1 && e.tok >= 0) {
+#pragma unroll
+      for (int j = 0; j < kChunks; j++) v[0][j] = embq4(e, min(stage_chunk(K, j), c4 - 1) * 4, K);
+    } else if (xp) {
 #pragma unroll
       for (int r = 0; r < kRows; r++)
 #pragma unroll
@@ -549,7 +579,7 @@ constexpr int kOutRows = kRows == 1 ? 1 : 4;
 template <int kR>
 __device__ __forceinline__ void request_residual(const LayersArgs &a, const uint64_t *xc,
                                                  const float *xp, int col, float (&rv)[4],
-                                                 uint64_t (&rc)[4]) {
+                                                 uint64_t (&rc)[4], const EmbQ &e = EmbQ{}) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int r = 0; r < 4; r++) {
@@ -557,7 +587,9 @@ __device__ __forceinline__ void request_residual(const LayersArgs &a, const uint
     rc[r] = r < kR ? cld(xc, (size_t)b * a.H + col) : 0ull;  // rows past kR: unused
     rv[r] = 0.0f;
   }
-  if (xp) {
+  if (kR == 1 && e.tok >= 0) {
+    rv[0] = embq1(e, col, a.H);
+  } else if (xp) {
 #pragma unroll
     for (int r = 0; r < kR; r++) {
       const int b = min(4 * (lane >> 4) + r, a.B - 1);
@@ -596,7 +628,8 @@ __device__ __forceinline__ void consume_cells(const uint64_t (&c)[4]) {
 // cells runs on this XCD (cst1)
 template <int kL, int kRows>
 __device__ __forceinline__ bool qkv_item(const LayersArgs &a, const LayerG &P, int l, int i, unsigned ep,
-                         const Lds &s, const u32x4 (&w)[kL][1], bool reuse, bool local) {
+                         const Lds &s, const u32x4 (&w)[kL][1], bool reuse, bool local,
+                         const EmbQ &e) {
   const int lane = threadIdx.x & 63, col = lane & 15;
   const float sc = P.sqkv[i * 16 + col];
   __builtin_amdgcn_sched_barrier(0);
@@ -606,7 +639,7 @@ __device__ __forceinline__ bool qkv_item(const LayersArgs &a, const LayerG &P, i
   if (reuse)
     lds_barrier();
   else if (!stage_rms<(kL + 3) / 4, kRows, true>(a, a.x0c, l == 0 ? a.x_in : nullptr, tag_of(ep, l - 1),
-                                                 P.norm1, a.H, s.xs, s.misc))
+                                                 P.norm1, a.H, s.xs, s.misc, l == 0 ? e : EmbQ{}))
     return false;
   SH_MARK(s.misc, l, 0);
   f32x4 acc[1];
@@ -629,14 +662,15 @@ __device__ __forceinline__ bool qkv_item(const LayersArgs &a, const LayerG &P, i
 // C: x_mid[b][16 i + c] = x[b][.] + scale * (W_o attn)
 template <int kL, int kRows>
 __device__ __forceinline__ bool o_item(const LayersArgs &a, const LayerG &P, int l, int i, unsigned ep,
-                       const Lds &s) {
+                       const Lds &s, const EmbQ &e) {
   const int lane = threadIdx.x & 63, col = lane & 15, K = a.heads * kD;
   u32x4 w[kL][1];
   load_weights<kL, 1>(w, P.wo, K, i);
   const float sc = P.so[i * 16 + col];
   float rv[4];
   uint64_t rc[4];
-  request_residual<kOutRows<kRows>>(a, a.x0c, l == 0 ? a.x_in : nullptr, i * 16 + col, rv, rc);
+  request_residual<kOutRows<kRows>>(a, a.x0c, l == 0 ? a.x_in : nullptr, i * 16 + col, rv, rc,
+                                    l == 0 ? e : EmbQ{});
   __builtin_amdgcn_sched_barrier(0);
   if (!stage_f16<(kL + 3) / 4, kRows, true>(a, a.attnc, tag_of(ep, l), K, s.xs, s.misc)) return false;
   f32x4 acc[1];
@@ -948,10 +982,13 @@ __device__ __forceinline__ void append_new(const LayersArgs &a, SH_GLOBAL uint16
 // before this one of the same (row, KV head): its normed, rotated q and new
 // k / v are still in LDS, so this item neither polls the cells nor
 // normalises again (the values, and so the arithmetic, are the same).
-template <int kG>
+// kRope: this step's RoPE factors of the lane's two frequencies arrive in
+// rcs / rsn (batch 1 with the embedding inside the kernel) instead of from
+// the embed kernel's table.
+template <int kG, bool kRope = false>
 __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, int l, int item, unsigned ep,
                           uint8_t *smem, Misc *misc, AttnKV &kv, bool runs, bool reuse, bool staged,
-                          int next, bool local) {
+                          int next, bool local, f32x2 rcs = f32x2{}, f32x2 rsn = f32x2{}) {
   static_assert((kG + 2) * kD / 2 <= kT, "one pair of q / k / v cells per thread");
   static_assert(kG <= 4, "MFMA rows 0..3 of lanes 0..15 hold the heads");
   AttnLds<kG> &S = *reinterpret_cast<AttnLds<kG> *>(smem);
@@ -990,12 +1027,12 @@ __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, 
   // This step's norm gains and RoPE factors are requested before the wait.
   static_assert(kG == 2 && (kG + 2) * kD / 2 == kT, "one head per wave");
   const int e0 = 2 * lane, fe = e0 & (kD / 2 - 1);
-  typedef float f32x2 __attribute__((ext_vector_type(2)));
   if (!reuse) {
     const SH_GLOBAL float *gain = wave == 2 ? P.k_norm : P.q_norm;
     const f32x2 g = *reinterpret_cast<const SH_GLOBAL f32x2 *>(gain + e0);
-    const f32x2 cs = *reinterpret_cast<const SH_GLOBAL f32x2 *>(gbl(a.rope) + (size_t)b * kD + fe);
-    const f32x2 sn = *reinterpret_cast<const SH_GLOBAL f32x2 *>(gbl(a.rope) + (size_t)b * kD + kD / 2 + fe);
+    const f32x2 cs = kRope ? rcs : *reinterpret_cast<const SH_GLOBAL f32x2 *>(gbl(a.rope) + (size_t)b * kD + fe);
+    const f32x2 sn = kRope ? rsn
+                           : *reinterpret_cast<const SH_GLOBAL f32x2 *>(gbl(a.rope) + (size_t)b * kD + kD / 2 + fe);
     float v0, v1;
     {
       const size_t qrow = (size_t)b * a.qkv_n;
@@ -1538,7 +1575,34 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
     (&misc->tr[0][0][0])[i] = 0;
 #endif
   lds_barrier();
-  const unsigned ep = *cnst(a.epoch);
+  // The step number: the embed kernel advanced the epoch word before this
+  // launch, or, at batch 1 (kOne), where this launch is the step's only one,
+  // it reads the previous number and workgroup 0 stores the new one after
+  // its last item. kOne also reads the step's position (a.pos points at the
+  // row lengths, which only that last act of workgroup 0 changes, after
+  // every item that reads them), the token from key set keys_in, and
+  // computes this lane's RoPE factors once for all layers.
+  unsigned ep;
+  EmbQ emb;
+  int pos0 = 0;
+  f32x2 rcs{}, rsn{};
+  if constexpr (kOne) {
+    ep = __builtin_amdgcn_readfirstlane(
+             __hip_atomic_load(a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) + 1u;
+    pos0 = __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(a.lens, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    emb.tok = step_token(a.keys_in, 0, a.vocab);
+    emb.head8 = gbl(a.head_w);
+    emb.scale = gbl(a.head_scale)[emb.tok];
+    const int fe = (2 * (threadIdx.x & 63)) & (kD / 2 - 1);  // attn_item's frequency pair
+    float s0, c0, s1, c1;
+    sincosf((float)pos0 * gbl(a.inv_freq)[fe], &s0, &c0);
+    sincosf((float)pos0 * gbl(a.inv_freq)[fe + 1], &s1, &c1);
+    rcs = f32x2{c0, c1};
+    rsn = f32x2{s0, s1};
+  } else {
+    ep = *cnst(a.epoch);
+  }
   const int G = gridDim.x, w = blockIdx.x;
   const int nA = a.qkv_n / 16, nB = B * a.kv_heads * a.splits, nM = B * a.heads * kMergeParts;
   const int nC = H / 16, nD = a.inter / 16, nE = H / 16;
@@ -1650,7 +1714,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
     auto qkv_one = [&](int i) {
       if (i != bQ) load_weights<kLA, 1>(wa, P.wqkv, H, i);
       if (i == bQ) SH_TRACE(misc, l, 0);
-      if (!qkv_item<kLA, kRows>(a, P, l, i, ep, lds, wa, !kPre && i != bQ, xl)) return false;
+      if (!qkv_item<kLA, kRows>(a, P, l, i, ep, lds, wa, !kPre && i != bQ, xl, emb)) return false;
       if (i == bQ) { SH_TRACE(misc, l, 1); SH_TRACE_WAIT(l, 0, misc); }
       return true;
     };
@@ -1683,7 +1747,8 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
         const bool reuse = !kOne && k != bA && i % a.splits != 0;
         const int nx = kStg && k + 1 < eA ? (kOne || kAct ? item_at(nxt) : k + 1) : -1;
         const bool staged = kStg && (k != bA || !kPre);
-        if (!attn_item<kG>(a, P, l, i, ep, smem, misc, kv, kStg, reuse, staged, nx, xl)) return false;
+        if (!attn_item<kG, kOne>(a, P, l, i, ep, smem, misc, kv, kStg, reuse, staged, nx, xl, rcs, rsn))
+          return false;
         if (k == bA) { SH_TRACE(misc, l, 3); SH_TRACE_WAIT(l, 1, misc); }
         if (k - bA < 8) SH_TRACE(misc, l, 16 + (k - bA));  // the run's first eight items' ends
         return true;
@@ -1725,7 +1790,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
     if (w < nE) load_weights<kLE, 1>(wd, P.wdown, a.inter, w);
     if (!for_items<kOne>(w, nC, G, [&](int i) {
           if (i == w) SH_TRACE(misc, l, 4);
-          if (!o_item<kLC, kRows>(a, P, l, i, ep, lds)) return false;
+          if (!o_item<kLC, kRows>(a, P, l, i, ep, lds, emb)) return false;
           if (i == w) { SH_TRACE(misc, l, 5); SH_TRACE_WAIT(l, 2, misc); }
           return true;
         }))
@@ -1768,6 +1833,23 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
   }
   if (a.head_on && !head_phase<kLA, kRows>(a, ep, lds)) return;
   SH_MARK(misc, a.n_layers, 1);
+  // kOne: the step's bookkeeping, by workgroup 0 after its last item. Every
+  // workgroup has read the epoch word, the lengths and key set keys_in by
+  // then: it read them first, and its items' cells carry the step's tag,
+  // position or token, while workgroup 0's last item (its head tiles or its
+  // last down item) waited, through the layers' chains of exchanges, on
+  // cells that depend on every item of the step.
+  if constexpr (kOne) {
+    if (w == 0) {
+      if (threadIdx.x < kKeySlots) gbl(a.keys_in)[(size_t)threadIdx.x * kKeyStride] = 0ull;
+      if (threadIdx.x == 0) {
+        if (pos0 < a.hist_len) gbl(a.hist)[pos0] = emb.tok;
+        gbl(a.pos_out)[0] = pos0;
+        gbl(a.lens)[0] = pos0 + 1;
+        gbl(a.epoch)[0] = ep;
+      }
+    }
+  }
 #ifdef SH_DECODE_TRACE
   lds_barrier();
   if (w < kTraceWgs)
@@ -1828,6 +1910,11 @@ size_t attn_lds(int g) {
 }
 
 }  // namespace
+
+bool decode_layers_folds_embed(const LayersArgs &a, int grid) {
+  // kernel_for's choice of the batch-1 instantiation (kOne)
+  return a.B == 1 && one_item_each(a, grid);
+}
 
 bool decode_layers_xcd_ok(const LayersArgs &a, int grid) {
   if (a.B != 1 || grid % 8 != 0 || a.kv_heads != 8 || a.heads % a.kv_heads != 0) return false;

@@ -122,9 +122,21 @@ struct LayersArgs {
   int max_pos = 0, splits = 1, chunk = 16;
   int vt_stride = 0;                   // positions per V^T cache row: max_pos rounded up to 16
   float eps = 1e-6f, scale = 1.0f;     // RMSNorm epsilon, attention 1 / sqrt(d)
-  const int *pos = nullptr;            // [B] this step's position (embed kernel)
+  const int *pos = nullptr;            // [B] this step's position (embed kernel; at
+                                       // batch 1, the row lengths, which the kernel advances)
   const float *rope = nullptr;         // [B][128]: cos | sin (embed kernel)
-  const unsigned *epoch = nullptr;     // this step's number (embed kernel)
+  unsigned *epoch = nullptr;           // this step's number (embed kernel; at batch 1,
+                                       // the previous one, which the kernel advances)
+  // batch 1 (one item per workgroup and phase; decode_layers_folds_embed):
+  // the kernel is the step's only launch. It reads the token from key set
+  // keys_in, embeds it (row of the tied FP8 head times its scale), computes
+  // RoPE's factors from inv_freq, and its workgroup 0 stores the step
+  // number, the row's length, position (pos_out) and history entry after
+  // its last item and clears keys_in's row 0
+  unsigned long long *keys_in = nullptr;
+  int *lens = nullptr, *pos_out = nullptr, *hist = nullptr;
+  int hist_len = 0, vocab = 0;
+  const float *inv_freq = nullptr;
   float *x_in = nullptr;               // [kMaxBatch][H] plain fp32: first layer's input
                                        // (embed kernel), last layer's output
   uint64_t *x0c = nullptr, *x1c = nullptr, *qkvc = nullptr, *partc = nullptr;
@@ -154,6 +166,9 @@ struct LayersArgs {
 // of the qkv, o, gate/up and down items) and the query heads per KV head.
 // Returns false for any other shape (the runner then keeps per-op kernels).
 bool decode_layers_supported(int layers, int H, int heads, int kv_heads, int head_dim, int inter);
+// Whether the launch of a at `grid` workgroups runs the batch-1 kernel, which
+// embeds the step's token itself (LayersArgs::keys_in ..).
+bool decode_layers_folds_embed(const LayersArgs &a, int grid);
 // Whether a (batch 1, `grid` workgroups) fits the XCD-local placement: eight
 // KV heads, one per XCD, each with grid / 8 QKV tiles (its query heads' q,
 // its k and v) and grid / 8 attention splits.

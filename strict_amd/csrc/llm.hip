@@ -211,12 +211,17 @@ int enqueue_step(sh_llm *m, bool logits) {
   e.half = d / 2;
   float *x_final = m->x;  // the layers kernel reads and writes m->x too
   if (m->layers_kernel) e.epoch = m->epoch;
-  SH_HIP_TRY(launch_embed(s, e, B));
+  // at batch 1 the decode-layers kernel embeds the token itself (one launch)
+  const bool fold = m->layers_kernel && decode_layers_folds_embed(m->la, m->layers_grid);
+  if (!fold) SH_HIP_TRY(launch_embed(s, e, B));
 
   if (m->layers_kernel) {
-    m->la.head_on = logits && m->head_in_layers ? 1 : 0;
-    m->la.keys = keys_out;
-    SH_HIP_TRY(launch_decode_layers(s, m->la, m->layers_grid, m->layers_lds, m->coop_layers));
+    LayersArgs &la = m->la;
+    la.head_on = logits && m->head_in_layers ? 1 : 0;
+    la.keys = keys_out;
+    la.keys_in = keys_in;
+    la.pos = fold ? m->lens : m->pos;  // at batch 1 the kernel reads (and advances) the lengths
+    SH_HIP_TRY(launch_decode_layers(s, la, m->layers_grid, m->layers_lds, m->coop_layers));
     m->epoch_host++;
   }
   for (Layer &L : m->layers) {
@@ -362,6 +367,13 @@ int setup_layers_kernel(sh_llm *m) {
   a.scale = 1.0f / std::sqrt((float)c.head_dim);
   a.pos = m->pos;
   a.rope = m->rope;
+  // what the batch-1 kernel reads and writes in place of the embed kernel
+  a.lens = m->lens;
+  a.pos_out = m->pos;
+  a.hist = m->hist;
+  a.hist_len = c.max_positions;
+  a.vocab = c.vocab;
+  a.inv_freq = m->inv_freq;
   a.spin_ticks = (unsigned long long)clock_khz * 50;  // 50 ms per wait
   // the kernel's merge limit must leave splits of at most kMaxSplitChunk positions
   const int max_sp = decode_layers_max_splits(c.hidden, c.heads, c.kv_heads, c.intermediate);
