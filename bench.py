@@ -842,9 +842,9 @@ def main() -> int:
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                     "traffic": read_traffic("qwen3_decode_step"),
-                    "kernel": "decode step: embed, then decode_layers_kernel (all 28 layers, "
-                              "final RMSNorm and LM head with greedy argmax in one persistent "
-                              "launch)"}
+                    "kernel": "decode step: one persistent decode_layers_kernel launch (the "
+                              "token's embedding, all 28 layers, final RMSNorm and LM head "
+                              "with greedy argmax)"}
         log(f"headline: {value:.1f} tokens/s, {achieved:.1f} GB/s algorithmic")
         if not args.no_extra:
             kernels.append(qwen3_batch_entry(ctx, 4, 32))
