@@ -54,6 +54,7 @@
 #include <hip/hip_runtime.h>
 
 #include "common.h"
+#include "exchange.h"
 #include "llm.h"
 #include "llm_device.h"
 
@@ -181,6 +182,36 @@ __device__ __forceinline__ bool spin_cells(const LayersArgs &a, const uint64_t *
 #if defined(SH_POLL_SLEEP) && SH_POLL_SLEEP > 0
     __builtin_amdgcn_s_sleep(SH_POLL_SLEEP);
 #endif
+  }
+}
+
+// spin_cells over cells taken two at a time (one 16-byte load each, with
+// the agent-scope cache policy of cld): at(k) for even k must be even, and
+// cell k + 1 is at(k) + 1 (at is called for even k only). Polls of adjacent
+// cells this way send half the line requests to memory.
+template <int kN, class At>
+__device__ __forceinline__ bool spin_pairs(const LayersArgs &a, const uint64_t *base, At at,
+                                           uint64_t mask, unsigned tag, uint64_t (&c)[kN]) {
+  static_assert(kN % 2 == 0, "pairs of cells");
+  const __amdgpu_buffer_rsrc_t rs = xchg::cell_rsrc(base);
+  unsigned long long t0 = 0;
+  for (int it = 0;; it++) {
+    // compiler barriers: a new load each round, every load issued before
+    // the checks (ordinary loads are otherwise moved into the branches of
+    // the checks, one round trip after another)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+#pragma unroll
+    for (int k = 0; k < kN; k += 2) xchg::cld2(rs, at(k), c[k], c[k + 1]);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < kN; k++) ok &= ((mask >> k & 1) == 0) | ((uint32_t)(c[k] >> 32) == tag);
+    if (ok) return true;
+    if (it == 0) {
+      t0 = wall_clock64();
+    } else if ((it & 7) == 0 && (ld_err(a.err) != 0 || wall_clock64() - t0 > a.spin_ticks)) {
+      return false;
+    }
   }
 }
 
@@ -461,7 +492,7 @@ __device__ __forceinline__ bool stage_rms(const LayersArgs &a, const uint64_t *x
 #pragma unroll
         for (int j = 0; j < kChunks; j++)
           if (b0 + r < B && stage_chunk_ok(K, j)) mask |= 15ull << ((r * kChunks + j) * 4);
-      ok = spin_cells(a, xc,
+      ok = spin_pairs(a, xc,
                       [&](int k) {
                         const int r = k / (kChunks * 4), j = (k / 4) % kChunks, e = k % 4;
                         return (size_t)min(b0 + r, B - 1) * K + min(stage_chunk(K, j), c4 - 1) * 4 + e;
@@ -537,7 +568,7 @@ __device__ __forceinline__ bool stage_f16(const LayersArgs &a, const uint64_t *c
 #pragma unroll
       for (int j = 0; j < kChunks; j++)
         if (b0 + r < B && stage_chunk_ok(K, j)) mask |= 3ull << ((r * kChunks + j) * 2);
-    const bool ok = spin_cells(a, cells,
+    const bool ok = spin_pairs(a, cells,
                                [&](int k) {
                                  const int r = k / (kChunks * 2), j = (k / 2) % kChunks, e = k % 2;
                                  return (size_t)min(b0 + r, B - 1) * row_cells +

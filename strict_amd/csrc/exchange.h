@@ -48,6 +48,28 @@ __device__ __forceinline__ uint64_t cld(const uint64_t *base, size_t cell) {
   return __hip_atomic_load(base + cell, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+typedef unsigned xu32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer resource over a cell array for cld2 (byte offsets below 2 GiB).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t cell_rsrc(const uint64_t *base) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7fffffff, 0x00020000);
+}
+
+// Cells `cell` and `cell + 1` (cell even) in one 16-byte load with cld's
+// agent-scope cache policy (sc1). Each cell is written by one 8-byte (or
+// two-cell 16-byte) store, so each half holds a cell as a store left it,
+// and each is checked for its tag on its own. A wave's poll of adjacent
+// cells this way sends half the line requests of 8-byte loads: measured
+// over 1,024 cells, 64 producer x 192 consumer workgroups, 1.45-1.59 us
+// per exchange against 1.76 us with four adjacent 8-byte cells per lane.
+// Loads of this kind are ordinary loads to the compiler, so the spin loops
+// that issue them keep a compiler barrier in each round.
+__device__ __forceinline__ void cld2(__amdgpu_buffer_rsrc_t rs, size_t cell, uint64_t &c0, uint64_t &c1) {
+  const xu32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(cell * 8), 0, 16 /* sc1 */);
+  c0 = (uint64_t)v.x | ((uint64_t)v.y << 32);
+  c1 = (uint64_t)v.z | ((uint64_t)v.w << 32);
+}
+
 // `local`: a workgroup-scope store instead, which lands in the XCD's L2 and
 // stays there; agent-scope loads on the same XCD see it (a hop ~0.22 us
 // against ~0.4-0.53 us, measured in a ping-pong between workgroups), those
@@ -91,6 +113,34 @@ __device__ __forceinline__ bool spin_cells(const A &a, const uint64_t *base, At 
     bool ok = true;
 #pragma unroll
     for (int k = 0; k < kN; k++) ok = ok && ((mask >> k & 1) == 0 || (uint32_t)(c[k] >> 32) == tag);
+    if (ok) return true;
+    if (it == 0) {
+      t0 = wall_clock64();
+    } else if ((it & 7) == 0 && (ld_err(a) != 0 || wall_clock64() - t0 > a.spin_ticks)) {
+      return false;
+    }
+  }
+}
+
+// spin_cells over cells taken two at a time (cld2): at(k) for even k must be
+// even, and cell k + 1 is at(k) + 1 (at is called for even k only).
+template <int kN, class A, class At>
+__device__ __forceinline__ bool spin_pairs(const A &a, const uint64_t *base, At at, uint64_t mask,
+                                           unsigned tag, uint64_t (&c)[kN]) {
+  static_assert(kN % 2 == 0, "pairs of cells");
+  const __amdgpu_buffer_rsrc_t rs = cell_rsrc(base);
+  unsigned long long t0 = 0;
+  for (int it = 0;; it++) {
+    // compiler barriers: a new load each round, every load issued before
+    // the checks (ordinary loads are otherwise moved into the branches of
+    // the checks, one round trip after another)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+#pragma unroll
+    for (int k = 0; k < kN; k += 2) cld2(rs, at(k), c[k], c[k + 1]);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < kN; k++) ok &= ((mask >> k & 1) == 0) | ((uint32_t)(c[k] >> 32) == tag);
     if (ok) return true;
     if (it == 0) {
       t0 = wall_clock64();

@@ -222,7 +222,7 @@ __device__ __forceinline__ bool stage_ln(const Gpt2Args &a, const uint64_t *xc, 
 #pragma unroll
     for (int j = 0; j < kC; j++)
       if (stage_chunk_ok(K, j)) mask |= 15ull << (j * 4);
-    ok = spin_cells(a, xc, [&](int k) { return (size_t)min(stage_chunk(K, k >> 2), c4 - 1) * 4 + (k & 3); },
+    ok = spin_pairs(a, xc, [&](int k) { return (size_t)min(stage_chunk(K, k >> 2), c4 - 1) * 4 + (k & 3); },
                     mask, tag, cv);
 #pragma unroll
     for (int j = 0; j < kC; j++)
@@ -268,7 +268,7 @@ __device__ __forceinline__ bool stage_f16(const Gpt2Args &a, const uint64_t *cel
 #pragma unroll
   for (int j = 0; j < kC; j++)
     if (stage_chunk_ok(K, j)) mask |= 3ull << (j * 2);
-  const bool ok = spin_cells(
+  const bool ok = spin_pairs(
       a, cells, [&](int k) { return (size_t)min(stage_chunk(K, k >> 1), c4 - 1) * 2 + (k & 1); }, mask, tag, cv);
   if (!waits_ok(a, ok, &S.votes)) return false;
 #pragma unroll
