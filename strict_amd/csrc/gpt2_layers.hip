@@ -173,6 +173,18 @@ __device__ __forceinline__ bool stage_chunk_ok(int K, int j) {
   return (threadIdx.x & 63) + 64 * j < (K >> 4);
 }
 
+// The 2-value pairs of a K-value row stage_ln stages: wave w holds those of
+// its K quarter, [w K / 8, (w + 1) K / 8), lane l the pairs w K / 8 + l +
+// 64 i (the same quarter of xs as stage_chunk). A pair is two adjacent
+// cells, so a wave's poll of its pairs i is one lane-contiguous 16-byte load,
+// which reaches memory as the fewest line requests.
+__device__ __forceinline__ int stage_pair(int K, int i) {
+  return (threadIdx.x >> 6) * (K >> 3) + (threadIdx.x & 63) + 64 * i;
+}
+__device__ __forceinline__ bool stage_pair_ok(int K, int i) {
+  return (threadIdx.x & 63) + 64 * i < (K >> 3);
+}
+
 // The first layer's input row straight from the embedding tables: row `tok`
 // of the tied head (fp16 tiled) plus the position row `wpe_row`, summed in
 // fp32 (the per-op path's embed kernel does the same sum).
@@ -192,64 +204,75 @@ __device__ __forceinline__ f32x4 emb4(const Emb &e, int k, int K) {
                f16_bits_to_f32((uint16_t)(t.y >> 16)) + f16_bits_to_f32((uint16_t)(p.y >> 16))};
 }
 
+// Values k, k + 1 of the embedded row (k even).
+__device__ __forceinline__ f32x2 emb2(const Emb &e, int k, int K) {
+  const uint32_t t = *reinterpret_cast<const SH_XGLOBAL uint32_t *>(e.wte + f16_tiled_offset(e.tok, k, K));
+  const uint32_t p = *reinterpret_cast<const SH_XGLOBAL uint32_t *>(e.wpe_row + k);
+  return f32x2{f16_bits_to_f32((uint16_t)t) + f16_bits_to_f32((uint16_t)p),
+               f16_bits_to_f32((uint16_t)(t >> 16)) + f16_bits_to_f32((uint16_t)(p >> 16))};
+}
+
 __device__ __forceinline__ float emb1(const Emb &e, int k, int K) {
   return f16_bits_to_f32(e.wte[f16_tiled_offset(e.tok, k, K)]) + f16_bits_to_f32(e.wpe_row[k]);
 }
 
 // LayerNorm of the fp32 row x (K values: cells tagged `tag`, or the embedded
-// row e when e.tok >= 0) with gains g and biases b -> xs (fp16). A thread holds the
-// 4-value chunks stage_chunk(K, j), j < kC. kLocal: the caller's waves read
-// only their own K quarter of xs, so no barrier follows the stores.
+// row e when e.tok >= 0) with gains g and biases b -> xs (fp16). A thread
+// holds the 2-value pairs stage_pair(K, i), i < 2 kC (kC >= K / 1024).
+// kLocal: the caller's waves read only their own K quarter of xs, so no
+// barrier follows the stores.
 template <int kC, bool kLocal>
 __device__ __forceinline__ bool stage_ln(const Gpt2Args &a, const uint64_t *xc, const Emb &e,
                                          unsigned tag, const SH_XGLOBAL float *g,
                                          const SH_XGLOBAL float *bta, int K, Lds &S) {
-  const int c4 = K >> 2;
-  f32x4 gv[kC], bv[kC], v[kC];
+  constexpr int kP = 2 * kC;
+  const int c2 = K >> 1;
+  f32x2 gv[kP], bv[kP], v[kP];
 #pragma unroll
-  for (int j = 0; j < kC; j++) {
-    const int c = min(stage_chunk(K, j), c4 - 1);
-    gv[j] = *reinterpret_cast<const SH_XGLOBAL f32x4 *>(g + c * 4);
-    bv[j] = *reinterpret_cast<const SH_XGLOBAL f32x4 *>(bta + c * 4);
+  for (int i = 0; i < kP; i++) {
+    const int c = min(stage_pair(K, i), c2 - 1);
+    gv[i] = *reinterpret_cast<const SH_XGLOBAL f32x2 *>(g + c * 2);
+    bv[i] = *reinterpret_cast<const SH_XGLOBAL f32x2 *>(bta + c * 2);
   }
   bool ok = true;
   if (e.tok >= 0) {
 #pragma unroll
-    for (int j = 0; j < kC; j++) v[j] = emb4(e, min(stage_chunk(K, j), c4 - 1) * 4, K);
+    for (int i = 0; i < kP; i++) v[i] = emb2(e, min(stage_pair(K, i), c2 - 1) * 2, K);
   } else {
-    uint64_t cv[kC * 4];
+    uint64_t cv[kP * 2];
     uint64_t mask = 0;
 #pragma unroll
-    for (int j = 0; j < kC; j++)
-      if (stage_chunk_ok(K, j)) mask |= 15ull << (j * 4);
-    ok = spin_pairs(a, xc, [&](int k) { return (size_t)min(stage_chunk(K, k >> 2), c4 - 1) * 4 + (k & 3); },
+    for (int i = 0; i < kP; i++)
+      if (stage_pair_ok(K, i)) mask |= 3ull << (i * 2);
+    ok = spin_pairs(a, xc, [&](int k) { return (size_t)min(stage_pair(K, k >> 1), c2 - 1) * 2 + (k & 1); },
                     mask, tag, cv);
 #pragma unroll
-    for (int j = 0; j < kC; j++)
-      v[j] = f32x4{cell_f32(cv[4 * j]), cell_f32(cv[4 * j + 1]), cell_f32(cv[4 * j + 2]),
-                   cell_f32(cv[4 * j + 3])};
+    for (int i = 0; i < kP; i++) v[i] = f32x2{cell_f32(cv[2 * i]), cell_f32(cv[2 * i + 1])};
   }
   if (!waits_ok(a, ok, &S.votes)) return false;
   float sm = 0.0f;
 #pragma unroll
-  for (int j = 0; j < kC; j++)
-    if (stage_chunk_ok(K, j)) sm += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
+  for (int i = 0; i < kP; i += 2) {
+    const float s0 = stage_pair_ok(K, i) ? v[i][0] + v[i][1] : 0.0f;
+    const float s1 = stage_pair_ok(K, i + 1) ? v[i + 1][0] + v[i + 1][1] : 0.0f;
+    sm += s0 + s1;
+  }
   const float mean = block_sum(sm, 0, S) / (float)K;
   float ss = 0.0f;
 #pragma unroll
-  for (int j = 0; j < kC; j++)
-    if (stage_chunk_ok(K, j)) {
-      const f32x4 d = v[j] - mean;
-      ss += (d[0] * d[0] + d[1] * d[1]) + (d[2] * d[2] + d[3] * d[3]);
-    }
+  for (int i = 0; i < kP; i += 2) {
+    const f32x2 d0 = v[i] - mean, d1 = v[i + 1] - mean;
+    const float s0 = stage_pair_ok(K, i) ? d0[0] * d0[0] + d0[1] * d0[1] : 0.0f;
+    const float s1 = stage_pair_ok(K, i + 1) ? d1[0] * d1[0] + d1[1] * d1[1] : 0.0f;
+    ss += s0 + s1;
+  }
   const float inv = 1.0f / sqrtf(block_sum(ss, 1, S) / (float)K + a.eps);
 #pragma unroll
-  for (int j = 0; j < kC; j++) {
-    const int c = stage_chunk(K, j);
-    if (stage_chunk_ok(K, j)) {
-      const f32x4 y = (v[j] - mean) * inv * gv[j] + bv[j];
-      *reinterpret_cast<f16x4 *>(S.xs + c * 4) =
-          f16x4{(_Float16)y[0], (_Float16)y[1], (_Float16)y[2], (_Float16)y[3]};
+  for (int i = 0; i < kP; i++) {
+    const int c = stage_pair(K, i);
+    if (stage_pair_ok(K, i)) {
+      const f32x2 y = (v[i] - mean) * inv * gv[i] + bv[i];
+      *reinterpret_cast<f16x2 *>(S.xs + c * 2) = f16x2{(_Float16)y[0], (_Float16)y[1]};
     }
   }
   if (!kLocal) lds_barrier();
