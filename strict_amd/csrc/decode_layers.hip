@@ -1095,7 +1095,14 @@ __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, 
       else if (wave == 2) cell = qrow + (size_t)a.heads * kD + kvh * kD + e0;
       else cell = qrow + (size_t)(a.heads + kvn) * kD + kvh * kD + e0;
       uint64_t cv[2];
-      const bool ok = spin_cells(a, a.qkvc, [&](int k) { return cell + k; }, 3ull, tag, cv);
+      // one 16-byte load per lane at batch 1; the batched variants measured
+      // ~1 % slower that way (b=4, with the merge polls below), so they keep
+      // 8-byte loads here and in merge_run
+      bool ok;
+      if constexpr (kRope)
+        ok = spin_pairs(a, a.qkvc, [&](int k) { return cell + k; }, 3ull, tag, cv);
+      else
+        ok = spin_cells(a, a.qkvc, [&](int k) { return cell + k; }, 3ull, tag, cv);
       if (!waits_ok(a, ok, misc)) return false;
       SH_MARK(misc, l, 8);
       v0 = cell_f32(cv[0]);
@@ -1330,7 +1337,7 @@ __device__ __forceinline__ bool merge_item(const LayersArgs &a, int l, int item,
   for (int k = 0; k < kPer; k++)
     if (sg + kGroups * k < active) mask |= 15ull << (4 * k);
   uint64_t cv[4 * kPer];
-  const bool ok = spin_cells(a, a.partc,
+  const bool ok = spin_pairs(a, a.partc,
                              [&](int k) {
                                const int j = min(sg + kGroups * (k / 4), active - 1);
                                return base + (size_t)j * kPStride +
