@@ -277,6 +277,37 @@ __device__ __forceinline__ bool block_any(bool p, Misc *misc) {
   return (vt[0] | vt[1] | vt[2] | vt[3]) != 0;
 }
 
+// block_any in two halves around a barrier that the caller places (a
+// wait's outcome can then share the barrier of values exchanged anyway):
+// vote_cast before the barrier, vote_seen with its result after it.
+__device__ __forceinline__ int vote_cast(bool p, Misc *misc) {
+  const int wave = threadIdx.x >> 6;
+  const int par = misc->par[wave];
+  const bool v = __any(p ? 1 : 0) != 0;
+  if ((threadIdx.x & 63) == 0) {
+    misc->vote[par][wave] = v ? 1 : 0;
+    misc->par[wave] = par ^ 1;
+  }
+  return par;
+}
+__device__ __forceinline__ bool vote_seen(int par, const Misc *misc) {
+  const int *vt = misc->vote[par];
+  return (vt[0] | vt[1] | vt[2] | vt[3]) != 0;
+}
+
+// After a vote on failed waits (block-uniform `failed`): marks the error
+// and returns false if any wait failed.
+__device__ __forceinline__ bool waits_done(const LayersArgs &a, bool failed, Misc *misc) {
+  if (failed) {
+    if (threadIdx.x == 0) atomicOr(a.err, 1u);
+    return false;
+  }
+#ifdef SH_DECODE_TRACE
+  if (threadIdx.x == 0) misc->t_wait = wall_clock64();
+#endif
+  return true;
+}
+
 // Every thread's wait succeeded (block-uniform); otherwise marks the error.
 __device__ __forceinline__ bool waits_ok(const LayersArgs &a, bool ok, Misc *misc) {
   if (block_any(!ok, misc)) {
@@ -430,15 +461,6 @@ struct EmbQ {
   float scale = 0.0f;
 };
 
-// Values k .. k + 3 (k a multiple of 4: four contiguous bytes of the tile).
-__device__ __forceinline__ f32x4 embq4(const EmbQ &e, int k, int K) {
-  const uint32_t q = *reinterpret_cast<const SH_GLOBAL uint32_t *>(e.head8 + fp8_tiled_offset(e.tok, k, K));
-  const f16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(q, 1.0f, false);
-  const f16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(q, 1.0f, true);
-  return f32x4{(float)lo[0] * e.scale, (float)lo[1] * e.scale, (float)hi[0] * e.scale,
-               (float)hi[1] * e.scale};
-}
-
 __device__ __forceinline__ float embq1(const EmbQ &e, int k, int K) {
   const uint8_t q = e.head8[fp8_tiled_offset(e.tok, k, K)];
   return (float)__builtin_amdgcn_cvt_scalef32_pk_f16_fp8((uint32_t)q, 1.0f, false)[0] * e.scale;
@@ -528,7 +550,15 @@ __device__ __forceinline__ bool stage_rms(const LayersArgs &a, const uint64_t *x
           v[r][i] = f32x2{cell_f32(cv[k]), cell_f32(cv[k + 1])};
         }
     }
-    if (!waits_ok(a, ok, misc)) return false;
+    // at batch 1 the waits' vote shares the barrier of the sums of squares
+    // (the batched variants vote first: their kernels measured ~1 % slower
+    // with the shared barrier)
+    int vpar = 0;
+    if constexpr (kRowsMax == 1) {
+      vpar = vote_cast(!ok, misc);
+    } else {
+      if (!waits_ok(a, ok, misc)) return false;
+    }
 #pragma unroll
     for (int r = 0; r < kRows; r++) {
       float ss = 0.0f;
@@ -546,6 +576,9 @@ __device__ __forceinline__ bool stage_rms(const LayersArgs &a, const uint64_t *x
       }
     }
     lds_barrier();
+    if constexpr (kRowsMax == 1) {
+      if (!waits_done(a, vote_seen(vpar, misc), misc)) return false;
+    }
 #pragma unroll
     for (int r = 0; r < kRows; r++) {
       const int b = b0 + r;

@@ -183,8 +183,10 @@ struct Votes {
   int par[4];
 };
 
-// True in every thread when p holds in any thread (a barrier; 4 waves).
-__device__ __forceinline__ bool block_any(bool p, Votes *v) {
+// block_any in two halves around a barrier that the caller places (a
+// wait's outcome can then share the barrier of values exchanged anyway):
+// vote_cast before the barrier, vote_seen with its result after it.
+__device__ __forceinline__ int vote_cast(bool p, Votes *v) {
   const int wave = threadIdx.x >> 6;
   const int par = v->par[wave];
   const bool any = __any(p ? 1 : 0) != 0;
@@ -192,20 +194,36 @@ __device__ __forceinline__ bool block_any(bool p, Votes *v) {
     v->vote[par][wave] = any ? 1 : 0;
     v->par[wave] = par ^ 1;
   }
-  lds_barrier();
+  return par;
+}
+__device__ __forceinline__ bool vote_seen(int par, const Votes *v) {
   const int *vt = v->vote[par];
   return (vt[0] | vt[1] | vt[2] | vt[3]) != 0;
+}
+
+// True in every thread when p holds in any thread (a barrier; 4 waves).
+__device__ __forceinline__ bool block_any(bool p, Votes *v) {
+  const int par = vote_cast(p, v);
+  lds_barrier();
+  return vote_seen(par, v);
+}
+
+// After a vote on failed waits (workgroup-uniform `failed`): marks the
+// sticky error and returns false if any wait failed.
+template <class A>
+__device__ __forceinline__ bool waits_done(const A &a, bool failed) {
+  if (failed) {
+    if (threadIdx.x == 0) atomicOr(a.err, 1u);
+    return false;
+  }
+  return true;
 }
 
 // Every thread's wait succeeded (workgroup-uniform); otherwise marks the
 // sticky error.
 template <class A>
 __device__ __forceinline__ bool waits_ok(const A &a, bool ok, Votes *v) {
-  if (block_any(!ok, v)) {
-    if (threadIdx.x == 0) atomicOr(a.err, 1u);
-    return false;
-  }
-  return true;
+  return waits_done(a, block_any(!ok, v));
 }
 
 }  // namespace xchg

@@ -193,17 +193,6 @@ struct Emb {
   const SH_XGLOBAL uint16_t *wte = nullptr, *wpe_row = nullptr;
 };
 
-// Values k .. k + 3 of the embedded row (k a multiple of 4: contiguous in
-// both tables).
-__device__ __forceinline__ f32x4 emb4(const Emb &e, int k, int K) {
-  const u32x2 t = *reinterpret_cast<const SH_XGLOBAL u32x2 *>(e.wte + f16_tiled_offset(e.tok, k, K));
-  const u32x2 p = *reinterpret_cast<const SH_XGLOBAL u32x2 *>(e.wpe_row + k);
-  return f32x4{f16_bits_to_f32((uint16_t)t.x) + f16_bits_to_f32((uint16_t)p.x),
-               f16_bits_to_f32((uint16_t)(t.x >> 16)) + f16_bits_to_f32((uint16_t)(p.x >> 16)),
-               f16_bits_to_f32((uint16_t)t.y) + f16_bits_to_f32((uint16_t)p.y),
-               f16_bits_to_f32((uint16_t)(t.y >> 16)) + f16_bits_to_f32((uint16_t)(p.y >> 16))};
-}
-
 // Values k, k + 1 of the embedded row (k even).
 __device__ __forceinline__ f32x2 emb2(const Emb &e, int k, int K) {
   const uint32_t t = *reinterpret_cast<const SH_XGLOBAL uint32_t *>(e.wte + f16_tiled_offset(e.tok, k, K));
@@ -249,7 +238,8 @@ __device__ __forceinline__ bool stage_ln(const Gpt2Args &a, const uint64_t *xc, 
 #pragma unroll
     for (int i = 0; i < kP; i++) v[i] = f32x2{cell_f32(cv[2 * i]), cell_f32(cv[2 * i + 1])};
   }
-  if (!waits_ok(a, ok, &S.votes)) return false;
+  // the waits' vote shares the barrier of the first sum
+  const int vpar = vote_cast(!ok, &S.votes);
   float sm = 0.0f;
 #pragma unroll
   for (int i = 0; i < kP; i += 2) {
@@ -258,6 +248,7 @@ __device__ __forceinline__ bool stage_ln(const Gpt2Args &a, const uint64_t *xc, 
     sm += s0 + s1;
   }
   const float mean = block_sum(sm, 0, S) / (float)K;
+  if (!waits_done(a, vote_seen(vpar, &S.votes))) return false;
   float ss = 0.0f;
 #pragma unroll
   for (int i = 0; i < kP; i += 2) {
