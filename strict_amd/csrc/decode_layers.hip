@@ -308,6 +308,15 @@ __device__ __forceinline__ bool waits_done(const LayersArgs &a, bool failed, Mis
   return true;
 }
 
+// Marks the error when a wait of this wave failed (no vote: the caller goes
+// on either way).
+__device__ __forceinline__ void wave_waits_ok(const LayersArgs &a, bool ok, Misc *misc) {
+  if (__any(ok ? 0 : 1) && (threadIdx.x & 63) == 0) atomicOr(a.err, 1u);
+#ifdef SH_DECODE_TRACE
+  if (threadIdx.x == 0) misc->t_wait = wall_clock64();
+#endif
+}
+
 // Every thread's wait succeeded (block-uniform); otherwise marks the error.
 __device__ __forceinline__ bool waits_ok(const LayersArgs &a, bool ok, Misc *misc) {
   if (block_any(!ok, misc)) {
@@ -631,7 +640,16 @@ __device__ __forceinline__ bool stage_f16(const LayersArgs &a, const uint64_t *c
                                         min(stage_chunk(K, j), c4 - 1) * 2 + e;
                                },
                                mask, tag, cv);
-    if (!waits_ok(a, ok, misc)) return false;
+    if constexpr (kRowsMax == 1 && kLocal) {
+      // batch 1: no vote, so no barrier. Each wave stages and then reads
+      // only its own quarter of xs, and the item's next barrier (the
+      // cross-wave sum) follows its MFMAs; a wave whose wait failed marks
+      // the error and goes on with what it loaded, so every wave reaches
+      // that barrier, and the host reports the step as failed.
+      wave_waits_ok(a, ok, misc);
+    } else if (!waits_ok(a, ok, misc)) {
+      return false;
+    }
 #pragma unroll
     for (int r = 0; r < kRows; r++)
 #pragma unroll

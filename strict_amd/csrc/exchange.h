@@ -219,6 +219,16 @@ __device__ __forceinline__ bool waits_done(const A &a, bool failed) {
   return true;
 }
 
+// For a wave that stages and then reads only its own part of the LDS before
+// the workgroup's next barrier: marks the sticky error when a wait of this
+// wave failed, without a vote (and its barrier). The caller goes on with
+// what it loaded either way, so every wave still reaches the next barrier,
+// and the host reports the step as failed.
+template <class A>
+__device__ __forceinline__ void wave_waits_ok(const A &a, bool ok) {
+  if (__any(ok ? 0 : 1) && (threadIdx.x & 63) == 0) atomicOr(a.err, 1u);
+}
+
 // Every thread's wait succeeded (workgroup-uniform); otherwise marks the
 // sticky error.
 template <class A>

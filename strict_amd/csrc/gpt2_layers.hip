@@ -284,7 +284,7 @@ __device__ __forceinline__ bool stage_f16(const Gpt2Args &a, const uint64_t *cel
     if (stage_chunk_ok(K, j)) mask |= 3ull << (j * 2);
   const bool ok = spin_pairs(
       a, cells, [&](int k) { return (size_t)min(stage_chunk(K, k >> 1), c4 - 1) * 2 + (k & 1); }, mask, tag, cv);
-  if (!waits_ok(a, ok, &S.votes)) return false;
+  wave_waits_ok(a, ok);  // no vote (no barrier): see wave_waits_ok
 #pragma unroll
   for (int j = 0; j < kC; j++) {
     const int c = stage_chunk(K, j);
@@ -515,7 +515,7 @@ __device__ __forceinline__ bool stage_attn_n(const Gpt2Args &a, unsigned tag, in
                                return pp + (f == 0 ? d : kHd + f - 1);
                              },
                              mask, tag, cv);
-  if (!waits_ok(a, ok, &S.votes)) return false;
+  wave_waits_ok(a, ok);  // no vote (no barrier): see wave_waits_ok
 #pragma unroll
   for (int j = 0; j < kC; j++) {
     if (lane + 64 * j >= q4) continue;
