@@ -86,7 +86,7 @@ __device__ __forceinline__ LayerP layer_p(const Gpt2Args &a, int l) {
 struct Lds {
   alignas(16) _Float16 xs[4096 + 8];  // the MFMA A operand row (fp16)
   alignas(16) float red[3][64][4];    // waves 1..3's accumulators
-  float part[2][4];                   // per-wave partial sums (LayerNorm's two)
+  float part[2][4];                   // per-wave LayerNorm statistics (means, squared deviations)
   Votes votes;
   // attention
   alignas(16) float q[kHd];
@@ -148,17 +148,6 @@ __device__ __forceinline__ f32x4 reduce_waves(f32x4 acc, Lds &S) {
     acc = (acc + r1) + (r2 + r3);
   }
   return acc;
-}
-
-// Sum of one value per thread over the workgroup (every thread gets it),
-// through partial-sum slot k (a slot is written again only after the
-// workgroup's next barrier).
-__device__ __forceinline__ float block_sum(float v, int k, Lds &S) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  v = wave_sum_rows(v);
-  if (lane == 0) S.part[k][wave] = v;
-  lds_barrier();
-  return (S.part[k][0] + S.part[k][1]) + (S.part[k][2] + S.part[k][3]);
 }
 
 // The 4-value chunks of a K-value row a thread stages: wave w holds those of
@@ -238,8 +227,14 @@ __device__ __forceinline__ bool stage_ln(const Gpt2Args &a, const uint64_t *xc, 
 #pragma unroll
     for (int i = 0; i < kP; i++) v[i] = f32x2{cell_f32(cv[2 * i]), cell_f32(cv[2 * i + 1])};
   }
-  // the waits' vote shares the barrier of the first sum
+  // Statistics in one exchange between the waves: each wave's mean and sum
+  // of squared deviations over its K / 4 values, merged as
+  //   mean = sum_w mean_w / 4,  M2 = sum_w M2_w + (K / 4) sum_w (mean_w - mean)^2
+  // (exact in real arithmetic, as stable as two passes over the row); the
+  // waits' vote shares that barrier.
   const int vpar = vote_cast(!ok, &S.votes);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float nw = (float)(K >> 2);
   float sm = 0.0f;
 #pragma unroll
   for (int i = 0; i < kP; i += 2) {
@@ -247,17 +242,28 @@ __device__ __forceinline__ bool stage_ln(const Gpt2Args &a, const uint64_t *xc, 
     const float s1 = stage_pair_ok(K, i + 1) ? v[i + 1][0] + v[i + 1][1] : 0.0f;
     sm += s0 + s1;
   }
-  const float mean = block_sum(sm, 0, S) / (float)K;
-  if (!waits_done(a, vote_seen(vpar, &S.votes))) return false;
+  const float mw = wave_sum_rows(sm) / nw;
   float ss = 0.0f;
 #pragma unroll
   for (int i = 0; i < kP; i += 2) {
-    const f32x2 d0 = v[i] - mean, d1 = v[i + 1] - mean;
+    const f32x2 d0 = v[i] - mw, d1 = v[i + 1] - mw;
     const float s0 = stage_pair_ok(K, i) ? d0[0] * d0[0] + d0[1] * d0[1] : 0.0f;
     const float s1 = stage_pair_ok(K, i + 1) ? d1[0] * d1[0] + d1[1] * d1[1] : 0.0f;
     ss += s0 + s1;
   }
-  const float inv = 1.0f / sqrtf(block_sum(ss, 1, S) / (float)K + a.eps);
+  ss = wave_sum_rows(ss);
+  if (lane == 0) {
+    S.part[0][wave] = mw;
+    S.part[1][wave] = ss;
+  }
+  lds_barrier();
+  if (!waits_done(a, vote_seen(vpar, &S.votes))) return false;
+  const float mean = ((S.part[0][0] + S.part[0][1]) + (S.part[0][2] + S.part[0][3])) * 0.25f;
+  const float e0 = S.part[0][0] - mean, e1 = S.part[0][1] - mean, e2 = S.part[0][2] - mean,
+              e3 = S.part[0][3] - mean;
+  const float m2 = ((S.part[1][0] + S.part[1][1]) + (S.part[1][2] + S.part[1][3])) +
+                   nw * ((e0 * e0 + e1 * e1) + (e2 * e2 + e3 * e3));
+  const float inv = 1.0f / sqrtf(m2 / (float)K + a.eps);
 #pragma unroll
   for (int i = 0; i < kP; i++) {
     const int c = stage_pair(K, i);
