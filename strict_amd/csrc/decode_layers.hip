@@ -640,12 +640,12 @@ __device__ __forceinline__ bool stage_f16(const LayersArgs &a, const uint64_t *c
                                         min(stage_chunk(K, j), c4 - 1) * 2 + e;
                                },
                                mask, tag, cv);
-    if constexpr (kRowsMax == 1 && kLocal) {
-      // batch 1: no vote, so no barrier. Each wave stages and then reads
-      // only its own quarter of xs, and the item's next barrier (the
-      // cross-wave sum) follows its MFMAs; a wave whose wait failed marks
-      // the error and goes on with what it loaded, so every wave reaches
-      // that barrier, and the host reports the step as failed.
+    if constexpr (kLocal) {
+      // No vote, so no barrier: each wave stages and then reads only its
+      // own quarter of xs (every pass's rows), and the item's next barrier
+      // (the cross-wave sum) follows its MFMAs. A wave whose wait failed
+      // marks the error and goes on with what it loaded, so every wave
+      // reaches that barrier, and the host reports the step as failed.
       wave_waits_ok(a, ok, misc);
     } else if (!waits_ok(a, ok, misc)) {
       return false;
