@@ -1154,7 +1154,12 @@ __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, 
         ok = spin_pairs(a, a.qkvc, [&](int k) { return cell + k; }, 3ull, tag, cv);
       else
         ok = spin_cells(a, a.qkvc, [&](int k) { return cell + k; }, 3ull, tag, cv);
-      if (!waits_ok(a, ok, misc)) return false;
+      // batch 1: no vote (see wave_waits_ok); every wave reaches the
+      // barrier after the q / k / v stores below
+      if constexpr (kRope)
+        wave_waits_ok(a, ok, misc);
+      else if (!waits_ok(a, ok, misc))
+        return false;
       SH_MARK(misc, l, 8);
       v0 = cell_f32(cv[0]);
       v1 = cell_f32(cv[1]);
@@ -1395,7 +1400,7 @@ __device__ __forceinline__ bool merge_item(const LayersArgs &a, int l, int item,
                                       ((k & 2) ? kD + (k & 1) : col + (k & 1));
                              },
                              mask, tag, cv);
-  if (!waits_ok(a, ok, misc)) return false;
+  wave_waits_ok(a, ok, misc);  // no vote: every wave reaches the barrier below
   SH_MARK(misc, l, 14);
   float mg = -INFINITY;
 #pragma unroll
