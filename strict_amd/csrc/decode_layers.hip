@@ -240,6 +240,7 @@ struct Misc {
   int vote[2][4];                  // per-wave votes of block_any (two alternating sets)
   int par[4];                      // each wave's current vote set
   float part_hi[4][kMaxRowsPerPass - kSmallBatchRows];  // rows 4.. of a pass
+  float inv[kMaxBatch];  // post-scaled staging, batched variants: each row's RMSNorm scale
 #ifdef SH_DECODE_TRACE
   unsigned long long t_wait;                          // when the last wait ended
   unsigned long long tr[2][kTraceLayers][kTraceSlots];  // this workgroup's timeline
@@ -499,14 +500,18 @@ __device__ __forceinline__ f32x2 embq2(const EmbQ &e, int k, int K) {
 }
 
 // Rows [B][K] of fp32 x -> RMSNorm with gains g -> xs (fp16, row stride
-// K + 8), kRows rows per pass. The rows come from cells xc tagged `tag` or,
+// K + 8), kRows rows per pass. kPost: xs holds x * g only, and the items
+// apply each row's scale 1 / rms to their GEMV results (row_inv); at batch
+// 1 the staging then needs no barrier (each wave reads only its own K
+// quarter of xs, and the sums of squares are read after the item's
+// cross-wave reduction). The rows come from cells xc tagged `tag` or,
 // for the first layer, from the plain buffer xp the embedding kernel wrote
 // before this launch or (batch 1, e.tok >= 0) from the embedding table. Each
 // thread keeps its 2-value pairs (stage_pair, 2 kChunks of them) in
 // registers; the per-row sums of squares are combined across the four waves
 // through LDS. kChunks >= K / 1024. kLocal: the caller's waves read only
 // their own K quarter of xs, so no barrier follows the stores.
-template <int kChunks, int kRowsMax, bool kLocal>
+template <int kChunks, int kRowsMax, bool kLocal, bool kPost = false>
 __device__ __forceinline__ bool stage_rms(const LayersArgs &a, const uint64_t *xc, const float *xp, unsigned tag,
                           const SH_GLOBAL float *g, int K, _Float16 *xs, Misc *misc,
                           const EmbQ &e = EmbQ{}) {
@@ -562,8 +567,12 @@ __device__ __forceinline__ bool stage_rms(const LayersArgs &a, const uint64_t *x
     // at batch 1 the waits' vote shares the barrier of the sums of squares
     // (the batched variants vote first: their kernels measured ~1 % slower
     // with the shared barrier)
+    // (post-scaled at batch 1: no vote and no barrier, see wave_waits_ok)
+    constexpr bool kFree = kPost && kRowsMax == 1;
     int vpar = 0;
-    if constexpr (kRowsMax == 1) {
+    if constexpr (kFree) {
+      wave_waits_ok(a, ok, misc);
+    } else if constexpr (kRowsMax == 1) {
       vpar = vote_cast(!ok, misc);
     } else {
       if (!waits_ok(a, ok, misc)) return false;
@@ -584,23 +593,29 @@ __device__ __forceinline__ bool stage_rms(const LayersArgs &a, const uint64_t *x
         else misc->part_hi[wave][r - kSmallBatchRows] = ss;
       }
     }
-    lds_barrier();
-    if constexpr (kRowsMax == 1) {
-      if (!waits_done(a, vote_seen(vpar, misc), misc)) return false;
+    if constexpr (!kFree) {
+      lds_barrier();
+      if constexpr (kRowsMax == 1) {
+        if (!waits_done(a, vote_seen(vpar, misc), misc)) return false;
+      }
     }
 #pragma unroll
     for (int r = 0; r < kRows; r++) {
       const int b = b0 + r;
       if (b >= B) break;
-      const float(&pr)[4][kSmallBatchRows] = *reinterpret_cast<const float(*)[4][kSmallBatchRows]>(
-          r < kSmallBatchRows ? &misc->part[0][r] : &misc->part_hi[0][r - kSmallBatchRows]);
-      const float ss = (pr[0][0] + pr[1][0]) + (pr[2][0] + pr[3][0]);
-      const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
+      float inv = 1.0f;
+      if constexpr (!kFree) {
+        const float(&pr)[4][kSmallBatchRows] = *reinterpret_cast<const float(*)[4][kSmallBatchRows]>(
+            r < kSmallBatchRows ? &misc->part[0][r] : &misc->part_hi[0][r - kSmallBatchRows]);
+        const float ss = (pr[0][0] + pr[1][0]) + (pr[2][0] + pr[3][0]);
+        inv = 1.0f / sqrtf(ss / (float)K + a.eps);
+        if (kPost && threadIdx.x == 0) misc->inv[b] = inv;
+      }
 #pragma unroll
       for (int i = 0; i < kP; i++) {
         const int c = stage_pair(K, i);
         if (stage_pair_ok(K, i)) {
-          const f32x2 y = v[r][i] * inv * gv[i];
+          const f32x2 y = kPost ? v[r][i] * gv[i] : v[r][i] * inv * gv[i];
           *reinterpret_cast<f16x2 *>(xs + b * (K + 8) + c * 2) = f16x2{(_Float16)y[0], (_Float16)y[1]};
         }
       }
@@ -731,6 +746,20 @@ __device__ __forceinline__ void consume_cells(const uint64_t (&c)[4]) {
 // A: qkv[b][16 i + c] = scale * (W_qkv RMSNorm(x)); w holds the item's
 // weights (load_weights, issued by the caller); local: every consumer of the
 // cells runs on this XCD (cst1)
+// The RMSNorm scale of row b of a post-scaled staging (stage_rms kPost),
+// for the items' results: at batch 1 from the four waves' sums of squares
+// (read after the item's cross-wave reduction), in the batched variants as
+// the staging stored it. The same expression as stage_rms's own.
+template <int kRows>
+__device__ __forceinline__ float row_inv(const LayersArgs &a, const Misc *misc, int b) {
+  if constexpr (kRows == 1) {
+    const float ss = (misc->part[0][0] + misc->part[1][0]) + (misc->part[2][0] + misc->part[3][0]);
+    return 1.0f / sqrtf(ss / (float)a.H + a.eps);
+  } else {
+    return misc->inv[b];
+  }
+}
+
 template <int kL, int kRows>
 __device__ __forceinline__ bool qkv_item(const LayersArgs &a, const LayerG &P, int l, int i, unsigned ep,
                          const Lds &s, const u32x4 (&w)[kL][1], bool reuse, bool local,
@@ -743,7 +772,7 @@ __device__ __forceinline__ bool qkv_item(const LayersArgs &a, const LayerG &P, i
   // this item's reduction writes behind the previous one's reads
   if (reuse)
     lds_barrier();
-  else if (!stage_rms<(kL + 3) / 4, kRows, true>(a, a.x0c, l == 0 ? a.x_in : nullptr, tag_of(ep, l - 1),
+  else if (!stage_rms<(kL + 3) / 4, kRows, true, true>(a, a.x0c, l == 0 ? a.x_in : nullptr, tag_of(ep, l - 1),
                                                  P.norm1, a.H, s.xs, s.misc, l == 0 ? e : EmbQ{}))
     return false;
   SH_MARK(s.misc, l, 0);
@@ -757,7 +786,9 @@ __device__ __forceinline__ bool qkv_item(const LayersArgs &a, const LayerG &P, i
 #pragma unroll
     for (int r = 0; r < kOutRows<kRows>; r++) {
       const int b = 4 * (lane >> 4) + r;
-      if (b < a.B) cst1(a.qkvc, (size_t)b * a.qkv_n + i * 16 + col, bits_of(acc[0][r] * sc), tag, local);
+      if (b < a.B)
+        cst1(a.qkvc, (size_t)b * a.qkv_n + i * 16 + col, bits_of(acc[0][r] * row_inv<kRows>(a, s.misc, b) * sc),
+             tag, local);
     }
   }
   SH_MARK(s.misc, l, 3);
@@ -805,7 +836,7 @@ __device__ __forceinline__ bool up_item(const LayersArgs &a, const LayerG &P, in
   const int ng = 2 * p * 16 + col;  // tiled rows of the gate and up tiles of pair p
   const float sg = P.sup[ng], su = P.sup[ng + 16];
   __builtin_amdgcn_sched_barrier(0);
-  if (!stage_rms<(kL + 3) / 4, kRows, true>(a, a.x1c, nullptr, tag_of(ep, l), P.norm2, a.H, s.xs, s.misc))
+  if (!stage_rms<(kL + 3) / 4, kRows, true, true>(a, a.x1c, nullptr, tag_of(ep, l), P.norm2, a.H, s.xs, s.misc))
     return false;
   f32x4 acc[2];
   mfma_weights<kL, 2>(w, s.xs, a.H + 8, kRows == 1 ? 1 : a.B, acc);
@@ -815,7 +846,8 @@ __device__ __forceinline__ bool up_item(const LayersArgs &a, const LayerG &P, in
 #pragma unroll
     for (int r = 0; r < kOutRows<kRows>; r++) {
       const int b = 4 * (lane >> 4) + r;
-      const uint32_t h = f32_to_f16_bits(silu(acc[0][r] * sg) * (acc[1][r] * su));
+      const float inv = row_inv<kRows>(a, s.misc, b);
+      const uint32_t h = f32_to_f16_bits(silu(acc[0][r] * inv * sg) * (acc[1][r] * inv * su));
       const uint32_t nb = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)h, 0xB1, 0xf, 0xf, false);
       if (b < a.B && (col & 1) == 0)
         cst1(a.actc, (size_t)b * (a.inter / 2) + (p * 16 + col) / 2, h | (nb << 16), tag);
