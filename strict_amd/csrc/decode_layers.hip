@@ -67,6 +67,9 @@ constexpr int kMaxSplits = 64;  // splits per (row, KV head) a merge item combin
 // batch rows staged together (each pass is one round of cell polls): 1 at
 // batch 1, 4 up to batch 4, 8 above
 constexpr int kMaxRowsPerPass = 8;
+// Wall-clock ticks (100 MHz) the batch-1 gate/up-only workgroups wait before
+// requesting the next layer's K / V and QKV weights (see the layer loop).
+constexpr unsigned long long kPrefetchDelay = 35;
 constexpr int kSmallBatchRows = 4;
 
 // Pointers the kernel reads from its argument table (LayerPtrs) are generic;
@@ -1968,6 +1971,17 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
       return;
     SH_MARK(misc, l, 20);
     if (!hasC && next) {
+      if constexpr (kOne) {
+        // batch 1: these 192 workgroups hold their requests back for ~0.35 us
+        // (wall clock, 100 MHz): issued at once, 15 MiB of them met the O /
+        // down workgroups' K / V in flight and the down items' polls behind
+        // it. Measured, one box each: delays of 0.25 / 0.35 / 0.5 / 0.7 us
+        // 0.4077 -> 0.4020 / 0.4024 / 0.4029 / 0.4037 ms per step; 0.1 and
+        // 0.15 us and 1 us neutral or slower, 1.5 us 0.4114 -> 0.4265;
+        // waiting for the item's cell stores instead, neutral.
+        const unsigned long long t0 = wall_clock64();
+        while (wall_clock64() - t0 < kPrefetchDelay) __builtin_amdgcn_s_sleep(1);
+      }
       if (kPre && bA < eA) attn_prefetch(a, layer_g(a, l + 1), item_of(bA), kv);
       if (hasQ) load_weights<kLA, 1>(wa, layer_g(a, l + 1).wqkv, H, bQ);
     }
