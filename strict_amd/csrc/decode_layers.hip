@@ -1973,12 +1973,12 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
     if (!hasC && next) {
       if constexpr (kOne) {
         // batch 1: these 192 workgroups hold their requests back for ~0.35 us
-        // (wall clock, 100 MHz): issued at once, 15 MiB of them met the O /
-        // down workgroups' K / V in flight and the down items' polls behind
-        // it. Measured, one box each: delays of 0.25 / 0.35 / 0.5 / 0.7 us
-        // 0.4077 -> 0.4020 / 0.4024 / 0.4029 / 0.4037 ms per step; 0.1 and
-        // 0.15 us and 1 us neutral or slower, 1.5 us 0.4114 -> 0.4265;
-        // waiting for the item's cell stores instead, neutral.
+        // (wall clock, 100 MHz): issued right after the item, the burst (15
+        // MiB) coincided with the O / down workgroups' K / V and the down
+        // items' polls. Measured, one box each: delays of 0.25 / 0.35 / 0.5
+        // / 0.7 us 0.4077 -> 0.4020 / 0.4024 / 0.4029 / 0.4037 ms per step;
+        // 0.1 and 0.15 us and 1 us neutral or slower, 1.5 us 0.4114 ->
+        // 0.4265; waiting for the item's cell stores instead, neutral.
         const unsigned long long t0 = wall_clock64();
         while (wall_clock64() - t0 < kPrefetchDelay) __builtin_amdgcn_s_sleep(1);
       }

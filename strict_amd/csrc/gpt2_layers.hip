@@ -64,6 +64,9 @@ constexpr int kT = 256;     // threads per workgroup (4 waves)
 constexpr int kHd = 64;     // head dim
 constexpr int kMaxChunk = 256;  // positions per split (one per thread)
 constexpr int kVJ = kMaxChunk / 32;  // V rows per thread
+// Wall-clock ticks (100 MHz) the fc workgroups wait before requesting the
+// next layer's K / V and QKV weights (see the layer loop).
+constexpr unsigned long long kPrefetchDelay = 125;
 
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
@@ -788,6 +791,13 @@ __global__ __launch_bounds__(kT, 1) void gpt2_layers_kernel(const Gpt2Args a) {
     if (hasD) {
       if (!fc_item<kLH>(a, P, l, w - nC, ep, S)) return;
       if (next) {
+        // the fc workgroups hold their requests back ~1.25 us (wall clock,
+        // 100 MHz): issued right after the item, the burst coincided with
+        // the proj items' polls for the fc results. Measured, one box:
+        // delays of 0.25 / 0.5 / 1 / 1.5 / 2 / 3 us: 0.1548 -> 0.1526 /
+        // 0.1526 / 0.1515 / 0.1511 / 0.1530 / 0.1597 ms per step.
+        const unsigned long long t0 = wall_clock64();
+        while (wall_clock64() - t0 < kPrefetchDelay) __builtin_amdgcn_s_sleep(1);
         if (bi >= 0) attn_prefetch(a, layer_p(a, l + 1), bi, L, kv);
         if (qa >= 0) load_weights<kLH>(wa, layer_p(a, l + 1).wqkv, a.H, qa);
       }
