@@ -1125,10 +1125,17 @@ __device__ __forceinline__ void append_new(const LayersArgs &a, SH_GLOBAL uint16
 // kRope: this step's RoPE factors of the lane's two frequencies arrive in
 // rcs / rsn (batch 1 with the embedding inside the kernel) instead of from
 // the embed kernel's table.
-template <int kG, bool kRope = false>
+struct NoRequest {
+  __device__ void operator()() const {}
+};
+
+// after_poll: requests issued once the item's q / k / v cells have arrived
+// (batch 1: the down weights of a workgroup with a down item)
+template <int kG, bool kRope = false, class AfterPoll = NoRequest>
 __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, int l, int item, unsigned ep,
                           uint8_t *smem, Misc *misc, AttnKV &kv, bool runs, bool reuse, bool staged,
-                          int next, bool local, f32x2 rcs = f32x2{}, f32x2 rsn = f32x2{}) {
+                          int next, bool local, f32x2 rcs = f32x2{}, f32x2 rsn = f32x2{},
+                          AfterPoll &&after_poll = AfterPoll{}) {
   static_assert((kG + 2) * kD / 2 <= kT, "one pair of q / k / v cells per thread");
   static_assert(kG <= 4, "MFMA rows 0..3 of lanes 0..15 hold the heads");
   AttnLds<kG> &S = *reinterpret_cast<AttnLds<kG> *>(smem);
@@ -1148,6 +1155,7 @@ __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, 
   const int L = cnst(a.pos)[b] + 1;  // context including the new token
   const int active = (L + chunk - 1) / chunk;
   if (s >= active || cap <= 0 || L > a.max_pos) {  // uniform
+    after_poll();
     // the next item's block is staged all the same; with none, a block
     // staged for this one lands before the phase ends
     if (next >= 0)
@@ -1195,6 +1203,7 @@ __device__ __forceinline__ bool attn_item(const LayersArgs &a, const LayerG &P, 
         wave_waits_ok(a, ok, misc);
       else if (!waits_ok(a, ok, misc))
         return false;
+      after_poll();
       SH_MARK(misc, l, 8);
       v0 = cell_f32(cv[0]);
       v1 = cell_f32(cv[1]);
@@ -1863,6 +1872,7 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
   for (int l = 0; l < a.n_layers; l++) {
     const LayerG P = layer_g(a, l);
     const bool next = l + 1 < a.n_layers;
+    u32x4 wd[kLE][1];  // this workgroup's down item's weights
     auto qkv_one = [&](int i) {
       if (i != bQ) load_weights<kLA, 1>(wa, P.wqkv, H, i);
       if (i == bQ) SH_TRACE(misc, l, 0);
@@ -1899,7 +1909,10 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
         const bool reuse = !kOne && k != bA && i % a.splits != 0;
         const int nx = kStg && k + 1 < eA ? (kOne || kAct ? item_at(nxt) : k + 1) : -1;
         const bool staged = kStg && (k != bA || !kPre);
-        if (!attn_item<kG, kOne>(a, P, l, i, ep, smem, misc, kv, kStg, reuse, staged, nx, xl, rcs, rsn))
+        if (!attn_item<kG, kOne>(a, P, l, i, ep, smem, misc, kv, kStg, reuse, staged, nx, xl, rcs, rsn,
+                                 [&] {
+                                   if (kOne && w < nE) load_weights<kLE, 1>(wd, P.wdown, a.inter, w);
+                                 }))
           return false;
         if (k == bA) { SH_TRACE(misc, l, 3); SH_TRACE_WAIT(l, 1, misc); }
         if (k - bA < 8) SH_TRACE(misc, l, 16 + (k - bA));  // the run's first eight items' ends
@@ -1938,8 +1951,9 @@ __global__ __launch_bounds__(kT, 1) void decode_layers_kernel(const LayersArgs a
     // it, so the windows before the O item's and the down item's polls
     // carry 80 and 64 KiB of requests (with the down weights after the O
     // item: 32 and 112 KiB, and the down items' polls came last).
-    u32x4 wd[kLE][1];
-    if (w < nE) load_weights<kLE, 1>(wd, P.wdown, a.inter, w);
+    // (batch 1: requested inside the workgroup's attention item, once its q
+    // / k / v cells have arrived, or here if it has none)
+    if ((!kOne || !(bA < eA)) && w < nE) load_weights<kLE, 1>(wd, P.wdown, a.inter, w);
     if (!for_items<kOne>(w, nC, G, [&](int i) {
           if (i == w) SH_TRACE(misc, l, 4);
           if (!o_item<kLC, kRows>(a, P, l, i, ep, lds, emb)) return false;
