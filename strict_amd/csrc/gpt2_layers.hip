@@ -501,48 +501,53 @@ __device__ __forceinline__ bool attn_item(const Gpt2Args &a, const LayerP &P, in
 }
 
 // The attention output of every head (the splits merged, fp16) -> xs: a
-// thread computes values wave H / 4 + lane + 64 j, j < kC, of the H =
-// heads * 64 (the wave's K quarter of the O item's MFMAs, so no barrier
-// follows), over the first kNS splits (the active ones, ns <= kNS; the polls
-// load only those: every poll of a wait reloads all of its cells).
+// thread computes the dim pairs wave H / 4 + 2 (lane + 64 j), j < kC2, of
+// the H = heads * 64 (the wave's K quarter of the O item's MFMAs, so no
+// barrier follows), over the first kNS splits (the active ones, ns <= kNS;
+// the polls load only those: every poll of a wait reloads all of its
+// cells). A pair's two acc cells and its split's (max, sum) cells are each
+// one 16-byte load (partials start at even cells, 68 apart).
 template <int kC, int kNS>
 __device__ __forceinline__ bool stage_attn_n(const Gpt2Args &a, unsigned tag, int ns, Lds &S) {
-  const int lane = threadIdx.x & 63, q4 = a.H >> 2, base = (threadIdx.x >> 6) * q4;
-  constexpr int kN = kC * kNS * 3;
+  const int lane = threadIdx.x & 63, q2 = a.H >> 3, base = (threadIdx.x >> 6) * (a.H >> 2);
+  constexpr int kC2 = (kC + 1) / 2;
+  constexpr int kN = kC2 * kNS * 4;
   uint64_t cv[kN];
   uint64_t mask = 0;
 #pragma unroll
-  for (int j = 0; j < kC; j++)
+  for (int j = 0; j < kC2; j++)
 #pragma unroll
     for (int s = 0; s < kNS; s++)
-      if (s < ns && lane + 64 * j < q4) mask |= 7ull << ((j * kNS + s) * 3);
-  const bool ok = spin_cells(a, a.partc,
+      if (s < ns && lane + 64 * j < q2) mask |= 15ull << ((j * kNS + s) * 4);
+  const bool ok = spin_pairs(a, a.partc,
                              [&](int k) {
-                               const int j = k / (kNS * 3), s = (k / 3) % kNS, f = k % 3;
-                               const int idx = base + min(lane + 64 * j, q4 - 1), h = idx >> 6, d = idx & 63;
+                               const int j = k / (kNS * 4), s = (k / 4) % kNS, f = k % 4;
+                               const int idx = base + 2 * min(lane + 64 * j, q2 - 1), h = idx >> 6, d = idx & 63;
                                const size_t pp = ((size_t)h * kGpt2Splits + min(s, ns - 1)) * kGpt2PStride;
-                               return pp + (f == 0 ? d : kHd + f - 1);
+                               return pp + (f == 0 ? d : kHd);
                              },
                              mask, tag, cv);
   wave_waits_ok(a, ok);  // no vote (no barrier): see wave_waits_ok
 #pragma unroll
-  for (int j = 0; j < kC; j++) {
-    if (lane + 64 * j >= q4) continue;
-    const int idx = base + lane + 64 * j;
+  for (int j = 0; j < kC2; j++) {
+    if (lane + 64 * j >= q2) continue;
+    const int idx = base + 2 * (lane + 64 * j);
     float M = -INFINITY;
 #pragma unroll
     for (int s = 0; s < kNS; s++)
-      if (s < ns) M = fmaxf(M, cell_f32(cv[(j * kNS + s) * 3 + 1]));
-    float num = 0.0f, den = 0.0f;
+      if (s < ns) M = fmaxf(M, cell_f32(cv[(j * kNS + s) * 4 + 2]));
+    float num0 = 0.0f, num1 = 0.0f, den = 0.0f;
 #pragma unroll
     for (int s = 0; s < kNS; s++)
       if (s < ns) {
-        const int k = (j * kNS + s) * 3;
-        const float f = expf(cell_f32(cv[k + 1]) - M);
-        num += f * cell_f32(cv[k]);
-        den += f * cell_f32(cv[k + 2]);
+        const int k = (j * kNS + s) * 4;
+        const float f = expf(cell_f32(cv[k + 2]) - M);
+        num0 += f * cell_f32(cv[k]);
+        num1 += f * cell_f32(cv[k + 1]);
+        den += f * cell_f32(cv[k + 3]);
       }
-    S.xs[idx] = (_Float16)(num / den);
+    S.xs[idx] = (_Float16)(num0 / den);
+    S.xs[idx + 1] = (_Float16)(num1 / den);
   }
   return true;
 }
