@@ -384,23 +384,27 @@ __device__ __forceinline__ bool attn_item(const Gpt2Args &a, const LayerP &P, in
   const int np = min(a.chunk, L - p0), pos = L - 1;
   const bool holds_new = p0 + np == L;
   const unsigned tag = tag_of(ep, l);
-  {  // q (threads 0..63), the new k (64..127), the new v (128..191)
-    const int part = min(t >> 6, 2), d = lane;
+  {  // q, the new k and the new v as 96 cell pairs (one 16-byte load each):
+     // thread t < 96 holds dims 2 (t % 32), + 1 of part t / 32 (q, k, v)
+    const int pr = min(t, 95), part = pr >> 5, d = 2 * (pr & 31);
     const size_t cell = (size_t)part * a.H + (size_t)h * kHd + d;
-    uint64_t cv[1];
-    const bool ok = spin_cells(a, a.qkvc, [&](int) { return cell; }, t < 192 ? 1ull : 0ull, tag, cv);
+    uint64_t cv[2];
+    const bool ok = spin_pairs(a, a.qkvc, [&](int) { return cell; }, t < 96 ? 3ull : 0ull, tag, cv);
     if (!waits_ok(a, ok, &S.votes)) return false;
     SH_G2WAIT(l, 1);
-    const float v = cell_f32(cv[0]);
-    if (t < 64) {
-      S.q[d] = v * a.scale;
-    } else if (t < 192) {
-      const _Float16 hv = (_Float16)v;
-      if (t < 128) S.knew[d] = hv;
-      else S.vnew[d] = hv;
+    const float v0 = cell_f32(cv[0]), v1 = cell_f32(cv[1]);
+    if (t < 32) {
+      S.q[d] = v0 * a.scale;
+      S.q[d + 1] = v1 * a.scale;
+    } else if (t < 96) {
+      const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
+      _Float16 *dst = t < 64 ? S.knew : S.vnew;
+      dst[d] = h0;
+      dst[d + 1] = h1;
       if (holds_new) {
-        SH_XGLOBAL uint16_t *c = (t < 128 ? P.kcache : P.vcache) + ((size_t)h * a.max_pos + pos) * kHd + d;
-        *c = __builtin_bit_cast(uint16_t, hv);
+        SH_XGLOBAL uint16_t *c = (t < 64 ? P.kcache : P.vcache) + ((size_t)h * a.max_pos + pos) * kHd + d;
+        *reinterpret_cast<SH_XGLOBAL uint32_t *>(c) =
+            (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
       }
     }
   }
