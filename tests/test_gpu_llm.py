@@ -295,6 +295,21 @@ def test_gpt2_small_shape_greedy_256(ctx):
         _greedy_check(m, prompt, 256, "gpt2-small-shape")
 
 
+def test_gpt2_full_width_three_and_four_splits(ctx):
+    # GPT-2 small's widths with max_positions 160: 48-position attention
+    # splits, so a 140-token prompt and 16 steps (contexts 141..156) run the
+    # O items' staging over 3 and then 4 active splits per head at hidden
+    # 768 (two dim pairs per lane), which configs[3] (256-position splits)
+    # reaches only past 512 positions
+    cfg = llm.GPT2_SMALL.with_(max_positions=160)
+    with llm.Model(ctx, cfg) as m:
+        assert m.uses_layers_kernel
+        m.init_random(seed=11, stddev=0.02)
+        _randomize_small_params(m, 3)
+        prompt = np.random.default_rng(5).integers(0, cfg.vocab, 140)
+        _greedy_check(m, prompt, 16, "gpt2-full-width-splits")
+
+
 def test_gpt2_config3_greedy_256(ctx):
     # GPT-2 small, random N(0, 0.02) fp16 weights, batch 1,
     # 128-token prompt of seeded uniform ids, 256 greedy steps with KV cache
